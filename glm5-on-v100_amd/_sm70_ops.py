@@ -1,0 +1,81 @@
+"""Drop-in replacement for the DSA part of vllm/_sm70_ops.py.
+
+Same function names, argument order and semantics as the reference's
+wrappers (reference/_sm70_ops.py:1802-1961); they dispatch to the torch ops
+registered by ops.py, which run the gfx950 HIP kernels.  `_op` raises
+RuntimeError for a missing op exactly like the reference (:23-29).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops as _ops
+
+
+def _op(name: str):
+    ns = _ops.register()
+    space = getattr(torch.ops, ns)
+    if not hasattr(space, name):
+        raise RuntimeError(
+            f"MI355X DSA op {ns}::{name} is not available. "
+            "Build libmi355_dsa.so (gfx950) to enable it.")
+    return getattr(space, name)
+
+
+def sm70_attn_fp8_gemv(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor,
+                       s: torch.Tensor) -> None:
+    """fp8-e4m3 weight-only GEMV y[M,N] = x[M,K] @ W[N,K]^T (M <= 8).
+
+    w: uint8 e4m3 bits [N,K]; s: fp32 [128,128]-block scale_inv
+    [ceil(N/128), ceil(K/128)]."""
+    _op("sm70_attn_fp8_gemv")(y, x, w, s)
+
+
+def sm70_attn_fp8_dequant(out: torch.Tensor, w: torch.Tensor, s: torch.Tensor) -> None:
+    """Dequantize fp8-e4m3 block-scaled weights into an fp16 scratch [N,K]."""
+    _op("sm70_attn_fp8_dequant")(out, w, s)
+
+
+def sm70_sparse_mla_decode(o: torch.Tensor, lse: torch.Tensor, q: torch.Tensor,
+                           kv_cache: torch.Tensor, idx: torch.Tensor,
+                           block_table: torch.Tensor, seq_lens: torch.Tensor,
+                           scale: float) -> None:
+    """Sparse (top-k) MLA attention: writes o [B,H,512] fp16, lse [B,H] fp32."""
+    _op("sm70_sparse_mla_decode")(o, lse, q, kv_cache, idx, block_table, seq_lens, scale)
+
+
+def sm70_indexer_logits(score: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
+                        weights: torch.Tensor, block_table: torch.Tensor,
+                        seq_lens: torch.Tensor, hist: torch.Tensor | None = None) -> None:
+    """DSA indexer logits -> score [B, max_kv] fp32 (pad = -inf).
+
+    hist (optional): pre-zeroed int32 [B, 4096]; the kernel also builds the
+    level-1 top-k histogram for sm70_decode_topk."""
+    _op("sm70_indexer_logits")(score, q, k_cache, weights, block_table, seq_lens, hist)
+
+
+def sm70_indexer_logits_packed(score: torch.Tensor, q_packed: torch.Tensor,
+                               k_cache: torch.Tensor, weights: torch.Tensor,
+                               block_table: torch.Tensor, seq_lens: torch.Tensor) -> None:
+    """Packed-Q indexer logits (prefill path); q_packed is
+    [32, ceil(B/16), 8, 16, 16] fp16 contiguous."""
+    _op("sm70_indexer_logits_packed")(score, q_packed, k_cache, weights, block_table, seq_lens)
+
+
+def sm70_decode_topk(idx: torch.Tensor, score: torch.Tensor, seq_lens: torch.Tensor,
+                     hist: torch.Tensor, k: int) -> None:
+    """Decode top-k select: idx [B, k] <- top-k positions of score
+    (p < seq_lens), ascending, -1 padded.  Graph-capture safe."""
+    _op("sm70_decode_topk")(idx, score, seq_lens, hist, k)
+
+
+def sm70_indexer_k_store(kv_cache: torch.Tensor, k: torch.Tensor,
+                         slot_mapping: torch.Tensor) -> None:
+    """Graph-safe indexer-K scatter into the paged cache (skips slot < 0)."""
+    _op("sm70_indexer_k_store")(kv_cache, k, slot_mapping)
+
+
+def persistent_topk(logits: torch.Tensor, lengths: torch.Tensor, output: torch.Tensor,
+                    workspace: torch.Tensor, k: int, max_seq_len: int) -> None:
+    """Row-wise top-k used by the prefill indexer (vLLM persistent_topk)."""
+    _op("persistent_topk")(logits, lengths, output, workspace, k, max_seq_len)

@@ -1,0 +1,41 @@
+// Host-side helpers shared by the C-ABI entry points: the thread-local error
+// string behind mi355_dsa_last_error() and argument/launch checking.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/mi355_dsa.h"
+
+namespace mi355dsa {
+
+// Records a formatted error message for mi355_dsa_last_error(); returns code.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the thread's error message (every entry point starts with this).
+void clear_error();
+
+// Converts a pending HIP launch error (if any) into MI355_DSA_EHIP.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned_to(const void* p, uintptr_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+}  // namespace mi355dsa
+
+// Argument check that mirrors the reference's TORCH_CHECK: on failure the
+// entry point returns MI355_DSA_EINVAL with the message recorded.
+#define DSA_CHECK(cond, ...)                                            \
+  do {                                                                  \
+    if (!(cond)) return ::mi355dsa::set_error(MI355_DSA_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+#define DSA_LAUNCH_CHECK(what)                                 \
+  do {                                                         \
+    int _rc = ::mi355dsa::check_launch(what);                  \
+    if (_rc != MI355_DSA_OK) return _rc;                       \
+  } while (0)

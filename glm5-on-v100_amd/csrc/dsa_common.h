@@ -1,0 +1,143 @@
+// Device-side building blocks shared by the DSA sparse-attention kernels
+// (gfx950 / CDNA4, wave64).
+//
+// Storage formats (byte layouts fixed by the op contract):
+//   * fp8_ds_mla latent row, 656 B: [0,512) e4m3 NoPE latents (4 tiles of
+//     128), [512,528) 4 fp32 tile scales, [528,656) 64 fp16 RoPE values.
+//     Dequant of dim d < 512 is e4m3(byte[d]) * scale[d / 128].
+//     (reference: csrc/attention/sm70_mla_decode.cu:74-100)
+//   * fp8 indexer-K row, 132 B: [0,128) e4m3, [128,132) fp32 per-row scale.
+//     (reference: csrc/attention/sm70_mla_decode.cu:102-115)
+//   * fp16 latent row: 576 halves; fp16 indexer-K row: 128 halves.
+//
+// MFMA operand layouts used throughout (v_mfma_f32_16x16x32_f16 and
+// v_mfma_f32_16x16x16_f16, one 64-lane wave, g = lane / 16, c = lane % 16):
+//   A (16 x K): lane holds row c, k-slots g*KPL .. g*KPL+KPL-1
+//   B (K x 16): lane holds column c, the same k-slots
+//   D (16 x 16, fp32): lane holds column c, rows 4g .. 4g+3
+// (KPL = 8 for the x32 form, 4 for the x16 form.)  Only D's placement is
+// observable: any permutation of the contraction index that A and B share
+// gives the same product, which the kernels use to pick load-friendly
+// k-slot -> dimension mappings.  mi355_dsa_selfcheck() verifies D's placement
+// on the device.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi355dsa {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// 16-byte vector that only promises 4-byte alignment (132-B indexer rows).
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+constexpr int kDsmlaRowBytes = 656;  // fp8_ds_mla latent row
+constexpr int kIdxkFp8RowBytes = 132;  // fp8 indexer-K row
+constexpr int kLatentDim = 576;        // qk dim (512 NoPE + 64 RoPE)
+constexpr int kValueDim = 512;         // v dim
+constexpr int kIdxHeadDim = 128;       // indexer head dim
+constexpr int kIdxHeads = 32;          // indexer heads
+constexpr int kTopkBins = 4096;        // 12-bit level histogram
+
+__device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x16(f16x4 a, f16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// Monotone unsigned key of an fp32 value: larger float -> larger key, with
+// -0 < +0 and -inf the smallest non-NaN key (0x007FFFFF).
+// (reference: sm70_mla_decode.cu:43-46)
+__device__ __forceinline__ uint32_t mono_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// ---------------------------------------------------------------------------
+// OCP e4m3 (e4m3fn: bias 7, no inf, max 448) codec, exact, integer based.
+// ---------------------------------------------------------------------------
+
+// e4m3 byte -> fp16 bit pattern of value/256.  Exact for every finite byte,
+// including denormals (they land on fp16 denormals): the 4-bit exponent
+// field moves into the low bits of fp16's 5-bit field, i.e. the bias grows
+// by 8.  Two bytes at a time: x01 holds byte0 in bits [0,8) and byte1 in
+// bits [16,24).
+__device__ __forceinline__ uint32_t e4m3x2_to_f16x2_div256(uint32_t x01) {
+  return ((x01 & 0x00800080u) << 8) | ((x01 & 0x007f007fu) << 7);
+}
+
+// Spread bytes (b0,b1) / (b2,b3) of a dword into the two 16-bit lanes.
+__device__ __forceinline__ uint32_t spread_lo(uint32_t w) {
+  return (w & 0xffu) | ((w << 8) & 0xff0000u);
+}
+__device__ __forceinline__ uint32_t spread_hi(uint32_t w) {
+  return ((w >> 16) & 0xffu) | ((w >> 8) & 0xff0000u);
+}
+
+// 4 e4m3 bytes (one dword) -> 4 exact fp32 values divided by 256.
+__device__ __forceinline__ void e4m3x4_to_f32_div256(uint32_t w, float out[4]) {
+  const uint32_t lo = e4m3x2_to_f16x2_div256(spread_lo(w));
+  const uint32_t hi = e4m3x2_to_f16x2_div256(spread_hi(w));
+  const f16x2 a = __builtin_bit_cast(f16x2, lo);
+  const f16x2 b = __builtin_bit_cast(f16x2, hi);
+  out[0] = (float)a[0];
+  out[1] = (float)a[1];
+  out[2] = (float)b[0];
+  out[3] = (float)b[1];
+}
+
+// fp32 -> e4m3 byte, round-to-nearest-even with saturation to +-448
+// (SATFINITE).  NaN maps to 0x7F (sign kept).
+__device__ __forceinline__ uint32_t f32_to_e4m3_satfinite(float x) {
+  const uint32_t bits = __float_as_uint(x);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  const uint32_t mag = bits & 0x7fffffffu;
+  if (mag > 0x7f800000u) return sign | 0x7fu;  // NaN
+  const float a = __uint_as_float(mag);
+  uint32_t code;
+  if (a >= 448.0f) {
+    code = 0x7eu;
+  } else if (a < 0.015625f) {  // below the smallest normal 2^-6
+    // denormal grid step is 2^-9; a*512 is exact; rintf rounds half-even.
+    code = (uint32_t)__builtin_rintf(a * 512.0f);  // 0..8 (8 == 2^-6 normal)
+  } else {
+    // keep 3 mantissa bits with RNE; a carry walks into the exponent.
+    const uint32_t r = mag + 0x7ffffu + ((mag >> 20) & 1u);
+    code = (r >> 20) - (120u << 3);
+    if (code > 0x7eu) code = 0x7eu;
+  }
+  return sign | code;
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level helpers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float shfl_xor_f(float v, int m) {
+  return __shfl_xor(v, m, 64);
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_f(v, m);
+  return v;
+}
+
+__host__ __device__ __forceinline__ int ilog2_pow2(int v) {
+  int s = 0;
+  while ((1 << s) < v) s++;
+  return s;
+}
+
+}  // namespace mi355dsa

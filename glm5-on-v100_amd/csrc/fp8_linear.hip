@@ -1,0 +1,187 @@
+// fp8-e4m3 weight-only projections: block dequant and the small-M GEMV.
+// Semantics follow sm70_attn_fp8_dequant / sm70_attn_fp8_gemv (reference
+// csrc/attention/sm70_attn_fp8.cu:51-215): w is row-major e4m3 [N,K] with
+// fp32 block scales s[ceil(N/128), ceil(K/128)], dequant = e4m3(w) * s.
+//
+// GEMV design for gfx950: the HBM-bound stream of W is fed straight into
+// v_mfma_f32_16x16x32_f16.  Each wave owns NB column blocks of 16 weight
+// rows; x (M <= 8 rows, zero padded to 16) is the A operand, the dequantised
+// weights the B operand.  e4m3 bytes become exact fp16 (value/256) with the
+// bit-level decode, so the fp16 products are exact and accumulate in fp32;
+// the block scale (x256) is applied once per 128-wide k block.  Waves of a
+// workgroup split K and are reduced through LDS.
+#include "capi_internal.h"
+#include "dsa_common.h"
+
+namespace mi355dsa {
+
+// ---------------------------------------------------------------------------
+// dequant: one thread per 16 weights; grid = (N, ceil(K/16/256))
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) fp8_dequant_kernel(
+    const uint8_t* __restrict__ w, const float* __restrict__ s,
+    f16* __restrict__ out, int K, int KB) {
+  const int n = blockIdx.x;
+  const int chunk = blockIdx.y * 256 + threadIdx.x;
+  const int k0 = chunk * 16;
+  if (k0 >= K) return;
+  const int64_t off = (int64_t)n * K + k0;
+  const float sc = s[(int64_t)(n >> 7) * KB + (k0 >> 7)] * 256.0f;
+  const u32x4 raw = *reinterpret_cast<const u32x4*>(w + off);
+  f16x8 o0, o1;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float v[4];
+    e4m3x4_to_f32_div256(raw[i], v);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const f16 h = (f16)(v[j] * sc);
+      if (i < 2)
+        o0[4 * i + j] = h;
+      else
+        o1[4 * (i - 2) + j] = h;
+    }
+  }
+  *reinterpret_cast<f16x8*>(out + off) = o0;
+  *reinterpret_cast<f16x8*>(out + off + 8) = o1;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV.  k-slot mapping inside a 128-wide k block: step s (0..3), lane group
+// g, slot e  ->  k = 32g + 8s + e.  A lane therefore reads 32 contiguous
+// weight bytes and 64 contiguous x bytes per k block.
+// ---------------------------------------------------------------------------
+template <int NB, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64) fp8_gemv_kernel(
+    const f16* __restrict__ x, const uint8_t* __restrict__ w,
+    const float* __restrict__ s, f16* __restrict__ y, int M, int N, int K,
+    int KB) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int n_base = blockIdx.x * (16 * NB);
+
+  f32x4 acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  const bool xrow = c < M;
+  const f16* xr = x + (int64_t)(xrow ? c : 0) * K;
+
+  for (int kb = wave; kb < KB; kb += WAVES) {
+    const int kvalid = K - kb * 128;  // multiple of 16
+    const int kofs = kb * 128 + 32 * g;
+    // A operand: x[c][kofs .. kofs+31]
+    f16x8 a[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const bool ok = xrow && (32 * g + 8 * q) < kvalid;
+      if (ok)
+        a[q] = *reinterpret_cast<const f16x8*>(xr + kofs + 8 * q);
+      else
+        a[q] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int n = n_base + 16 * j + c;
+      u32x4 b0 = {0u, 0u, 0u, 0u}, b1 = {0u, 0u, 0u, 0u};
+      if (n < N) {
+        const uint8_t* wr = w + (int64_t)n * K + kofs;
+        if (32 * g < kvalid) b0 = *reinterpret_cast<const u32x4*>(wr);
+        if (32 * g + 16 < kvalid) b1 = *reinterpret_cast<const u32x4*>(wr + 16);
+      }
+      f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t d0 = (q < 2) ? b0[2 * q] : b1[2 * (q - 2)];
+        const uint32_t d1 = (q < 2) ? b0[2 * q + 1] : b1[2 * (q - 2) + 1];
+        u32x4 h;
+        h[0] = e4m3x2_to_f16x2_div256(spread_lo(d0));
+        h[1] = e4m3x2_to_f16x2_div256(spread_hi(d0));
+        h[2] = e4m3x2_to_f16x2_div256(spread_lo(d1));
+        h[3] = e4m3x2_to_f16x2_div256(spread_hi(d1));
+        t = mfma16x16x32(a[q], __builtin_bit_cast(f16x8, h), t);
+      }
+      // every row of this 16-row column block shares one 128x128 scale block
+      const int nb_row = (n_base + 16 * j) >> 7;
+      const float sc = (n_base + 16 * j < N)
+                           ? s[(int64_t)nb_row * KB + kb] * 256.0f
+                           : 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[j][r] += sc * t[r];
+    }
+  }
+
+  // reduce the WAVES partial sums through LDS
+  __shared__ float red[WAVES][NB][4][64];
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) red[wave][j][r][lane] = acc[j][r];
+  __syncthreads();
+  // D layout: lane (col c, group g), reg r -> x row m = 4g + r, weight row c.
+  for (int e = threadIdx.x; e < NB * 4 * 64; e += WAVES * 64) {
+    const int j = e / 256, r = (e / 64) & 3, l = e & 63;
+    const int m = 4 * (l >> 4) + r;
+    const int n = n_base + 16 * j + (l & 15);
+    if (m >= M || n >= N) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < WAVES; wv++) v += red[wv][j][r][l];
+    y[(int64_t)m * N + n] = (f16)v;
+  }
+}
+
+template <int NB>
+static void launch_gemv(const f16* x, const uint8_t* w, const float* s, f16* y,
+                        int M, int N, int K, int KB, hipStream_t st) {
+  constexpr int WAVES = 8;
+  const int blocks = (N + 16 * NB - 1) / (16 * NB);
+  fp8_gemv_kernel<NB, WAVES><<<blocks, WAVES * 64, 0, st>>>(x, w, s, y, M, N, K,
+                                                           KB);
+}
+
+}  // namespace mi355dsa
+
+using namespace mi355dsa;
+
+extern "C" int mi355_dsa_attn_fp8_gemv(void* y, const void* x, const uint8_t* w,
+                                       const float* s, int M, int N, int K,
+                                       void* stream) {
+  clear_error();
+  DSA_CHECK(M >= 1 && M <= 8, "sm70_attn_fp8_gemv: M must be 1..8, got %d", M);
+  DSA_CHECK(K > 0 && N > 0 && K % 16 == 0 && N % 8 == 0, "bad N/K alignment");
+  DSA_CHECK(y && x && w && s, "null pointer argument");
+  DSA_CHECK(aligned_to(x, 16) && aligned_to(w, 16),
+            "x and w must be 16-byte aligned");
+  const int KB = (K + 127) / 128;
+  hipStream_t st = as_stream(stream);
+  const f16* xp = reinterpret_cast<const f16*>(x);
+  f16* yp = reinterpret_cast<f16*>(y);
+  if (N >= 16384)
+    launch_gemv<4>(xp, w, s, yp, M, N, K, KB, st);
+  else if (N >= 4096)
+    launch_gemv<2>(xp, w, s, yp, M, N, K, KB, st);
+  else
+    launch_gemv<1>(xp, w, s, yp, M, N, K, KB, st);
+  DSA_LAUNCH_CHECK("attn_fp8_gemv");
+  return MI355_DSA_OK;
+}
+
+extern "C" int mi355_dsa_attn_fp8_dequant(void* out, const uint8_t* w,
+                                          const float* s, int N, int K,
+                                          void* stream) {
+  clear_error();
+  DSA_CHECK(K > 0 && N >= 0 && K % 16 == 0, "K must be a multiple of 16");
+  if (N == 0) return MI355_DSA_OK;
+  DSA_CHECK(out && w && s, "null pointer argument");
+  DSA_CHECK(aligned_to(out, 16) && aligned_to(w, 16),
+            "out and w must be 16-byte aligned");
+  const int KB = (K + 127) / 128;
+  const int chunks = K / 16;
+  dim3 grid(N, (chunks + 255) / 256);
+  fp8_dequant_kernel<<<grid, 256, 0, as_stream(stream)>>>(
+      w, s, reinterpret_cast<f16*>(out), K, KB);
+  DSA_LAUNCH_CHECK("attn_fp8_dequant");
+  return MI355_DSA_OK;
+}

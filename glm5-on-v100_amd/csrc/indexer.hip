@@ -1,0 +1,466 @@
+// DSA lightning-indexer logits on gfx950 MFMA.
+//
+//   score[b,p] = sum_{h<32} relu(q[b,h,:] . K[row(b,p),:]) * w[b,h]
+//
+// Two kernels, one per reference entry point:
+//  * indexer_logits_kernel  -- mi355_dsa_indexer_logits (decode and generic
+//    path; reference sm70_indexer_logits, csrc/attention/sm70_mla_decode.cu:
+//    150-329 / host :2626-2764).  HBM-bound scan: a wave scores 16 keys per
+//    MFMA group (S = Q . K^T, M = 16 heads x 2 tiles, N = 16 keys, K = 128),
+//    keys are loaded straight from HBM into B-operand registers (no LDS),
+//    double buffered.  The fused top-k histogram is built in LDS and flushed
+//    once per workgroup (nonzero bins only).
+//  * indexer_logits_packed_kernel -- mi355_dsa_indexer_logits_packed
+//    (prefill; reference sm70_indexer_logits_packed, :542-653 / :2771-2836).
+//    MFMA-bound: a 512-thread workgroup owns 64 queries x 512 keys; each wave
+//    keeps its 64 keys resident in A-operand registers for all 32 heads,
+//    streams the packed Q of one head at a time through LDS (double
+//    buffered) and keeps the relu * w head-sum in registers.
+//
+// fp8 (132-byte) indexer rows: the decode kernel multiplies the exact
+// e4m3 dot by the row scale before the relu (reference :309-313); the packed
+// kernel dequantises keys to fp16 first (reference idxk_fp8_load4 + half
+// store, :567-583).
+#include <float.h>
+
+#include "capi_internal.h"
+#include "dsa_common.h"
+
+namespace mi355dsa {
+
+// ===========================================================================
+// decode / generic kernel
+// ===========================================================================
+constexpr int kIdxWaves = 4;
+constexpr int kIdxPPB = 1024;             // positions per workgroup
+constexpr int kIdxBlocksPerWave = kIdxPPB / 16 / kIdxWaves;  // 16
+constexpr int kIdxGroup = 2;              // 16-key blocks per pipeline stage
+
+// Key-row fragment of one 16-key block for one lane (key c, group g): dims
+// [32g, 32g+32) -- 64 bytes of an fp16 row or 32 bytes of an fp8 row.
+struct KeyFrag {
+  u32x4 v[4];
+  float scale;  // fp8: row scale * 256; fp16: 1
+};
+
+template <bool KFP8>
+__device__ __forceinline__ void load_key_frag(KeyFrag& f, const void* kv,
+                                              int64_t row) {
+  if (row < 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) f.v[i] = (u32x4){0u, 0u, 0u, 0u};
+    f.scale = 0.f;
+    return;
+  }
+  const int g = (threadIdx.x & 63) >> 4;
+  if constexpr (KFP8) {
+    const uint8_t* rp =
+        reinterpret_cast<const uint8_t*>(kv) + row * (int64_t)kIdxkFp8RowBytes;
+    const u32x4_a4* p = reinterpret_cast<const u32x4_a4*>(rp + 32 * g);
+    f.v[0] = p[0];
+    f.v[1] = p[1];
+    f.scale = *reinterpret_cast<const float*>(rp + 128) * 256.0f;
+  } else {
+    const u32x4* p = reinterpret_cast<const u32x4*>(
+        reinterpret_cast<const f16*>(kv) + row * kIdxHeadDim + 32 * g);
+#pragma unroll
+    for (int i = 0; i < 4; i++) f.v[i] = p[i];
+    f.scale = 1.f;
+  }
+}
+
+// B operand for step s (dims 32g + 8s .. +8) from a key fragment.
+template <bool KFP8>
+__device__ __forceinline__ f16x8 key_operand(const KeyFrag& f, int s) {
+  if constexpr (KFP8) {
+    const uint32_t d0 = f.v[s >> 1][2 * (s & 1)];
+    const uint32_t d1 = f.v[s >> 1][2 * (s & 1) + 1];
+    u32x4 h;
+    h[0] = e4m3x2_to_f16x2_div256(spread_lo(d0));
+    h[1] = e4m3x2_to_f16x2_div256(spread_hi(d0));
+    h[2] = e4m3x2_to_f16x2_div256(spread_lo(d1));
+    h[3] = e4m3x2_to_f16x2_div256(spread_hi(d1));
+    return __builtin_bit_cast(f16x8, h);
+  } else {
+    return __builtin_bit_cast(f16x8, f.v[s]);
+  }
+}
+
+template <bool KFP8>
+__global__ void __launch_bounds__(kIdxWaves * 64) indexer_logits_kernel(
+    const f16* __restrict__ Q, const void* __restrict__ Kv,
+    const f16* __restrict__ W, const int32_t* __restrict__ block_table,
+    const int32_t* __restrict__ seq_lens, float* __restrict__ score,
+    uint32_t* __restrict__ hist, int64_t n_kv_rows, int max_blocks,
+    int page_shift, int max_kv) {
+  const int b = blockIdx.y;
+  const int p_lo = blockIdx.x * kIdxPPB;
+  const int p_hi = min(p_lo + kIdxPPB, max_kv);
+  const int seq_len = seq_lens[b];
+  float* srow = score + (int64_t)b * max_kv;
+
+  // tiles wholly past the context only need the -inf padding
+  if (p_lo >= seq_len) {
+    for (int i = p_lo + threadIdx.x; i < p_hi; i += blockDim.x) srow[i] = -INFINITY;
+    return;
+  }
+
+  __shared__ int32_t s_bt[kIdxPPB + 2];
+  __shared__ uint32_t s_hist[kTopkBins];
+  const int page = 1 << page_shift;
+  const int pg0 = p_lo >> page_shift;
+  const int npg = ((p_hi - 1) >> page_shift) - pg0 + 1;
+  const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
+  for (int i = threadIdx.x; i < npg; i += blockDim.x)
+    s_bt[i] = (pg0 + i < max_blocks) ? bt_row[pg0 + i] : -1;
+  if (hist != nullptr)
+    for (int i = threadIdx.x; i < kTopkBins; i += blockDim.x) s_hist[i] = 0u;
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+
+  // A operands: q rows (heads c and 16 + c).  k-slot mapping: step s,
+  // group g, slot e -> dim 32g + 8s + e, so a lane's key data is one
+  // contiguous 64-byte (fp16) / 32-byte (fp8) span of the row.
+  f16x8 qa[2][4];
+  const f16* qb = Q + (int64_t)b * kIdxHeads * kIdxHeadDim;
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+      qa[t][s] = *reinterpret_cast<const f16x8*>(
+          qb + (16 * t + c) * kIdxHeadDim + 32 * g + 8 * s);
+  // head weights of this lane's D rows: heads 4g + r and 16 + 4g + r
+  float wv[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      wv[t][r] = (float)W[(int64_t)b * kIdxHeads + 16 * t + 4 * g + r];
+
+  // Row of the key this lane loads for block `blk` (-1: zero key).
+  auto key_row = [&](int blk) -> int64_t {
+    const int p = p_lo + 16 * blk + c;
+    if (p >= p_hi || p >= seq_len) return -1;
+    const int32_t pb = s_bt[(p >> page_shift) - pg0];
+    const int64_t row = ((int64_t)pb << page_shift) + (p & (page - 1));
+    return (pb < 0 || row >= n_kv_rows) ? -1 : row;
+  };
+
+  KeyFrag cur[kIdxGroup], nxt[kIdxGroup];
+  constexpr int n_groups = kIdxBlocksPerWave / kIdxGroup;
+  // wave w owns blocks w, w+4, w+8, ... ; stage i covers its blocks
+  // [i*kIdxGroup, (i+1)*kIdxGroup) in that order.
+  auto blk_of = [&](int stage, int j) { return (stage * kIdxGroup + j) * kIdxWaves + wave; };
+#pragma unroll
+  for (int j = 0; j < kIdxGroup; j++) load_key_frag<KFP8>(cur[j], Kv, key_row(blk_of(0, j)));
+
+  for (int st = 0; st < n_groups; st++) {
+    if (16 * blk_of(st, 0) + p_lo >= p_hi) break;
+    if (st + 1 < n_groups) {
+#pragma unroll
+      for (int j = 0; j < kIdxGroup; j++)
+        load_key_frag<KFP8>(nxt[j], Kv, key_row(blk_of(st + 1, j)));
+    }
+#pragma unroll
+    for (int j = 0; j < kIdxGroup; j++) {
+      const int p0 = p_lo + 16 * blk_of(st, j);
+      if (p0 < p_hi) {
+        float v = 0.f;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < 4; s++) acc = mfma16x16x32(qa[t][s], key_operand<KFP8>(cur[j], s), acc);
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            float d = acc[r];
+            if constexpr (KFP8) d *= cur[j].scale;
+            v += (d > 0.f ? d : 0.f) * wv[t][r];
+          }
+        }
+        v += shfl_xor_f(v, 16);
+        v += shfl_xor_f(v, 32);
+        const int p = p0 + c;
+        if (g == 0 && p < p_hi) {
+          if (p < seq_len) {
+            srow[p] = v;
+            if (hist != nullptr) atomicAdd(&s_hist[mono_key(v) >> 20], 1u);
+          } else {
+            srow[p] = -INFINITY;
+          }
+        }
+      }
+    }
+    if (st + 1 < n_groups) {
+#pragma unroll
+      for (int j = 0; j < kIdxGroup; j++) cur[j] = nxt[j];
+    }
+  }
+
+  if (hist != nullptr) {
+    __syncthreads();
+    uint32_t* hrow = hist + (int64_t)b * kTopkBins;
+    for (int i = threadIdx.x; i < kTopkBins; i += blockDim.x) {
+      const uint32_t n = s_hist[i];
+      if (n) atomicAdd(&hrow[i], n);
+    }
+  }
+}
+
+// ===========================================================================
+// packed (prefill) kernel
+// ===========================================================================
+constexpr int kPkWaves = 8;
+constexpr int kPkQT = 64;                 // queries per workgroup (4 x 16)
+constexpr int kPkKT = 64 * kPkWaves;      // keys per workgroup (64 per wave)
+
+template <bool KFP8>
+__global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
+    const f16* __restrict__ Qp, const void* __restrict__ Kv,
+    const f16* __restrict__ W, const int32_t* __restrict__ block_table,
+    const int32_t* __restrict__ seq_lens, float* __restrict__ score, int B,
+    int64_t n_kv_rows, int max_blocks, int page_shift, int max_kv) {
+  const int q_base = blockIdx.y * kPkQT;
+  const int p_base = blockIdx.x * kPkKT;
+  const int n_qt = (B + 15) >> 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+
+  __shared__ f16 s_q[2][4 * 8 * 256];   // packed Q of one head, 4 query tiles
+  __shared__ float s_w[kIdxHeads][kPkQT];
+  __shared__ int32_t s_sl[kPkQT];
+  __shared__ int s_maxsl;
+
+  if (threadIdx.x == 0) s_maxsl = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < kPkQT; i += blockDim.x) {
+    const int q = q_base + i;
+    const int sl = (q < B) ? seq_lens[q] : 0;
+    s_sl[i] = sl;
+    atomicMax(&s_maxsl, sl);
+  }
+  for (int i = threadIdx.x; i < kIdxHeads * kPkQT; i += blockDim.x) {
+    const int h = i / kPkQT, qi = i % kPkQT;
+    const int q = q_base + qi;
+    s_w[h][qi] = (q < B) ? (float)W[(int64_t)q * kIdxHeads + h] : 0.f;
+  }
+  __syncthreads();
+
+  const int key0 = p_base + 64 * wave;  // this wave's 64 keys
+  if (p_base >= s_maxsl) {
+    // no query of this tile reaches these keys: -inf padding only
+    for (int e = threadIdx.x; e < kPkQT * kPkKT; e += blockDim.x) {
+      const int qi = e / kPkKT, p = p_base + e % kPkKT;
+      const int q = q_base + qi;
+      if (q < B && p < max_kv) score[(int64_t)q * max_kv + p] = -INFINITY;
+    }
+    return;
+  }
+
+  // A operands: this wave's keys (4 blocks of 16) for the 4 x32 steps.
+  // Keys are gathered with the block-table row of the tile's first query
+  // (all rows of a call share one table, see the C-ABI contract).
+  const int32_t* bt_row = block_table + (int64_t)q_base * max_blocks;
+  f16x8 ka[4][4];
+  const int page = 1 << page_shift;
+#pragma unroll
+  for (int kb = 0; kb < 4; kb++) {
+    const int p = key0 + 16 * kb + c;
+    int64_t row = -1;
+    if (p < max_kv) {
+      const int pg = p >> page_shift;
+      if (pg < max_blocks) {
+        const int32_t pb = bt_row[pg];
+        const int64_t r = ((int64_t)pb << page_shift) + (p & (page - 1));
+        if (pb >= 0 && r < n_kv_rows) row = r;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      // dims 32s + 8g .. +8
+      if (row < 0) {
+        ka[kb][s] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      } else if constexpr (KFP8) {
+        const uint8_t* rp = reinterpret_cast<const uint8_t*>(Kv) +
+                            row * (int64_t)kIdxkFp8RowBytes;
+        const u32x2 raw =
+            *reinterpret_cast<const u32x2*>(rp + 32 * s + 8 * g);  // 4-B aligned
+        const float sc = *reinterpret_cast<const float*>(rp + 128);
+        float v[8];
+        e4m3x4_to_f32_div256(raw[0], v);
+        e4m3x4_to_f32_div256(raw[1], v + 4);
+        f16x8 h;
+#pragma unroll
+        for (int e = 0; e < 8; e++) h[e] = (f16)(v[e] * (sc * 256.0f));
+        ka[kb][s] = h;
+      } else {
+        ka[kb][s] = *reinterpret_cast<const f16x8*>(
+            reinterpret_cast<const f16*>(Kv) + row * kIdxHeadDim + 32 * s + 8 * g);
+      }
+    }
+  }
+
+  // packed Q of head h for this workgroup's 4 query tiles -> LDS buffer
+  const int qt0 = q_base >> 4;
+  auto stage_q = [&](int h, int buf) {
+    // 4 tiles x 2048 halves = 1024 16-byte chunks; 512 threads x 2
+    for (int i = threadIdx.x; i < 1024; i += blockDim.x) {
+      const int tile = i >> 8;  // 256 chunks per tile
+      const int qt = qt0 + tile;
+      f16x8 v = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      if (qt < n_qt)
+        v = *reinterpret_cast<const f16x8*>(
+            Qp + ((int64_t)h * n_qt + qt) * 2048 + (i & 255) * 8);
+      *reinterpret_cast<f16x8*>(&s_q[buf][i * 8]) = v;
+    }
+  };
+
+  f32x4 sacc[4][4];  // [key block][query block], relu*w summed over heads
+#pragma unroll
+  for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+    for (int qb = 0; qb < 4; qb++) sacc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  stage_q(0, 0);
+  __syncthreads();
+  for (int h = 0; h < kIdxHeads; h++) {
+    const int buf = h & 1;
+    if (h + 1 < kIdxHeads) stage_q(h + 1, buf ^ 1);
+#pragma unroll
+    for (int qb = 0; qb < 4; qb++) {
+      // B operand: query column c of tile qb, dims 32s + 8g .. +8, i.e.
+      // packed chunk (kt = 2s + g/2, row c, half 8*(g&1))
+      f32x4 acc[4];
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) acc[kb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const int kt = 2 * s + (g >> 1);
+        const f16x8 bq = *reinterpret_cast<const f16x8*>(
+            &s_q[buf][qb * 2048 + kt * 256 + c * 16 + 8 * (g & 1)]);
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) acc[kb] = mfma16x16x32(ka[kb][s], bq, acc[kb]);
+      }
+      const float wq = s_w[h][16 * qb + c];
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float d = acc[kb][r];
+          sacc[kb][qb][r] += (d > 0.f ? d : 0.f) * wq;
+        }
+    }
+    __syncthreads();
+  }
+
+  // D layout: lane (query col c, key rows 4g+r) -> 4 consecutive keys.
+#pragma unroll
+  for (int qb = 0; qb < 4; qb++) {
+    const int qi = 16 * qb + c;
+    const int q = q_base + qi;
+    if (q >= B) continue;
+    const int sl = s_sl[qi];
+    float* srow = score + (int64_t)q * max_kv;
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++) {
+      const int p0 = key0 + 16 * kb + 4 * g;
+      f32x4 v;
+#pragma unroll
+      for (int r = 0; r < 4; r++) v[r] = (p0 + r < sl) ? sacc[kb][qb][r] : -INFINITY;
+      if (p0 + 3 < max_kv && (max_kv & 3) == 0) {
+        *reinterpret_cast<f32x4*>(srow + p0) = v;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (p0 + r < max_kv) srow[p0 + r] = v[r];
+      }
+    }
+  }
+}
+
+}  // namespace mi355dsa
+
+using namespace mi355dsa;
+
+static int check_indexer_args(int B, int max_kv, const void* k_cache,
+                              int64_t n_kv_rows, int page_size,
+                              const void* weights, const int32_t* block_table,
+                              int max_blocks, const int32_t* seq_lens) {
+  DSA_CHECK(B >= 0 && max_kv >= 0, "B and max_kv must be >= 0");
+  DSA_CHECK(k_cache && weights && block_table && seq_lens, "null pointer argument");
+  DSA_CHECK(page_size > 0 && (page_size & (page_size - 1)) == 0,
+            "indexer cache page size must be a power of two");
+  DSA_CHECK(n_kv_rows >= 0 && max_blocks >= 0, "bad cache / block-table size");
+  return MI355_DSA_OK;
+}
+
+extern "C" int mi355_dsa_indexer_logits(
+    float* score, int B, int max_kv, const void* q, int n_ihead, int head_dim,
+    const void* k_cache, int k_fp8, int64_t n_kv_rows, int page_size,
+    const void* weights, const int32_t* block_table, int max_blocks,
+    const int32_t* seq_lens, int32_t* hist, void* stream) {
+  clear_error();
+  DSA_CHECK(head_dim == 128, "indexer head_dim must be 128");
+  DSA_CHECK(n_ihead == 32, "kernel specialized for 32 indexer heads");
+  int rc = check_indexer_args(B, max_kv, k_cache, n_kv_rows, page_size, weights,
+                              block_table, max_blocks, seq_lens);
+  if (rc) return rc;
+  if (B == 0 || max_kv == 0) return MI355_DSA_OK;
+  DSA_CHECK(score && q, "null pointer argument");
+  DSA_CHECK(aligned_to(q, 16), "q must be 16-byte aligned");
+  DSA_CHECK(k_fp8 ? aligned_to(k_cache, 4) : aligned_to(k_cache, 16),
+            "k_cache is misaligned");
+  DSA_CHECK(B <= 65535, "B too large");
+  const dim3 grid((max_kv + kIdxPPB - 1) / kIdxPPB, B);
+  const int shift = ilog2_pow2(page_size);
+  hipStream_t st = as_stream(stream);
+  uint32_t* h = reinterpret_cast<uint32_t*>(hist);
+  if (k_fp8)
+    indexer_logits_kernel<true><<<grid, kIdxWaves * 64, 0, st>>>(
+        reinterpret_cast<const f16*>(q), k_cache, reinterpret_cast<const f16*>(weights),
+        block_table, seq_lens, score, h, n_kv_rows, max_blocks, shift, max_kv);
+  else
+    indexer_logits_kernel<false><<<grid, kIdxWaves * 64, 0, st>>>(
+        reinterpret_cast<const f16*>(q), k_cache, reinterpret_cast<const f16*>(weights),
+        block_table, seq_lens, score, h, n_kv_rows, max_blocks, shift, max_kv);
+  DSA_LAUNCH_CHECK("indexer_logits");
+  return MI355_DSA_OK;
+}
+
+extern "C" int mi355_dsa_indexer_logits_packed(
+    float* score, int B, int max_kv, const void* q_packed, const void* k_cache,
+    int k_fp8, int64_t n_kv_rows, int page_size, const void* weights,
+    const int32_t* block_table, int max_blocks, const int32_t* seq_lens,
+    void* stream) {
+  clear_error();
+  int rc = check_indexer_args(B, max_kv, k_cache, n_kv_rows, page_size, weights,
+                              block_table, max_blocks, seq_lens);
+  if (rc) return rc;
+  if (B == 0 || max_kv == 0) return MI355_DSA_OK;
+  DSA_CHECK(score && q_packed, "null pointer argument");
+  DSA_CHECK(aligned_to(q_packed, 16), "q_packed must be 16-byte aligned");
+  DSA_CHECK(k_fp8 ? aligned_to(k_cache, 4) : aligned_to(k_cache, 16),
+            "k_cache is misaligned");
+  DSA_CHECK(aligned_to(score, 16), "score must be 16-byte aligned");
+  const int qtiles = (B + kPkQT - 1) / kPkQT;
+  DSA_CHECK(qtiles <= 65535, "B too large");
+  const dim3 grid((max_kv + kPkKT - 1) / kPkKT, qtiles);
+  const int shift = ilog2_pow2(page_size);
+  hipStream_t st = as_stream(stream);
+  if (k_fp8)
+    indexer_logits_packed_kernel<true><<<grid, kPkWaves * 64, 0, st>>>(
+        reinterpret_cast<const f16*>(q_packed), k_cache,
+        reinterpret_cast<const f16*>(weights), block_table, seq_lens, score, B,
+        n_kv_rows, max_blocks, shift, max_kv);
+  else
+    indexer_logits_packed_kernel<false><<<grid, kPkWaves * 64, 0, st>>>(
+        reinterpret_cast<const f16*>(q_packed), k_cache,
+        reinterpret_cast<const f16*>(weights), block_table, seq_lens, score, B,
+        n_kv_rows, max_blocks, shift, max_kv);
+  DSA_LAUNCH_CHECK("indexer_logits_packed");
+  return MI355_DSA_OK;
+}

@@ -1,0 +1,289 @@
+// Exact per-row top-k selection for the DSA indexer (decode and prefill).
+//
+// Contract (reference sm70_decode_topk, csrc/attention/sm70_mla_decode.cu:
+// 1187-1212, host :2844-2905, made exact): idx[r,:] holds the positions
+// p < min(seq_len[r], width) of the k largest scores under the 32-bit
+// monotone key order; among equal keys the lower position wins; positions
+// are written in ascending order and the tail is padded with -1.  When
+// seq_len <= k every valid position is selected.
+//
+// Design for gfx950: one 1024-thread workgroup per row, no inter-workgroup
+// synchronisation (the reference's co-resident spin grid needs a forward-
+// progress guarantee that a plain launch does not give).  A 3-level radix
+// select (12 + 12 + 8 bits) on LDS histograms finds the exact k-th key tau
+// and how many keys equal to tau are taken; levels stop early once a bin is
+// taken whole.  The decode path starts from the level-1 histogram the
+// indexer kernel already built.  A final pass does an ordered compaction:
+// each thread owns 16 consecutive positions (staged through LDS so the HBM
+// reads stay coalesced) and one packed block scan yields every thread's
+// output offset, so the result is deterministic.
+#include "capi_internal.h"
+#include "dsa_common.h"
+
+namespace mi355dsa {
+
+constexpr int kTkThreads = 1024;
+constexpr int kTkWaves = kTkThreads / 64;
+constexpr int kTkV = 16;                         // positions per thread, final pass
+constexpr int kTkChunk = kTkThreads * kTkV;      // 16384 positions per chunk
+constexpr int kTkChunkPad = kTkChunk + kTkChunk / kTkV;
+
+struct TopkShared {
+  uint32_t hist[kTopkBins];
+  float chunk[kTkChunkPad];
+  uint32_t wsum[kTkWaves + 1];
+  int T;
+  uint32_t above;
+};
+
+// Block-wide exclusive prefix sum over threads; *total gets the full sum.
+__device__ uint32_t block_excl_scan(uint32_t v, uint32_t* wsum, uint32_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t run = 0;
+    for (int w = 0; w < kTkWaves; w++) {
+      const uint32_t t = wsum[w];
+      wsum[w] = run;
+      run += t;
+    }
+    wsum[kTkWaves] = run;
+  }
+  __syncthreads();
+  const uint32_t res = wsum[wave] + x - v;
+  *total = wsum[kTkWaves];
+  __syncthreads();
+  return res;
+}
+
+// Bin T of an nbins histogram with above(T) < need <= above(T) + hist[T],
+// where above(T) counts keys in bins > T.  Requires need <= total.
+__device__ void find_threshold(TopkShared& sh, int nbins, uint32_t need, int* T,
+                               uint32_t* above) {
+  const int per = nbins >= kTkThreads ? nbins / kTkThreads : 1;
+  const int lo = threadIdx.x * per;
+  uint32_t cs = 0;
+  if (lo < nbins)
+    for (int i = 0; i < per; i++) cs += sh.hist[lo + i];
+  uint32_t total;
+  const uint32_t excl = block_excl_scan(cs, sh.wsum, &total);
+  if (threadIdx.x == 0) sh.T = -1;
+  __syncthreads();
+  if (lo < nbins) {
+    uint32_t a = total - excl - cs;  // keys in bins above this thread's chunk
+    for (int bin = lo + per - 1; bin >= lo; bin--) {
+      const uint32_t h = sh.hist[bin];
+      if (a < need && a + h >= need) {
+        sh.T = bin;
+        sh.above = a;
+        break;
+      }
+      a += h;
+    }
+  }
+  __syncthreads();
+  *T = sh.T;
+  *above = sh.above;
+  __syncthreads();
+}
+
+template <bool HAVE_HIST>
+__global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
+    const float* __restrict__ score, int64_t row_stride,
+    const int32_t* __restrict__ seq_lens, const uint32_t* __restrict__ hist_in,
+    int32_t* __restrict__ idx, int K) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  TopkShared& sh = *reinterpret_cast<TopkShared*>(smem_raw);
+  const int r = blockIdx.x;
+  const float* row = score + (int64_t)r * row_stride;
+  int32_t* out = idx + (int64_t)r * K;
+  int L = seq_lens[r];
+  if (L > row_stride) L = (int)row_stride;
+  if (L < 0) L = 0;
+
+  if (L <= K) {
+    for (int p = threadIdx.x; p < K; p += kTkThreads) out[p] = (p < L) ? p : -1;
+    return;
+  }
+
+  // ---- level 1: bits [20,32) ----
+  bool rebuild = !HAVE_HIST;
+  if (HAVE_HIST) {
+    const uint32_t* h = hist_in + (int64_t)r * kTopkBins;
+    uint32_t part = 0;
+    for (int i = threadIdx.x; i < kTopkBins; i += kTkThreads) {
+      sh.hist[i] = h[i];
+      part += h[i];
+    }
+    uint32_t total;
+    block_excl_scan(part, sh.wsum, &total);
+    // a histogram that does not describe this row exactly is rebuilt
+    rebuild = (total != (uint32_t)L);
+  }
+  if (rebuild) {
+    for (int i = threadIdx.x; i < kTopkBins; i += kTkThreads) sh.hist[i] = 0u;
+    __syncthreads();
+    for (int p = threadIdx.x; p < L; p += kTkThreads)
+      atomicAdd(&sh.hist[mono_key(row[p]) >> 20], 1u);
+    __syncthreads();
+  }
+  int T;
+  uint32_t above;
+  find_threshold(sh, kTopkBins, (uint32_t)K, &T, &above);
+  uint32_t need = (uint32_t)K - above;
+  uint32_t prefix = (uint32_t)T;
+  int shift = 20;
+  uint32_t bin_count = sh.hist[T];
+
+  // ---- level 2: bits [8,20) of keys in bin T ----
+  if (bin_count > need) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < kTopkBins; i += kTkThreads) sh.hist[i] = 0u;
+    __syncthreads();
+    for (int p = threadIdx.x; p < L; p += kTkThreads) {
+      const uint32_t key = mono_key(row[p]);
+      if ((key >> 20) == prefix) atomicAdd(&sh.hist[(key >> 8) & 0xfffu], 1u);
+    }
+    __syncthreads();
+    find_threshold(sh, kTopkBins, need, &T, &above);
+    need -= above;
+    prefix = (prefix << 12) | (uint32_t)T;
+    shift = 8;
+    bin_count = sh.hist[T];
+    // ---- level 3: bits [0,8) ----
+    if (bin_count > need) {
+      __syncthreads();
+      for (int i = threadIdx.x; i < 256; i += kTkThreads) sh.hist[i] = 0u;
+      __syncthreads();
+      for (int p = threadIdx.x; p < L; p += kTkThreads) {
+        const uint32_t key = mono_key(row[p]);
+        if ((key >> 8) == prefix) atomicAdd(&sh.hist[key & 0xffu], 1u);
+      }
+      __syncthreads();
+      find_threshold(sh, 256, need, &T, &above);
+      need -= above;
+      prefix = (prefix << 8) | (uint32_t)T;
+      shift = 0;
+    }
+  }
+  // Selection: (key >> shift) > prefix, plus the `need` lowest positions
+  // with (key >> shift) == prefix.
+  const uint32_t n_eq_take = need;
+
+  uint32_t base_gt = 0, base_eq = 0;
+  for (int c0 = 0; c0 < L; c0 += kTkChunk) {
+    __syncthreads();
+    for (int i = 0; i < kTkV; i++) {
+      const int q = i * kTkThreads + threadIdx.x;  // coalesced
+      const int p = c0 + q;
+      sh.chunk[q + q / kTkV] = (p < L) ? row[p] : 0.f;
+    }
+    __syncthreads();
+    const int my0 = threadIdx.x * kTkV;
+    uint32_t gt_mask = 0, eq_mask = 0;
+    for (int i = 0; i < kTkV; i++) {
+      const int q = my0 + i;
+      if (c0 + q < L) {
+        const uint32_t k = mono_key(sh.chunk[q + q / kTkV]) >> shift;
+        if (k > prefix) gt_mask |= 1u << i;
+        else if (k == prefix) eq_mask |= 1u << i;
+      }
+    }
+    const uint32_t packed =
+        (uint32_t)__popc(gt_mask) | ((uint32_t)__popc(eq_mask) << 16);
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan(packed, sh.wsum, &tot);
+    const uint32_t G = base_gt + (ex & 0xffffu);
+    uint32_t E = base_eq + (ex >> 16);
+    uint32_t o = G + (E < n_eq_take ? E : n_eq_take);
+    for (int i = 0; i < kTkV; i++) {
+      const bool gt = (gt_mask >> i) & 1u;
+      const bool eq = (eq_mask >> i) & 1u;
+      if (gt) {
+        out[o++] = c0 + my0 + i;
+      } else if (eq) {
+        if (E < n_eq_take) out[o++] = c0 + my0 + i;
+        E++;
+      }
+    }
+    base_gt += tot & 0xffffu;
+    base_eq += tot >> 16;
+  }
+  // Exactly K positions were written (L > K); nothing to pad.
+}
+
+template <bool HAVE_HIST>
+static int launch_topk(const float* score, int n_rows, int64_t row_stride,
+                       const int32_t* seq_lens, const uint32_t* hist, int32_t* idx,
+                       int K, hipStream_t st) {
+  static bool attr_set = false;
+  const size_t smem = sizeof(TopkShared);
+  if (!attr_set) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(topk_row_kernel<HAVE_HIST>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    attr_set = true;
+  }
+  topk_row_kernel<HAVE_HIST><<<n_rows, kTkThreads, smem, st>>>(score, row_stride, seq_lens,
+                                                              hist, idx, K);
+  return check_launch("topk");
+}
+
+}  // namespace mi355dsa
+
+using namespace mi355dsa;
+
+extern "C" size_t mi355_dsa_decode_topk_workspace_size(int B, int max_kv, int k) {
+  (void)B;
+  (void)max_kv;
+  (void)k;
+  return 0;
+}
+
+extern "C" int mi355_dsa_decode_topk(int32_t* idx, const float* score,
+                                     const int32_t* seq_lens, const int32_t* hist,
+                                     int B, int max_kv, int k, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  clear_error();
+  (void)workspace;
+  (void)workspace_bytes;
+  DSA_CHECK(k >= 1, "k must be >= 1");
+  DSA_CHECK(B >= 0 && max_kv >= 0, "B and max_kv must be >= 0");
+  DSA_CHECK(k <= (1 << 16) - 1, "k too large");
+  if (B == 0) return MI355_DSA_OK;
+  DSA_CHECK(idx && score && seq_lens && hist, "null pointer argument");
+  return launch_topk<true>(score, B, max_kv, seq_lens,
+                           reinterpret_cast<const uint32_t*>(hist), idx, k,
+                           as_stream(stream));
+}
+
+extern "C" size_t mi355_dsa_persistent_topk_workspace_size(int n_rows, int row_stride,
+                                                           int k) {
+  (void)n_rows;
+  (void)row_stride;
+  (void)k;
+  return 0;
+}
+
+extern "C" int mi355_dsa_persistent_topk(const float* score, int n_rows, int row_stride,
+                                         const int32_t* seq_lens, int32_t* idx, int k,
+                                         int max_seq_len, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  clear_error();
+  (void)workspace;
+  (void)workspace_bytes;
+  DSA_CHECK(k >= 1, "k must be >= 1");
+  DSA_CHECK(k <= (1 << 16) - 1, "k too large");
+  DSA_CHECK(n_rows >= 0 && row_stride >= 0, "n_rows and row_stride must be >= 0");
+  DSA_CHECK(max_seq_len >= 0, "max_seq_len must be >= 0");
+  if (n_rows == 0) return MI355_DSA_OK;
+  DSA_CHECK(idx && score && seq_lens, "null pointer argument");
+  return launch_topk<false>(score, n_rows, row_stride, seq_lens, nullptr, idx, k,
+                            as_stream(stream));
+}

@@ -1,0 +1,174 @@
+/*
+ * mi355_dsa.h -- C ABI of the MI355X (gfx950) DSA sparse-attention kernels.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream
+ * (passed as void*; NULL selects the null stream), launches asynchronously on
+ * that stream and returns MI355_DSA_OK or an error code.  On error nothing is
+ * launched and mi355_dsa_last_error() returns the message of the calling
+ * thread's last failure.  No entry point allocates device memory: scratch
+ * comes from a caller-provided workspace whose size the matching
+ * *_workspace_size() function reports.  No entry point synchronises the
+ * stream except mi355_dsa_selfcheck().
+ *
+ * Each function replaces one host launcher of the reference (file:line
+ * citations are relative to the bayley/glm5-on-v100 tree); the argument
+ * meaning, tensor layouts and masking conventions follow it.  The torch op
+ * schemas that wrap these functions are the reference's
+ * (patches/glm5-v100-sm70-glue.patch:494-565).
+ *
+ * Dtype codes: fp16 tensors are IEEE binary16; "fp8" caches are uint8 rows
+ * in the layouts described per function; all index tensors are int32.
+ */
+#ifndef MI355_DSA_H_
+#define MI355_DSA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI355_DSA_OK 0
+#define MI355_DSA_EINVAL 1 /* bad argument (shape / size / alignment) */
+#define MI355_DSA_EHIP 2   /* HIP runtime error at launch */
+#define MI355_DSA_ECHECK 3 /* device self-check mismatch */
+
+/* Message of the calling thread's last error ("" if none). */
+const char* mi355_dsa_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int mi355_dsa_abi_version(void);
+
+/*
+ * Device self-check, synchronous on `stream`: verifies the MFMA accumulator
+ * placement the kernels assume and the e4m3 decode used in the gathers.
+ * Replaces the reference's first-launch WMMA layout probe
+ * (csrc/attention/sm70_mla_decode.cu:511-540, :2807-2818).
+ * Returns MI355_DSA_ECHECK on a mismatch.
+ */
+int mi355_dsa_selfcheck(void* stream);
+
+/*
+ * Indexer-K cache scatter: kv_cache row slot_mapping[t] <- k[t] for every
+ * token t with 0 <= slot < n_rows (other slots are skipped on device).
+ *   kv_fp8 == 0: kv_cache fp16 rows of head_dim halves (plain copy).
+ *   kv_fp8 == 1: kv_cache rows of 132 bytes = 128 e4m3 + fp32 scale, with
+ *                scale = max(amax/448, FLT_MIN), e4m3 = RNE-satfinite(k/scale);
+ *                head_dim must be 128.
+ *   k: fp16 [n_tok, head_dim] contiguous; n_rows = rows in kv_cache.
+ * Replaces sm70_indexer_k_store (csrc/attention/sm70_mla_decode.cu:2910-2939).
+ */
+int mi355_dsa_indexer_k_store(void* kv_cache, int kv_fp8, int64_t n_rows,
+                              const void* k, int64_t n_tok, int head_dim,
+                              const int32_t* slot_mapping, void* stream);
+
+/*
+ * Indexer logits (decode and generic path):
+ *   score[b,p] = sum_h relu(q[b,h,:] . K[row(b,p),:]) * w[b,h]   (p < seq_len[b])
+ *   score[b,p] = -inf                                          (seq_len[b] <= p < max_kv)
+ * with row(b,p) = bt[b, p/page]*page + p%page; a row outside [0,n_kv_rows)
+ * or a page index >= max_blocks reads K = 0.  q fp16 [B,32,128], w fp16
+ * [B,32], bt int32 [B,max_blocks], seq_lens int32 [B], score fp32
+ * [B,max_kv].  k_fp8 selects the 132-byte fp8 rows (see k_store), else fp16
+ * rows of 128 halves.  page_size must be a power of two.  hist (nullable)
+ * is a caller-zeroed int32 [B,4096]; when given, hist[b, mono(score)>>20]
+ * is incremented for every p < seq_len[b] (mono = monotone fp32 key).
+ * Replaces sm70_indexer_logits (csrc/attention/sm70_mla_decode.cu:2626-2764).
+ */
+int mi355_dsa_indexer_logits(float* score, int B, int max_kv, const void* q,
+                             int n_ihead, int head_dim, const void* k_cache,
+                             int k_fp8, int64_t n_kv_rows, int page_size,
+                             const void* weights, const int32_t* block_table,
+                             int max_blocks, const int32_t* seq_lens,
+                             int32_t* hist, void* stream);
+
+/*
+ * Prefill indexer logits from pre-packed Q.  Same math as
+ * mi355_dsa_indexer_logits without hist; q_packed is fp16
+ * [32, ceil(B/16), 8, 16, 16] with q_packed[h][t][kt][r][c] = q[16t+r, h,
+ * 16kt+c] (rows >= B zero).  As in the reference, the key tile of a query
+ * tile is gathered with the block-table row of the tile's first query: all
+ * rows of a call are expected to share one table (the per-segment caller
+ * expands a single request row).
+ * Replaces sm70_indexer_logits_packed (csrc/attention/sm70_mla_decode.cu:2771-2836).
+ */
+int mi355_dsa_indexer_logits_packed(float* score, int B, int max_kv,
+                                    const void* q_packed, const void* k_cache,
+                                    int k_fp8, int64_t n_kv_rows, int page_size,
+                                    const void* weights,
+                                    const int32_t* block_table, int max_blocks,
+                                    const int32_t* seq_lens, void* stream);
+
+/*
+ * Decode top-k: idx[b,:] = the positions p < seq_len[b] of the k largest
+ * score[b,p] (exact 32-bit order; equal scores prefer the lower position),
+ * written in ascending position order and padded with -1.  hist is the
+ * [B,4096] level-1 histogram built by mi355_dsa_indexer_logits.
+ * Replaces sm70_decode_topk (csrc/attention/sm70_mla_decode.cu:2844-2905).
+ */
+size_t mi355_dsa_decode_topk_workspace_size(int B, int max_kv, int k);
+int mi355_dsa_decode_topk(int32_t* idx, const float* score,
+                          const int32_t* seq_lens, const int32_t* hist, int B,
+                          int max_kv, int k, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
+ * Row-wise top-k for prefill: same selection contract as decode_topk, per
+ * row r of score [n_rows, row_stride] with valid length seq_lens[r]
+ * (clamped to row_stride); idx [n_rows, k].  Builds its own histograms.
+ * Replaces vLLM's persistent_topk as called at
+ * reference/sparse_attn_indexer.py:873-880 (max_seq_len is accepted for
+ * signature parity and only bounds-checked).
+ */
+size_t mi355_dsa_persistent_topk_workspace_size(int n_rows, int row_stride,
+                                                int k);
+int mi355_dsa_persistent_topk(const float* score, int n_rows, int row_stride,
+                              const int32_t* seq_lens, int32_t* idx, int k,
+                              int max_seq_len, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/*
+ * Sparse (top-k) MLA attention over the paged latent cache, decode and
+ * prefill.  For each token b and head h:
+ *   s_j  = fp16(q[b,h,:] * fp16(scale)) . K_j      (576 dims)
+ *   o    = sum_j softmax(s)_j V_j                   (V_j = K_j[0:512])
+ *   lse  = max_j s_j + ln sum_j exp(s_j - max)      (-inf when no key valid)
+ * over the selected keys j = idx[b,i] with 0 <= j < seq_len[b] and a
+ * resolved row inside the cache.  q fp16 [B,H,576], o fp16 [B,H,512],
+ * lse fp32 [B,H], idx int32 [B,topk] (logical positions, -1 unused),
+ * bt int32 [B,max_blocks], seq_lens int32 [B].  kv_fp8 == 0: fp16 rows of
+ * 576 halves; kv_fp8 == 1: 656-byte fp8_ds_mla rows.
+ * Replaces sm70_sparse_mla_decode (csrc/attention/sm70_mla_decode.cu:2457-2616).
+ */
+size_t mi355_dsa_sparse_mla_workspace_size(int B, int n_head, int topk);
+int mi355_dsa_sparse_mla_decode(void* o, float* lse, const void* q, int B,
+                                int n_head, const void* kv_cache, int kv_fp8,
+                                int64_t n_kv_rows, int page_size,
+                                const int32_t* idx, int topk,
+                                const int32_t* block_table, int max_blocks,
+                                const int32_t* seq_lens, float scale,
+                                void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/*
+ * fp8-e4m3 weight-only GEMV: y[m,n] = sum_k x[m,k] * e4m3(w[n,k]) * s[n/128,k/128]
+ * x fp16 [M,K], w uint8 [N,K], s fp32 [ceil(N/128), ceil(K/128)], y fp16
+ * [M,N]; 1 <= M <= 8, K % 16 == 0, N % 8 == 0, all contiguous.
+ * Replaces sm70_attn_fp8_gemv (csrc/attention/sm70_attn_fp8.cu:148-191).
+ */
+int mi355_dsa_attn_fp8_gemv(void* y, const void* x, const uint8_t* w,
+                            const float* s, int M, int N, int K, void* stream);
+
+/*
+ * fp8-e4m3 block dequant: out[n,k] = fp16_rn(e4m3(w[n,k]) * s[n/128,k/128]).
+ * Replaces sm70_attn_fp8_dequant (csrc/attention/sm70_attn_fp8.cu:193-215).
+ */
+int mi355_dsa_attn_fp8_dequant(void* out, const uint8_t* w, const float* s,
+                               int N, int K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355_DSA_H_ */

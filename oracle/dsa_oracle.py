@@ -1,0 +1,353 @@
+"""CPU restatement of the DSA hot-path ops -- TEST INFRASTRUCTURE ONLY.
+
+Every function cites the reference file:line it restates (paths relative to
+the bayley/glm5-on-v100 tree).  Inputs/outputs are CPU torch tensors with the
+same layouts as the GPU ops.  Float math runs in fp32 or fp64 as noted;
+integer/byte work is exact.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+FLT_MIN = float(np.finfo(np.float32).tiny)
+DSMLA_ROW_BYTES = 656
+IDXK_FP8_ROW_BYTES = 132
+TOPK_NBIN = 4096
+
+
+# ---------------------------------------------------------------------------
+# e4m3 codec and monotone key
+# ---------------------------------------------------------------------------
+def e4m3_encode(x: torch.Tensor) -> torch.Tensor:
+    """fp32 -> OCP e4m3 bytes with round-to-nearest-even and SATFINITE.
+
+    Restates __nv_cvt_float_to_fp8(v, __NV_SATFINITE, __NV_E4M3)
+    (sm70_mla_decode.cu:704) and the weight quantizer's clamp-then-cast
+    (glue.patch:1529-1530).  torch's own cast is not saturating (it maps
+    values above 464 to NaN), so the value is clamped to +-448 first; NaN
+    stays NaN (0x7f with its sign).
+    """
+    xf = x.to(torch.float32)
+    c = torch.where(torch.isnan(xf), xf, xf.clamp(-448.0, 448.0))
+    return c.to(torch.float8_e4m3fn).view(torch.uint8)
+
+
+def e4m3_decode(b: torch.Tensor) -> torch.Tensor:
+    """e4m3 bytes -> exact fp32 values (sm70_attn_fp8.cu:16-20)."""
+    return b.contiguous().view(torch.float8_e4m3fn).to(torch.float32)
+
+
+def mono_key(x: torch.Tensor) -> torch.Tensor:
+    """Monotone uint32 key of fp32 values as int64 (sm70_mla_decode.cu:43-46)."""
+    u = x.contiguous().to(torch.float32).view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    neg = (u & 0x80000000) != 0
+    return torch.where(neg, (~u) & 0xFFFFFFFF, u | 0x80000000)
+
+
+# ---------------------------------------------------------------------------
+# paged cache helpers
+# ---------------------------------------------------------------------------
+def resolve_rows(pos: torch.Tensor, bt_row: torch.Tensor, page: int,
+                 n_rows: int) -> torch.Tensor:
+    """Logical positions -> physical cache rows, -1 where the page index is
+    beyond the table or the row is outside the cache
+    (sm70_mla_decode.cu:186-193, :227-233, :983-989)."""
+    pos = pos.to(torch.int64)
+    pg = torch.div(pos, page, rounding_mode="floor")
+    ok = (pos >= 0) & (pg < bt_row.numel())
+    blk = torch.where(ok, bt_row.to(torch.int64)[pg.clamp(0, max(bt_row.numel() - 1, 0))],
+                      torch.full_like(pos, -1))
+    row = blk * page + (pos - pg * page)
+    ok = ok & (row >= 0) & (row < n_rows)
+    return torch.where(ok, row, torch.full_like(row, -1))
+
+
+def idxk_rows_fp32(k_cache: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """Gather indexer-K rows as fp32 (rows == -1 -> zeros).  fp16 cache:
+    exact; fp8 132-B cache: e4m3 * per-row scale in fp32
+    (idxk_fp8_load4, sm70_mla_decode.cu:106-115)."""
+    if k_cache.dtype == torch.float16:
+        flat = k_cache.reshape(-1, k_cache.shape[-1]).to(torch.float32)
+        d = flat.shape[1]
+    else:
+        flat_b = k_cache.reshape(-1, IDXK_FP8_ROW_BYTES)
+        vals = e4m3_decode(flat_b[:, :128].contiguous())
+        sc = flat_b[:, 128:132].contiguous().view(torch.float32)
+        flat = vals * sc
+        d = 128
+    out = torch.zeros(rows.numel(), d, dtype=torch.float32)
+    ok = rows >= 0
+    out[ok] = flat[rows[ok]]
+    return out
+
+
+def latent_rows_fp16(kv_cache: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """Gather latent rows as the fp16 values the attention consumes
+    (rows == -1 -> zeros).  fp8_ds_mla rows are dequantized as
+    fp16_rn(e4m3 * tile_scale) for the 512 NoPE dims and copied for the 64
+    fp16 RoPE dims (dsmla_load4, sm70_mla_decode.cu:81-100, then the fp16
+    store into the key tile at :1006-1012)."""
+    if kv_cache.dtype == torch.float16:
+        flat = kv_cache.reshape(-1, kv_cache.shape[-1])
+    else:
+        fb = kv_cache.reshape(-1, DSMLA_ROW_BYTES)
+        vals = e4m3_decode(fb[:, :512].contiguous()).view(-1, 4, 128)
+        sc = fb[:, 512:528].contiguous().view(torch.float32).view(-1, 4, 1)
+        nope = (vals * sc).reshape(-1, 512).to(torch.float16)
+        rope = fb[:, 528:656].contiguous().view(torch.float16)
+        flat = torch.cat([nope, rope], dim=1)
+    out = torch.zeros(rows.numel(), flat.shape[1], dtype=torch.float16)
+    ok = rows >= 0
+    out[ok] = flat[rows[ok]]
+    return out
+
+
+# ---------------------------------------------------------------------------
+# indexer-K store (sm70_mla_decode.cu:654-706, host :2910-2939)
+# ---------------------------------------------------------------------------
+def idxk_fp8_row(k_row: torch.Tensor) -> torch.Tensor:
+    """One 128-dim fp16 key -> 132 bytes [128 e4m3 | fp32 scale] with
+    scale = max(amax/448, FLT_MIN) (sm70_mla_decode.cu:690-705)."""
+    v = k_row.to(torch.float32).reshape(-1, 128)
+    amax = v.abs().amax(dim=1, keepdim=True)
+    scale = torch.clamp(amax / 448.0, min=FLT_MIN)
+    q = e4m3_encode(v / scale)
+    sb = scale.to(torch.float32).contiguous().view(torch.uint8).reshape(-1, 4)
+    return torch.cat([q, sb], dim=1)
+
+
+def indexer_k_store(kv_cache: torch.Tensor, k: torch.Tensor,
+                    slot: torch.Tensor) -> torch.Tensor:
+    """Returns a copy of kv_cache with k[t] scattered into row slot[t];
+    slots < 0 or >= n_rows are skipped.  Later tokens win on duplicate
+    slots only in the sense that the reference is race-free per token; tests
+    use unique slots."""
+    out = kv_cache.clone()
+    if out.dtype == torch.float16:
+        flat = out.view(-1, k.shape[1])
+        n_rows = flat.shape[0]
+        for t in range(k.shape[0]):
+            r = int(slot[t])
+            if 0 <= r < n_rows:
+                flat[r] = k[t]
+        return out
+    flat = out.view(-1, IDXK_FP8_ROW_BYTES)
+    n_rows = flat.shape[0]
+    rows = idxk_fp8_row(k)
+    s = slot.to(torch.int64)
+    ok = (s >= 0) & (s < n_rows)
+    flat[s[ok]] = rows[ok]
+    return out
+
+
+# ---------------------------------------------------------------------------
+# indexer logits (sm70_mla_decode.cu:150-329 decode, :542-653 packed)
+# ---------------------------------------------------------------------------
+def indexer_logits(q: torch.Tensor, k_cache: torch.Tensor, w: torch.Tensor,
+                   bt: torch.Tensor, seq_lens: torch.Tensor, max_kv: int,
+                   dtype=torch.float64, with_hist: bool = False):
+    """score[b,p] = sum_h relu(q[b,h].K[row(b,p)]) * w[b,h] for p < seq_len,
+    -inf for seq_len <= p < max_kv; K of an unresolvable row is 0.
+    Returns (score fp32 [B,max_kv], hist int32 [B,4096] or None).  The dot
+    and head sum run in `dtype` (fp64 default) and are rounded to fp32 once;
+    for the fp8 cache the per-row scale multiplies the dot before the relu
+    (sm70_mla_decode.cu:309-313)."""
+    B = q.shape[0]
+    page = k_cache.shape[-2]
+    n_rows = k_cache.numel() // (k_cache.shape[-1])
+    score = torch.full((B, max_kv), float("-inf"), dtype=torch.float32)
+    hist = torch.zeros(B, TOPK_NBIN, dtype=torch.int32) if with_hist else None
+    fp8 = k_cache.dtype == torch.uint8
+    for b in range(B):
+        L = min(int(seq_lens[b]), max_kv)
+        if L <= 0:
+            continue
+        pos = torch.arange(L)
+        rows = resolve_rows(pos, bt[b], page, n_rows)
+        if fp8:
+            flat_b = k_cache.reshape(-1, IDXK_FP8_ROW_BYTES)
+            kv = torch.zeros(L, 128, dtype=dtype)
+            sc = torch.zeros(L, dtype=dtype)
+            ok = rows >= 0
+            kv[ok] = e4m3_decode(flat_b[rows[ok], :128].contiguous()).to(dtype)
+            sc[ok] = flat_b[rows[ok], 128:132].contiguous().view(torch.float32).reshape(-1).to(dtype)
+            dots = (q[b].to(dtype) @ kv.T) * sc  # [32, L]
+        else:
+            kv = idxk_rows_fp32(k_cache, rows).to(dtype)
+            dots = q[b].to(dtype) @ kv.T
+        s = (torch.relu(dots) * w[b].to(dtype)[:, None]).sum(dim=0)
+        score[b, :L] = s.to(torch.float32)
+        if with_hist:
+            bins = (mono_key(score[b, :L]) >> 20).to(torch.int64)
+            hist[b] = torch.bincount(bins, minlength=TOPK_NBIN).to(torch.int32)
+    return score, hist
+
+
+def pack_indexer_q(q: torch.Tensor) -> torch.Tensor:
+    """[n,32,128] -> [32, ceil(n/16), 8, 16, 16] (zero-padded rows), the
+    packing of reference/sparse_attn_indexer.py:136-145."""
+    n = q.shape[0]
+    n16 = (n + 15) // 16 * 16
+    if n16 != n:
+        q = torch.nn.functional.pad(q, (0, 0, 0, 0, 0, n16 - n))
+    return (q.reshape(n16 // 16, 16, 32, 8, 16).permute(2, 0, 3, 1, 4).contiguous())
+
+
+def unpack_indexer_q(qp: torch.Tensor, n: int) -> torch.Tensor:
+    """Inverse of pack_indexer_q."""
+    nqt = qp.shape[1]
+    return qp.permute(1, 3, 0, 2, 4).reshape(nqt * 16, 32, 128)[:n]
+
+
+def indexer_logits_packed(qp: torch.Tensor, k_cache, w, bt, seq_lens, max_kv,
+                          dtype=torch.float64):
+    """Prefill logits from packed Q; every query tile gathers keys with the
+    block-table row of the call's first row (sm70_mla_decode.cu:566-567);
+    callers pass one shared row, expanded."""
+    B = w.shape[0]
+    q = unpack_indexer_q(qp, B)
+    bt0 = bt[:1].expand(B, bt.shape[1])
+    return indexer_logits(q, k_cache, w, bt0, seq_lens, max_kv, dtype)[0]
+
+
+# ---------------------------------------------------------------------------
+# top-k selection (contract of sm70_mla_decode.cu:1187-1212 made exact)
+# ---------------------------------------------------------------------------
+def topk_rows(score: torch.Tensor, seq_lens: torch.Tensor, k: int) -> torch.Tensor:
+    """idx[r,:] = positions p < min(seq_len[r], width) of the k largest
+    scores (32-bit monotone-key order, equal keys -> lower position first),
+    emitted in ascending position order, -1 padded.  numpy lexsort brute
+    force."""
+    score = score.contiguous()
+    R, W = score.shape
+    out = np.full((R, k), -1, dtype=np.int32)
+    keys = mono_key(score).numpy()
+    for r in range(R):
+        L = max(0, min(int(seq_lens[r]), W))
+        if L == 0:
+            continue
+        kr = keys[r, :L]
+        pos = np.arange(L)
+        order = np.lexsort((pos, -kr))  # primary: key desc, secondary: pos asc
+        sel = np.sort(order[:k])
+        out[r, :sel.size] = sel
+    return torch.from_numpy(out)
+
+
+# ---------------------------------------------------------------------------
+# sparse MLA attention (sm70_mla_decode.cu:918-1184; triton_mla.py:494-554)
+# ---------------------------------------------------------------------------
+def scaled_q(q: torch.Tensor, scale: float) -> torch.Tensor:
+    """q * scale rounded to fp16 with the scale itself rounded to fp16
+    (__hmul(q, __float2half(scale)), sm70_mla_decode.cu:1016-1018)."""
+    s16 = float(torch.tensor(scale, dtype=torch.float16))
+    return (q.to(torch.float32) * s16).to(torch.float16)
+
+
+def sparse_mla(q: torch.Tensor, kv_cache: torch.Tensor, idx: torch.Tensor,
+               bt: torch.Tensor, seq_lens: torch.Tensor, scale: float,
+               dtype=torch.float64):
+    """Reference sparse attention for every token/head.  A selected entry j
+    is used iff 0 <= idx < seq_len and its row resolves inside the cache
+    (sm70_mla_decode.cu:977-992).  Returns (o fp32 [B,H,512], lse fp32
+    [B,H]); tokens with no valid key get o = 0 and lse = -inf (merge
+    convention, sm70_mla_decode.cu:1175-1183)."""
+    B, H, D = q.shape
+    page = kv_cache.shape[-2]
+    row_w = kv_cache.shape[-1]
+    n_rows = kv_cache.numel() // row_w
+    o = torch.zeros(B, H, 512, dtype=torch.float32)
+    lse = torch.full((B, H), float("-inf"), dtype=torch.float32)
+    qs = scaled_q(q, scale).to(dtype)
+    for b in range(B):
+        sel = idx[b].to(torch.int64)
+        L = int(seq_lens[b])
+        valid = (sel >= 0) & (sel < L)
+        rows = resolve_rows(torch.where(valid, sel, torch.zeros_like(sel)),
+                            bt[b], page, n_rows)
+        rows = torch.where(valid, rows, torch.full_like(rows, -1))
+        use = rows >= 0
+        if not bool(use.any()):
+            continue
+        kv = latent_rows_fp16(kv_cache, rows[use]).to(dtype)  # [n, 576]
+        s = qs[b] @ kv.T  # [H, n]
+        m = s.max(dim=1, keepdim=True).values
+        p = torch.exp(s - m)
+        l = p.sum(dim=1, keepdim=True)
+        o[b] = ((p @ kv[:, :512]) / l).to(torch.float32)
+        lse[b] = (m + torch.log(l)).squeeze(1).to(torch.float32)
+    return o, lse
+
+
+def dense_mla(q: torch.Tensor, kv_cache: torch.Tensor, bt: torch.Tensor,
+              seq_lens: torch.Tensor, scale: float, dtype=torch.float64):
+    """Dense causal MLA decode over positions [0, seq_len): the plain-torch
+    path of reference/triton_mla.py:494-554 (gather -> bmm -> mask ->
+    softmax -> bmm), with q scaled as the sparse kernel does."""
+    B = q.shape[0]
+    max_kv = bt.shape[1] * kv_cache.shape[-2]
+    idx = torch.arange(max_kv, dtype=torch.int32).expand(B, max_kv).contiguous()
+    return sparse_mla(q, kv_cache, idx, bt, seq_lens, scale, dtype)
+
+
+# ---------------------------------------------------------------------------
+# fp8_ds_mla latent-cache writer (generator side; the reference's writer
+# concat_and_cache_ds_mla is not vendored, only its 656-B layout is:
+# sm70_mla_decode.cu:74-100, triton_mla.py:92-95)
+# ---------------------------------------------------------------------------
+def dsmla_rows(latent: torch.Tensor, per_tile: bool = False) -> torch.Tensor:
+    """[n,576] fp16/fp32 -> [n,656] uint8 rows.  NoPE scale = amax/448 over
+    the 512 NoPE dims written into all 4 tile slots (per_tile=False), or
+    one amax/448 per 128-dim tile (per_tile=True); RoPE copied as fp16."""
+    x = latent.to(torch.float32)
+    n = x.shape[0]
+    nope = x[:, :512].reshape(n, 4, 128)
+    if per_tile:
+        amax = nope.abs().amax(dim=2, keepdim=True)
+    else:
+        amax = nope.abs().amax(dim=(1, 2), keepdim=True).expand(n, 4, 1)
+    scale = torch.clamp(amax / 448.0, min=FLT_MIN).contiguous()
+    qb = e4m3_encode(nope / scale).reshape(n, 512)
+    sb = scale.reshape(n, 4).contiguous().view(torch.uint8).reshape(n, 16)
+    rb = x[:, 512:576].to(torch.float16).contiguous().view(torch.uint8).reshape(n, 128)
+    return torch.cat([qb, sb, rb], dim=1).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# fp8 weight-only projections (glue.patch:1515-1532; sm70_attn_fp8.cu)
+# ---------------------------------------------------------------------------
+def attn_fp8_quantize(weight: torch.Tensor):
+    """[128,128]-block e4m3 quantization of an [N,K] weight: pad to 128
+    multiples, scale = clamp(amax/448, 1e-12), q = clamp(w/scale, +-448) ->
+    e4m3, crop (restates _sm70_attn_fp8_quantize, glue.patch:1515-1532)."""
+    n, k = weight.shape
+    nb, kb = (n + 127) // 128, (k + 127) // 128
+    padded = torch.zeros(nb * 128, kb * 128, dtype=torch.float32)
+    padded[:n, :k] = weight.float()
+    blocks = padded.view(nb, 128, kb, 128)
+    scale = (blocks.abs().amax(dim=(1, 3)) / 448.0).clamp(min=1e-12)
+    qv = (blocks / scale[:, None, :, None]).clamp(-448.0, 448.0)
+    q8 = qv.to(torch.float8_e4m3fn).view(torch.uint8)
+    q8 = q8.view(nb * 128, kb * 128)[:n, :k].contiguous()
+    return q8, scale.contiguous()
+
+
+def expand_block_scale(s: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    return s.repeat_interleave(128, 0).repeat_interleave(128, 1)[:n, :k]
+
+
+def attn_fp8_dequant(w: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """fp16_rn(fp32(e4m3(w) * s)) (sm70_attn_fp8.cu:122-144)."""
+    n, k = w.shape
+    return (e4m3_decode(w) * expand_block_scale(s, n, k)).to(torch.float16)
+
+
+def attn_fp8_gemv(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """y = x @ deq(W)^T in fp64 (sm70_attn_fp8.cu:51-116 computes the same
+    sum with fp16/fp32 partial sums)."""
+    n, k = w.shape
+    deq = e4m3_decode(w).double() * expand_block_scale(s, n, k).double()
+    return x.double() @ deq.T

@@ -1,0 +1,174 @@
+"""GPU parity: indexer logits (decode and packed prefill) and the fused
+histogram.  Dyadic inputs make every fp32 partial sum exact, so those cases
+are bit-exact against the oracle; random inputs are compared within fp32
+reassociation tolerance; the histogram is bit-exact given the kernel's own
+scores."""
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def make_case(seed, B, nblk, page, fp8, dyadic, max_kv, seq):
+    g = torch.Generator().manual_seed(seed)
+    if dyadic:
+        k = (torch.randint(-8, 9, (nblk * page, 128), generator=g) / 8).to(torch.float16)
+        q = (torch.randint(-8, 9, (B, 32, 128), generator=g) / 8).to(torch.float16)
+        w = (torch.randint(-4, 5, (B, 32), generator=g) / 4).to(torch.float16)
+    else:
+        k = torch.randn(nblk * page, 128, generator=g).to(torch.float16)
+        q = torch.randn(B, 32, 128, generator=g).to(torch.float16)
+        w = (torch.randn(B, 32, generator=g) / 32 ** 0.5).to(torch.float16)
+    if fp8:
+        kc = O.indexer_k_store(torch.zeros(nblk, page, 132, dtype=torch.uint8), k,
+                               torch.arange(nblk * page, dtype=torch.int32))
+    else:
+        kc = k.view(nblk, page, 128)
+    mb = (max_kv + page - 1) // page
+    bt = torch.stack([torch.randperm(nblk, generator=g)[:mb] for _ in range(B)]).to(torch.int32)
+    seq = torch.tensor(seq, dtype=torch.int32)
+    return q, kc, w, bt, seq
+
+
+CASES = [
+    # seed, B, nblk, page, fp8, dyadic, max_kv, seq_lens
+    (0, 1, 40, 64, False, True, 2048, [2048]),
+    (1, 3, 40, 64, False, True, 2500, [2500, 1, 1700]),
+    (2, 4, 70, 16, False, False, 1100, [1100, 900, 1024, 0]),
+    (3, 2, 40, 64, True, True, 2048, [2000, 2048]),
+    (4, 2, 40, 64, True, False, 2560, [2560, 77]),
+    (5, 9, 20, 64, False, False, 1280, [1280] * 9),   # B >= 8 (reference WMMA branch)
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"seed{c[0]}" for c in CASES])
+def test_logits_and_hist(ops, dev, case):
+    seed, B, nblk, page, fp8, dyadic, max_kv, seq = case
+    q, kc, w, bt, seq = make_case(seed, B, nblk, page, fp8, dyadic, max_kv, seq)
+    score = torch.full((B, max_kv), 7.0, device=dev)
+    hist = torch.zeros(B, 4096, dtype=torch.int32, device=dev)
+    ops.sm70_indexer_logits(score, q.to(dev), kc.to(dev), w.to(dev), bt.to(dev), seq.to(dev), hist)
+    got = score.cpu()
+    want, _ = O.indexer_logits(q, kc, w, bt, seq, max_kv)
+    assert torch.equal(torch.isinf(got), torch.isinf(want))
+    fin = torch.isfinite(want)
+    if dyadic and not fp8:
+        assert torch.equal(got[fin], want[fin])
+    else:
+        tol = 1e-5 * want[fin].abs().max().item() + 1e-6
+        assert (got[fin] - want[fin]).abs().max().item() <= tol
+    # histogram == bincount of the kernel's own scores over p < seq_len
+    for b in range(B):
+        L = min(int(seq[b]), max_kv)
+        ref = torch.bincount((O.mono_key(got[b, :L]) >> 20).long(), minlength=4096)
+        assert torch.equal(hist[b].cpu().long(), ref)
+
+
+def test_duplicate_keys_score_identically(ops, dev):
+    g = torch.Generator().manual_seed(11)
+    page, nblk = 64, 32
+    k = torch.randn(nblk * page, 128, generator=g).to(torch.float16)
+    src = torch.randint(0, nblk * page, (300,), generator=g)
+    dst = torch.randint(0, nblk * page, (300,), generator=g)
+    k[dst] = k[src]
+    q = torch.randn(1, 32, 128, generator=g).to(torch.float16)
+    w = torch.randn(1, 32, generator=g).to(torch.float16)
+    bt = torch.arange(nblk, dtype=torch.int32)[None]
+    seq = torch.tensor([nblk * page], dtype=torch.int32)
+    score = torch.empty(1, nblk * page, device=dev)
+    ops.sm70_indexer_logits(score, q.to(dev), k.view(nblk, page, 128).to(dev), w.to(dev),
+                            bt.to(dev), seq.to(dev), None)
+    s = score.cpu()[0]
+    assert torch.equal(s[dst], s[src])
+
+
+PACKED = [
+    # seed, B, nblk, page, fp8, dyadic, max_kv, causal
+    (0, 16, 20, 64, False, True, 1024, True),
+    (1, 37, 20, 64, False, True, 1280, True),
+    (2, 130, 40, 64, False, False, 2560, True),
+    (3, 64, 20, 64, True, False, 1024, False),
+    (4, 5, 10, 16, False, False, 160, True),
+]
+
+
+@pytest.mark.parametrize("case", PACKED, ids=[f"p{c[0]}" for c in PACKED])
+def test_packed_logits(ops, dev, case):
+    seed, B, nblk, page, fp8, dyadic, max_kv, causal = case
+    base = max_kv - B
+    seq = [base + i + 1 for i in range(B)] if causal else [max_kv] * B
+    q, kc, w, bt1, seq = make_case(seed, 1, nblk, page, fp8, dyadic, max_kv, seq[:1])
+    g = torch.Generator().manual_seed(seed + 100)
+    if dyadic:
+        q = (torch.randint(-8, 9, (B, 32, 128), generator=g) / 8).to(torch.float16)
+        w = (torch.randint(-4, 5, (B, 32), generator=g) / 4).to(torch.float16)
+    else:
+        q = torch.randn(B, 32, 128, generator=g).to(torch.float16)
+        w = (torch.randn(B, 32, generator=g) / 32 ** 0.5).to(torch.float16)
+    seqs = torch.tensor([base + i + 1 for i in range(B)] if causal else [max_kv] * B,
+                        dtype=torch.int32)
+    bt = bt1.expand(B, bt1.shape[1]).contiguous()  # one request row, expanded
+    qp = O.pack_indexer_q(q)
+    score = torch.full((B, max_kv), 7.0, device=dev)
+    ops.sm70_indexer_logits_packed(score, qp.to(dev), kc.to(dev), w.to(dev), bt.to(dev),
+                                   seqs.to(dev))
+    got = score.cpu()
+    if fp8:
+        # the packed path dequantises keys to fp16 first (fp16_rn(e4m3*scale))
+        flat = kc.view(-1, 132)
+        k16 = (O.e4m3_decode(flat[:, :128].contiguous()) *
+               flat[:, 128:].contiguous().view(torch.float32)).to(torch.float16)
+        kc_ref = k16.view(nblk, page, 128)
+    else:
+        kc_ref = kc
+    want = O.indexer_logits_packed(qp, kc_ref, w, bt, seqs, max_kv)
+    assert torch.equal(torch.isinf(got), torch.isinf(want))
+    fin = torch.isfinite(want)
+    if dyadic:
+        assert torch.equal(got[fin], want[fin])
+    else:
+        tol = 1e-5 * want[fin].abs().max().item() + 1e-6
+        assert (got[fin] - want[fin]).abs().max().item() <= tol
+
+
+def test_packed_matches_decode_kernel_on_dyadic(ops, dev):
+    """Both kernels compute exactly the same scores on exact inputs."""
+    B, nblk, page, max_kv = 24, 20, 64, 1280
+    q, kc, w, bt1, _ = make_case(21, 1, nblk, page, False, True, max_kv, [max_kv])
+    g = torch.Generator().manual_seed(22)
+    q = (torch.randint(-8, 9, (B, 32, 128), generator=g) / 8).to(torch.float16)
+    w = (torch.randint(-4, 5, (B, 32), generator=g) / 4).to(torch.float16)
+    bt = bt1.expand(B, bt1.shape[1]).contiguous().to(dev)
+    seq = torch.arange(max_kv - B + 1, max_kv + 1, dtype=torch.int32, device=dev)
+    a = torch.empty(B, max_kv, device=dev)
+    b = torch.empty(B, max_kv, device=dev)
+    ops.sm70_indexer_logits(a, q.to(dev), kc.to(dev), w.to(dev), bt, seq, None)
+    ops.sm70_indexer_logits_packed(b, O.pack_indexer_q(q).to(dev), kc.to(dev), w.to(dev), bt, seq)
+    assert torch.equal(a, b)
+
+
+def test_decode_c2_full_size(ops, pkg, dev):
+    """Config C2 (B=4, 64k keys, ~1% duplicated keys) against an fp32 torch
+    computation on the GPU (gather + matmul + relu*w), then top-k bit-exact
+    against the C oracle on the kernel's own scores."""
+    from oracle import cref
+
+    d = pkg.synthetic.indexer_decode_inputs(device=dev)
+    B, max_kv = 4, d["max_kv"]
+    score = torch.empty(B, max_kv, device=dev)
+    hist = torch.zeros(B, 4096, dtype=torch.int32, device=dev)
+    ops.sm70_indexer_logits(score, d["q"], d["kc"], d["w"], d["bt"], d["seq"], hist)
+    page = 64
+    pos = torch.arange(max_kv, device=dev)
+    rows = (d["bt"].long()[:, pos // page] * page + pos % page)  # [B, max_kv]
+    K = d["k"].float()[rows]  # [B, max_kv, 128]
+    dots = torch.bmm(d["q"].float(), K.transpose(1, 2).contiguous())  # [B, 32, max_kv]
+    ref = (torch.relu(dots) * d["w"].float()[:, :, None]).sum(1)
+    err = (score - ref).abs().max().item()
+    assert err <= 1e-5 * ref.abs().max().item(), err
+    idx = torch.empty(B, 2048, dtype=torch.int32, device=dev)
+    ops.sm70_decode_topk(idx, score, d["seq"], hist, 2048)
+    want = cref.topk_rows(score.cpu(), d["seq"].cpu(), 2048)
+    assert torch.equal(idx.cpu(), want)

@@ -1,0 +1,164 @@
+"""GPU parity: sparse MLA attention (decode split/merge configuration and the
+64-head prefill configuration), fp16 and fp8_ds_mla caches.
+
+Tolerances: o within 2e-3 relative / 1e-3 absolute
+(fp16), lse within 1e-4 absolute, against the fp64 oracle on the same
+seeded inputs."""
+import math
+
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 576 ** -0.5
+RTOL, ATOL, LSE_ATOL = 2e-3, 1e-3, 1e-4
+
+
+def make(seed, B, H, nblk, page, fp8, topk, seqs, invalid_frac=0.0, shared_bt=False):
+    g = torch.Generator().manual_seed(seed)
+    lat = torch.randn(nblk * page, 576, generator=g) / 24.0
+    kv = (O.dsmla_rows(lat).view(nblk, page, 656) if fp8
+          else lat.to(torch.float16).view(nblk, page, 576))
+    mb = max((max(seqs) + page - 1) // page, 1)
+    if shared_bt:
+        bt = torch.randperm(nblk, generator=g)[:mb].expand(B, mb).to(torch.int32).contiguous()
+    else:
+        bt = torch.stack([torch.randperm(nblk, generator=g)[:mb] for _ in range(B)]).to(torch.int32)
+    seq = torch.tensor(seqs, dtype=torch.int32)
+    q = (torch.randn(B, H, 576, generator=g) / 24.0 * 6).to(torch.float16)
+    idx = torch.full((B, topk), -1, dtype=torch.int32)
+    for b in range(B):
+        L = int(seq[b])
+        n = min(L, topk)
+        if n > 0:
+            sel = torch.randperm(L, generator=g)[:n].sort().values
+            idx[b, :n] = sel.to(torch.int32)
+    if invalid_frac:
+        m = torch.rand(B, topk, generator=g) < invalid_frac
+        idx[m] = -1
+        idx[torch.rand(B, topk, generator=g) < invalid_frac] = 10 ** 8  # >= seq_len
+    return q, kv, idx, bt, seq
+
+
+def run(ops, dev, q, kv, idx, bt, seq):
+    B, H = q.shape[:2]
+    o = torch.full((B, H, 512), float("nan"), dtype=torch.float16, device=dev)
+    lse = torch.full((B, H), float("nan"), device=dev)
+    ops.sm70_sparse_mla_decode(o, lse, q.to(dev), kv.to(dev), idx.to(dev), bt.to(dev),
+                               seq.to(dev), SCALE)
+    return o.float().cpu(), lse.cpu()
+
+
+def check(o, lse, ro, rl):
+    assert torch.equal(torch.isinf(lse), torch.isinf(rl))
+    fin = torch.isfinite(rl)
+    assert (lse[fin] - rl[fin]).abs().max().item() <= LSE_ATOL if fin.any() else True
+    torch.testing.assert_close(o, ro, rtol=RTOL, atol=ATOL)
+
+
+DECODE = [
+    # seed, B, H, nblk, page, fp8, topk, seqs
+    (0, 1, 64, 40, 64, False, 2048, [2500]),
+    (1, 4, 64, 40, 64, True, 2048, [2500, 2048, 700, 1]),
+    (2, 2, 16, 30, 64, True, 512, [1900, 30]),
+    (3, 3, 8, 20, 16, False, 256, [300, 200, 17]),   # partial head tile
+    (4, 4, 64, 60, 64, True, 2048, [3800, 3800, 3800, 3800]),
+    (5, 1, 128, 40, 64, False, 1024, [2400]),         # two 64-head groups
+]
+
+
+@pytest.mark.parametrize("case", DECODE, ids=[f"d{c[0]}" for c in DECODE])
+def test_decode(ops, dev, case):
+    seed, B, H, nblk, page, fp8, topk, seqs = case
+    q, kv, idx, bt, seq = make(seed, B, H, nblk, page, fp8, topk, seqs)
+    o, lse = run(ops, dev, q, kv, idx, bt, seq)
+    ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
+    check(o, lse, ro, rl)
+
+
+def test_decode_invalid_entries(ops, dev):
+    q, kv, idx, bt, seq = make(10, 3, 64, 40, 64, True, 2048, [2500, 1000, 2048],
+                               invalid_frac=0.3)
+    idx[2] = -1  # a token with no valid key: o = 0, lse = -inf
+    o, lse = run(ops, dev, q, kv, idx, bt, seq)
+    ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
+    check(o, lse, ro, rl)
+    assert torch.all(o[2] == 0) and torch.all(torch.isinf(lse[2]))
+
+
+def test_prefill_config(ops, dev):
+    """B >= 256 tokens takes the 64-head prefill configuration."""
+    B = 300
+    seqs = [1800 + 3 * i for i in range(B)]
+    q, kv, idx, bt, seq = make(20, B, 64, 60, 64, True, 2048, seqs, shared_bt=True)
+    o, lse = run(ops, dev, q, kv, idx, bt, seq)
+    ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
+    check(o, lse, ro, rl)
+
+
+def test_prefill_equals_decode_config(ops, dev):
+    """Split-count / configuration invariance: the first rows of a 256-token
+    batch (prefill configuration) equal the same rows run alone (decode
+    configuration with splits and merge) within rounding."""
+    B = 256
+    q, kv, idx, bt, seq = make(21, B, 64, 40, 64, False, 2048, [2300] * B, shared_bt=True)
+    o_all, l_all = run(ops, dev, q, kv, idx, bt, seq)
+    o_4, l_4 = run(ops, dev, q[:4], kv, idx[:4], bt[:4], seq[:4])
+    torch.testing.assert_close(o_all[:4], o_4, rtol=RTOL, atol=ATOL)
+    assert (l_all[:4] - l_4).abs().max() <= LSE_ATOL
+
+
+def test_closed_forms(ops, dev):
+    g = torch.Generator().manual_seed(30)
+    nblk, page = 8, 64
+    lat = torch.randn(nblk * page, 576, generator=g) / 24.0
+    kv = lat.to(torch.float16).view(nblk, page, 576)
+    bt = torch.arange(nblk, dtype=torch.int32)[None].repeat(2, 1)
+    seq = torch.tensor([500, 500], dtype=torch.int32)
+    q = torch.randn(2, 64, 576, generator=g).to(torch.float16)
+    idx = torch.full((2, 2048), -1, dtype=torch.int32)
+    idx[0, 1000] = 123          # single key: o = V, lse = s
+    q[1] = 0                    # equal scores: o = mean V, lse = ln n
+    idx[1, :10] = torch.arange(10, 20, dtype=torch.int32)
+    o, lse = run(ops, dev, q, kv, idx, bt, seq)
+    V = kv.view(-1, 576).float()
+    torch.testing.assert_close(o[0], V[123, :512].expand(64, 512), rtol=1e-3, atol=1e-3)
+    qs = O.scaled_q(q[:1], SCALE)[0].float()
+    assert (lse[0] - qs @ V[123]).abs().max() <= LSE_ATOL
+    torch.testing.assert_close(o[1], V[10:20, :512].mean(0).expand(64, 512), rtol=1e-3, atol=1e-3)
+    assert (lse[1] - math.log(10)).abs().max() <= LSE_ATOL
+
+
+def test_sparse_equals_dense_below_topk(ops, dev):
+    """DSA invariant (reference/triton_mla.py:225-233): with seq_len <= topk
+    every position is selected and sparse attention equals dense attention."""
+    q, kv, idx, bt, seq = make(31, 2, 64, 40, 64, True, 2048, [1500, 2048])
+    o, lse = run(ops, dev, q, kv, idx, bt, seq)
+    ro, rl = O.dense_mla(q, kv, bt, seq, SCALE)
+    check(o, lse, ro, rl)
+
+
+def test_c3_full_size(ops, pkg, dev):
+    """Config C3: B=4, 180k context, 64 heads, topk 2048, fp8_ds_mla cache of
+    11,520 pages; the oracle runs on just the selected rows."""
+    d = pkg.synthetic.decode_inputs(device=dev)
+    B, H = d["q"].shape[:2]
+    o = torch.empty(B, H, 512, dtype=torch.float16, device=dev)
+    lse = torch.empty(B, H, device=dev)
+    ops.sm70_sparse_mla_decode(o, lse, d["q"], d["kv"], d["idx"], d["bt"], d["seq"], d["scale"])
+    # compact cache with only the selected rows, in idx order
+    page = d["kv"].shape[1]
+    pos = d["idx"].long()
+    rows = d["bt"].long().gather(1, pos // page) * page + pos % page
+    sel = d["kv"].view(-1, 656)[rows.reshape(-1)].cpu()
+    n = sel.shape[0]
+    kv_c = sel.view(n // 64, 64, 656)
+    topk = pos.shape[1]
+    idx_c = torch.arange(B * topk, dtype=torch.int32).view(B, topk)
+    bt_c = torch.arange(n // 64, dtype=torch.int32)[None].repeat(B, 1)
+    seq_c = torch.full((B,), n, dtype=torch.int32)
+    ro, rl = O.sparse_mla(d["q"].cpu(), kv_c, idx_c, bt_c, seq_c, d["scale"])
+    check(o.float().cpu(), lse.cpu(), ro, rl)

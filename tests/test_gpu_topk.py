@@ -1,0 +1,91 @@
+"""GPU parity: decode top-k and the prefill row top-k (persistent_topk),
+bit-exact against the C oracle on identical score tensors (ties, -inf,
+seq_len <= k, all-equal rows, inconsistent histogram)."""
+import pytest
+import torch
+
+from oracle import cref
+from oracle import dsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def hist_of(score, seq):
+    B, W = score.shape
+    h = torch.zeros(B, 4096, dtype=torch.int32)
+    for b in range(B):
+        L = min(int(seq[b]), W)
+        h[b] = torch.bincount((O.mono_key(score[b, :L]) >> 20).long(), minlength=4096).to(torch.int32)
+    return h
+
+
+def scores(kind, B, W, g):
+    if kind == "randn":
+        return torch.randn(B, W, generator=g)
+    if kind == "ties":
+        return torch.round(torch.randn(B, W, generator=g) * 2) / 2
+    if kind == "equal":
+        return torch.full((B, W), 0.25)
+    if kind == "mixed":
+        s = torch.randn(B, W, generator=g) * 1e3
+        s[:, ::3] = float("-inf")
+        s[:, 1::7] = -0.0
+        s[:, 2::7] = 0.0
+        return s
+    raise ValueError(kind)
+
+
+CASES = [
+    ("randn", 4, 65536, [65536, 65000, 3000, 2049]),
+    ("ties", 3, 20000, [20000, 2048, 2047]),
+    ("equal", 2, 10000, [10000, 5000]),
+    ("mixed", 2, 33000, [33000, 16385]),
+    ("randn", 1, 100, [100]),
+    ("randn", 2, 70000, [0, 70000]),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-{c[1]}x{c[2]}" for c in CASES])
+@pytest.mark.parametrize("K", [2048, 512, 1])
+def test_decode_topk(ops, dev, case, K):
+    kind, B, W, seq = case
+    g = torch.Generator().manual_seed(B * W + K)
+    s = scores(kind, B, W, g)
+    seq = torch.tensor(seq, dtype=torch.int32)
+    idx = torch.full((B, K), 123, dtype=torch.int32, device=dev)
+    ops.sm70_decode_topk(idx, s.to(dev), seq.to(dev), hist_of(s, seq).to(dev), K)
+    assert torch.equal(idx.cpu(), cref.topk_rows(s, seq, K))
+
+
+def test_decode_topk_rebuilds_bad_hist(ops, dev):
+    g = torch.Generator().manual_seed(5)
+    s = torch.randn(2, 9000, generator=g)
+    seq = torch.tensor([9000, 8000], dtype=torch.int32)
+    idx = torch.empty(2, 2048, dtype=torch.int32, device=dev)
+    ops.sm70_decode_topk(idx, s.to(dev), seq.to(dev), torch.zeros(2, 4096, dtype=torch.int32, device=dev), 2048)
+    assert torch.equal(idx.cpu(), cref.topk_rows(s, seq, 2048))
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-{c[1]}x{c[2]}" for c in CASES])
+def test_persistent_topk(ops, dev, case):
+    kind, B, W, seq = case
+    g = torch.Generator().manual_seed(B + W)
+    s = scores(kind, B, W, g)
+    seq = torch.tensor(seq, dtype=torch.int32)
+    out = torch.full((B, 2048), 77, dtype=torch.int32, device=dev)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+    ops.persistent_topk(s.to(dev), seq.view(B, 1).to(dev), out, ws, 2048, W)
+    assert torch.equal(out.cpu(), cref.topk_rows(s, seq, 2048))
+
+
+def test_persistent_topk_causal_block(ops, dev):
+    """A 128-row prefill sub-block with causal lengths (rows < 2048 select
+    everything up to themselves)."""
+    g = torch.Generator().manual_seed(9)
+    R, W = 128, 4096
+    s = torch.randn(R, W, generator=g)
+    seq = torch.arange(1985, 1985 + R, dtype=torch.int32) * 2 - 1985  # crosses 2048
+    out = torch.empty(R, 2048, dtype=torch.int32, device=dev)
+    ops.persistent_topk(s.to(dev), seq.view(R, 1).to(dev), out,
+                        torch.empty(1 << 20, dtype=torch.uint8, device=dev), 2048, W)
+    assert torch.equal(out.cpu(), cref.topk_rows(s, seq, 2048))

@@ -1,0 +1,124 @@
+"""Pins the oracle's sparse MLA attention and fp8_ds_mla writer (CPU only).
+
+Independent checks: closed forms (one key, equal scores, no valid key), the
+DSA invariant sparse == dense when every context position is selected
+(reference/triton_mla.py:225-233), invariance under idx order and under a
+physical block permutation, and byte-level layout checks of the 656-byte
+row (csrc/attention/sm70_mla_decode.cu:74-100).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+
+SCALE = 576 ** -0.5
+
+
+def make_cache(g, nblk=6, page=16, fp8=False):
+    lat = torch.randn(nblk * page, 576, generator=g) / 4
+    if fp8:
+        return O.dsmla_rows(lat).view(nblk, page, 656), lat
+    return lat.to(torch.float16).view(nblk, page, 576), lat
+
+
+def test_single_key_closed_form():
+    g = torch.Generator().manual_seed(0)
+    kv, _ = make_cache(g)
+    bt = torch.randperm(6, generator=g).to(torch.int32)[None]
+    q = torch.randn(1, 4, 576, generator=g).to(torch.float16)
+    j = 37
+    idx = torch.full((1, 8), -1, dtype=torch.int32)
+    idx[0, 3] = j
+    o, lse = O.sparse_mla(q, kv, idx, bt, torch.tensor([50], dtype=torch.int32), SCALE)
+    row = int(bt[0, j // 16]) * 16 + j % 16
+    K = kv.view(-1, 576)[row].double()
+    assert torch.allclose(o[0], K[:512].float().expand(4, 512))
+    qs = O.scaled_q(q, SCALE)[0].double()
+    assert torch.allclose(lse[0].double(), qs @ K, atol=1e-6)
+
+
+def test_equal_scores_closed_form():
+    g = torch.Generator().manual_seed(1)
+    kv, _ = make_cache(g)
+    bt = torch.arange(6, dtype=torch.int32)[None]
+    q = torch.zeros(1, 2, 576, dtype=torch.float16)
+    idx = torch.tensor([[5, 9, 11, -1, 70, 2]], dtype=torch.int32)  # 70 >= seq_len
+    o, lse = O.sparse_mla(q, kv, idx, bt, torch.tensor([64], dtype=torch.int32), SCALE)
+    V = kv.view(-1, 576)[[5, 9, 11, 2], :512].double()
+    assert torch.allclose(o[0].double(), V.mean(0).expand(2, 512), atol=1e-6)
+    assert torch.allclose(lse[0].double(), torch.full((2,), math.log(4.0), dtype=torch.float64))
+
+
+def test_no_valid_key():
+    g = torch.Generator().manual_seed(2)
+    kv, _ = make_cache(g)
+    bt = torch.arange(6, dtype=torch.int32)[None]
+    q = torch.randn(1, 3, 576, generator=g).to(torch.float16)
+    idx = torch.tensor([[-1, 40, 41]], dtype=torch.int32)
+    o, lse = O.sparse_mla(q, kv, idx, bt, torch.tensor([40], dtype=torch.int32), SCALE)
+    assert torch.all(o == 0) and torch.all(torch.isinf(lse)) and torch.all(lse < 0)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_sparse_equals_dense_when_all_selected(fp8):
+    g = torch.Generator().manual_seed(3)
+    kv, _ = make_cache(g, fp8=fp8)
+    B, H = 2, 8
+    bt = torch.stack([torch.randperm(6, generator=g) for _ in range(B)]).to(torch.int32)
+    seq = torch.tensor([61, 96], dtype=torch.int32)
+    q = (torch.randn(B, H, 576, generator=g) / 4).to(torch.float16)
+    idx = torch.full((B, 128), -1, dtype=torch.int32)
+    for b in range(B):
+        perm = torch.randperm(int(seq[b]), generator=g).to(torch.int32)
+        idx[b, : perm.numel()] = perm
+    o_s, l_s = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
+    o_d, l_d = O.dense_mla(q, kv, bt, seq, SCALE)
+    assert torch.allclose(o_s, o_d, atol=1e-6)
+    assert torch.allclose(l_s, l_d, atol=1e-6)
+
+
+def test_block_permutation_invariance():
+    g = torch.Generator().manual_seed(4)
+    kv, _ = make_cache(g)
+    q = torch.randn(1, 4, 576, generator=g).to(torch.float16)
+    bt = torch.arange(6, dtype=torch.int32)[None]
+    idx = torch.randint(0, 90, (1, 32), generator=g, dtype=torch.int32)
+    seq = torch.tensor([90], dtype=torch.int32)
+    o1, l1 = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
+    perm = torch.randperm(6, generator=g)
+    kv2 = torch.empty_like(kv)
+    kv2[perm] = kv  # logical block i now lives in physical block perm[i]
+    o2, l2 = O.sparse_mla(q, kv2, idx, perm.to(torch.int32)[None], seq, SCALE)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+def test_dsmla_row_layout():
+    g = torch.Generator().manual_seed(5)
+    lat = torch.randn(10, 576, generator=g)
+    rows = O.dsmla_rows(lat)
+    assert rows.shape == (10, 656) and rows.dtype == torch.uint8
+    sc = rows[:, 512:528].contiguous().view(torch.float32)
+    amax = lat[:, :512].abs().amax(1)
+    assert torch.equal(sc, (amax / 448.0).unsqueeze(1).expand(10, 4))
+    rope = rows[:, 528:].contiguous().view(torch.float16)
+    assert torch.equal(rope, lat[:, 512:].to(torch.float16))
+    deq = O.e4m3_decode(rows[:, :512].contiguous()) * sc.repeat_interleave(128, 1)
+    err = (deq - lat[:, :512]).abs() / amax[:, None]
+    assert err.max() <= 2.0 ** -4  # e4m3 relative step at the top binade
+    # the row maximum itself is encoded as +-448
+    i = lat[:, :512].abs().argmax(1)
+    top = rows[torch.arange(10), i] & 0x7F
+    assert torch.all(top == 0x7E)
+
+
+def test_dsmla_per_tile_layout():
+    lat = torch.zeros(1, 576)
+    lat[0, 0] = 4.0
+    lat[0, 200] = -8.0
+    rows = O.dsmla_rows(lat, per_tile=True)
+    sc = rows[:, 512:528].contiguous().view(torch.float32)[0]
+    assert sc[0] == 4.0 / 448 and sc[1] == 8.0 / 448
+    assert sc[2] == O.FLT_MIN and sc[3] == O.FLT_MIN
+    assert int(rows[0, 0]) == 0x7E and int(rows[0, 200]) == 0xFE
