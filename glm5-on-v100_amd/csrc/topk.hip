@@ -140,7 +140,7 @@ __global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
   uint32_t need = (uint32_t)K - above;
   uint32_t prefix = (uint32_t)T;
   int shift = 20;
-  uint32_t bin_count = sh.hist[T];
+  uint32_t bin_count = (T >= 0) ? sh.hist[T] : 0u;
 
   // ---- level 2: bits [8,20) of keys in bin T ----
   if (bin_count > need) {
@@ -156,7 +156,7 @@ __global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
     need -= above;
     prefix = (prefix << 12) | (uint32_t)T;
     shift = 8;
-    bin_count = sh.hist[T];
+    bin_count = (T >= 0) ? sh.hist[T] : 0u;
     // ---- level 3: bits [0,8) ----
     if (bin_count > need) {
       __syncthreads();
@@ -206,10 +206,16 @@ __global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
     for (int i = 0; i < kTkV; i++) {
       const bool gt = (gt_mask >> i) & 1u;
       const bool eq = (eq_mask >> i) & 1u;
+      // o < K always holds by construction; the bound keeps a logic error
+      // from ever writing outside the row
       if (gt) {
-        out[o++] = c0 + my0 + i;
+        if (o < (uint32_t)K) out[o] = c0 + my0 + i;
+        o++;
       } else if (eq) {
-        if (E < n_eq_take) out[o++] = c0 + my0 + i;
+        if (E < n_eq_take) {
+          if (o < (uint32_t)K) out[o] = c0 + my0 + i;
+          o++;
+        }
         E++;
       }
     }

@@ -182,7 +182,8 @@ def indexer_logits_packed_impl(score, q_packed, k_cache, weights, block_table, s
            and q_packed.size(2) == 8 and q_packed.size(3) == 16 and q_packed.size(4) == 16,
            "q_packed must be [32, ceil(B/16), 8, 16, 16]")
     _check(weights.numel() == B * 32, "weights must be [B, 32]")
-    _check(block_table.dim() == 2 and block_table.size(0) >= 1, "block_table must be 2-D")
+    _check(block_table.dim() == 2 and block_table.size(0) == B,
+           "block_table must be [B, max_blocks]")
     _check(seq_lens.numel() == B, "seq_lens must be [B]")
     if B == 0 or score.size(1) == 0:
         return
