@@ -1,0 +1,275 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X DSA sparse-attention hot path on one GPU.
+
+Headline (BASELINE.json metric "sparse MLA decode us/layer @180k ctx (HBM
+GB/s); indexer prefill TFLOPS @64k"):
+
+* step = one decode step of the model's DSA attention: sparse MLA decode
+  for a batch of 4 tokens (64 heads, qk 576 / v 512, top-2048 keys, 180k
+  context, fp8_ds_mla paged cache) through `--layers` layers (default 78,
+  GLM-5.1's depth), each layer with its own queries and top-k indices so the
+  gathered rows do not stay resident in the 256 MB MALL.  The layer calls are
+  captured once in a HIP graph and replayed; `value` is microseconds per
+  layer (lower is better).
+* extra records: indexer prefill logits TFLOPS over a 64k-token causal
+  prefill (the caller's 128-row sub-chunks, causal-triangle FLOPs only), a
+  context-flatness sweep of the decode, the roofline of the decode kernel
+  and the CPU baseline (the oracle's PyTorch restatement on the host cores).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L]
+Only one GPU is supported: --gpus N with N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+METRIC = ("sparse MLA decode µs/layer @180k ctx (HBM GB/s); "
+          "indexer prefill TFLOPS @64k")
+HBM_PEAK_GBPS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+# algorithmic bytes of one C3 decode layer at B=4 (gathered 656-B rows,
+# q, o, lse, idx and the block-table entries read)
+DECODE_BYTES = 5_997_568
+DECODE_FLOPS = 4 * 64 * 2048 * (576 + 512) * 2
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--layers", type=int, default=78)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-extra", action="store_true", help="only the headline decode")
+    p.add_argument("--cpu-seconds", type=float, default=15.0)
+    return p.parse_args()
+
+
+def time_graph(torch, graph, steps, warmup):
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)  # ms
+
+
+def capture(torch, fn):
+    fn()  # eager run: first-launch attribute setup happens outside capture
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def bench_decode(torch, pkg, dev, ctx, layers, steps, warmup, seed=3):
+    S = pkg.synthetic
+    ops = pkg._sm70_ops
+    d = S.decode_inputs(B=4, H=64, ctx=ctx, topk=2048, fp8=True, device=dev, seed=seed)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 100)
+    idxs = [S.sorted_unique_positions(4, 2048, ctx, g, dev) for _ in range(layers)]
+    qs = [(torch.randn(4, 64, 576, generator=g, device=dev) / 24.0).to(torch.float16)
+          for _ in range(layers)]
+    outs = [torch.empty(4, 64, 512, dtype=torch.float16, device=dev) for _ in range(layers)]
+    lses = [torch.empty(4, 64, device=dev) for _ in range(layers)]
+
+    def run():
+        for l in range(layers):
+            ops.sm70_sparse_mla_decode(outs[l], lses[l], qs[l], d["kv"], idxs[l], d["bt"],
+                                       d["seq"], d["scale"])
+
+    graph = capture(torch, run)
+    ms = time_graph(torch, graph, steps, warmup)
+    assert all(torch.isfinite(o).all() for o in outs[:2])
+    del graph
+    return ms, d, idxs, qs
+
+
+def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
+    """Config C4 indexer: packed-Q logits over a causal 64k prefill, in the
+    caller's sub-chunks (reference/sparse_attn_indexer.py:764-881)."""
+    ops = pkg._sm70_ops
+    page = 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    npg = (T + page - 1) // page
+    kc = torch.randn(npg, page, 128, generator=g, device=dev).to(torch.float16)
+    bt_row = torch.randperm(npg, generator=g, device=dev).to(torch.int32)
+    bt = bt_row[None].expand(sub, npg).contiguous()
+    q = torch.randn(T, 32, 128, generator=g, device=dev).to(torch.float16)
+    w = (torch.randn(T, 32, generator=g, device=dev) / 32 ** 0.5).to(torch.float16)
+    score_buf = torch.empty(sub * T, device=dev)
+    chunks = []
+    for lo in range(0, T, sub):
+        n = min(sub, T - lo)
+        qs = q[lo:lo + n]
+        n16 = (n + 15) // 16 * 16
+        if n16 != n:
+            qs = torch.nn.functional.pad(qs, (0, 0, 0, 0, 0, n16 - n))
+        qp = qs.reshape(n16 // 16, 16, 32, 8, 16).permute(2, 0, 3, 1, 4).contiguous()
+        max_kv = min(npg * page, (lo + n + 63) // 64 * 64)
+        seq = torch.arange(lo + 1, lo + n + 1, dtype=torch.int32, device=dev)
+        chunks.append((qp, w[lo:lo + n].contiguous(), seq, n, max_kv))
+    del q
+
+    def run():
+        for qp, wc, seq, n, max_kv in chunks:
+            score = score_buf[: n * max_kv].view(n, max_kv)
+            ops.sm70_indexer_logits_packed(score, qp, kc, wc, bt[:n], seq)
+
+    graph = capture(torch, run)
+    ms = time_graph(torch, graph, steps, warmup) / steps
+    flops = 8192.0 * T * (T + 1) / 2
+    del graph
+    return ms, flops
+
+
+def cpu_baseline(torch, d, idxs, qs, budget_s):
+    """The oracle's PyTorch restatement (fp32) of the same decode layers on
+    the host cores: gather -> dequant -> QK -> softmax -> PV."""
+    sys.path.insert(0, ROOT)
+    from oracle import dsa_oracle as O
+
+    kv = d["kv"].cpu()
+    bt = d["bt"].cpu()
+    seq = d["seq"].cpu()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.sparse_mla(qs[n % len(qs)].cpu(), kv, idxs[n % len(idxs)].cpu(), bt, seq,
+                     d["scale"], dtype=torch.float32)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 200:
+            break
+    return el / n * 1e6, n
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures the hot path on one GPU only; multi-GPU runs are "
+              "not part of this build (see DESIGN.md for how the path shards).",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    sys.path.insert(0, ROOT)
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    pkg.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"device: {torch.cuda.get_device_name(dev)}")
+
+    # ---- headline: C3 decode at 180k ----
+    L = args.layers
+    torch.cuda.synchronize()
+    ms, d, idxs, qs = bench_decode(torch, pkg, dev, 184320, L, args.steps, args.warmup)
+    ms_per_step = ms / args.steps
+    us_layer = ms_per_step * 1000.0 / L
+    gbps = DECODE_BYTES / (us_layer * 1e-6) / 1e9
+    tflops = DECODE_FLOPS / (us_layer * 1e-6) / 1e12
+    log(f"decode C3: {us_layer:.2f} us/layer, {gbps:.0f} GB/s, {tflops:.1f} TFLOPS")
+
+    line = {
+        "metric": METRIC,
+        "value": round(us_layer, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": ("C3 sparse MLA decode: B=4 tokens, 64 heads, qk 576 / v 512, "
+                         "topk 2048, ctx 184320, fp8_ds_mla paged cache (page 64, "
+                         "11520 pages), one step = %d layers replayed from a HIP graph" % L),
+            "batch": 4, "heads": 64, "topk": 2048, "ctx": 184320, "kv": "fp8_ds_mla",
+            "layers_per_step": L,
+        },
+        "hbm_gbps": round(gbps, 1),
+        "tflops": round(tflops, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "kernel": "sparse_mla_kernel (decode config) + sparse_mla_merge_kernel",
+            "bytes_per_launch": DECODE_BYTES,
+        },
+    }
+
+    if not args.no_extra:
+        sweep = {}
+        for ctx in (4096, 16384, 65536):
+            ms_c, *_ = bench_decode(torch, pkg, dev, ctx, L, max(args.steps // 2, 3),
+                                    2, seed=7)
+            sweep[str(ctx)] = round(ms_c / max(args.steps // 2, 3) * 1000.0 / L, 3)
+            torch.cuda.empty_cache()
+        sweep["184320"] = line["value"]
+        line["ctx_sweep_us_per_layer"] = sweep
+        log(f"ctx sweep: {sweep}")
+        pms, pflops = bench_indexer_prefill(torch, pkg, dev)
+        ptf = pflops / (pms * 1e-3) / 1e12
+        line["indexer_prefill"] = {
+            "tflops": round(ptf, 2),
+            "ms": round(pms, 3),
+            "flops": pflops,
+            "frac_fp16_peak": round(ptf / FP16_PEAK_TFLOPS, 4),
+            "workload": ("65536-token causal prefill, indexer 32 heads x 128, fp16 "
+                         "K cache, 128-row sub-chunks, causal-triangle FLOPs only"),
+        }
+        log(f"indexer prefill: {ptf:.1f} TFLOPS ({pms:.2f} ms)")
+        torch.cuda.empty_cache()
+
+    if not args.no_cpu:
+        cores = torch.get_num_threads()
+        cpu_us, n = cpu_baseline(torch, d, idxs, qs, args.cpu_seconds)
+        line["cpu_baseline"] = {
+            "value": round(cpu_us, 1),
+            "unit": "us/layer",
+            "cores": cores,
+            "kind": "port",
+            "sample": (f"{n} C3 decode layers (B=4, 64 heads, topk 2048, fp8_ds_mla) "
+                       "through the oracle's fp32 PyTorch restatement on the host CPU"),
+        }
+        log(f"cpu baseline: {cpu_us:.0f} us/layer on {cores} threads ({n} layers)")
+
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

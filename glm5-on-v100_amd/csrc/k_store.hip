@@ -53,13 +53,12 @@ __global__ void __launch_bounds__(256) k_store_fp8_kernel(
     row = slot[t];
     raw = k[t * 16 + sub];
   }
+  // Whole-vector bit_cast: hipcc (ROCm 7.2) lowers a bit_cast of a single
+  // vector element inside an unrolled loop to a load of element 0 only.
+  const f16x8 h8 = __builtin_bit_cast(f16x8, raw);
   float v[8];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const f16x2 h = __builtin_bit_cast(f16x2, raw[i]);
-    v[2 * i] = (float)h[0];
-    v[2 * i + 1] = (float)h[1];
-  }
+  for (int i = 0; i < 8; i++) v[i] = (float)h8[i];
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));

@@ -92,9 +92,8 @@ def indexer_decode_inputs(B=4, ctx=65536, page=64, dup_frac=0.01, seed=2, device
     k = torch.randn(pool * page, 128, generator=g, device=device).to(torch.float16)
     ndup = int(dup_frac * pool * page)
     if ndup:
-        src = torch.randint(0, pool * page, (ndup,), generator=g, device=device)
-        dst = torch.randint(0, pool * page, (ndup,), generator=g, device=device)
-        k[dst] = k[src]
+        perm = torch.randperm(pool * page, generator=g, device=device)
+        k[perm[ndup:2 * ndup]] = k[perm[:ndup]]  # disjoint source / target rows
     bt = paged_block_table(B, bps, pool, g, device)
     q = torch.randn(B, 32, 128, generator=g, device=device).to(torch.float16)
     w = (torch.randn(B, 32, generator=g, device=device) / 32 ** 0.5).to(torch.float16)

@@ -69,18 +69,15 @@ def idxk_rows_fp32(k_cache: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
     """Gather indexer-K rows as fp32 (rows == -1 -> zeros).  fp16 cache:
     exact; fp8 132-B cache: e4m3 * per-row scale in fp32
     (idxk_fp8_load4, sm70_mla_decode.cu:106-115)."""
-    if k_cache.dtype == torch.float16:
-        flat = k_cache.reshape(-1, k_cache.shape[-1]).to(torch.float32)
-        d = flat.shape[1]
-    else:
-        flat_b = k_cache.reshape(-1, IDXK_FP8_ROW_BYTES)
-        vals = e4m3_decode(flat_b[:, :128].contiguous())
-        sc = flat_b[:, 128:132].contiguous().view(torch.float32)
-        flat = vals * sc
-        d = 128
-    out = torch.zeros(rows.numel(), d, dtype=torch.float32)
     ok = rows >= 0
-    out[ok] = flat[rows[ok]]
+    out = torch.zeros(rows.numel(), 128, dtype=torch.float32)
+    if not bool(ok.any()):
+        return out
+    if k_cache.dtype == torch.float16:
+        out[ok] = k_cache.reshape(-1, k_cache.shape[-1])[rows[ok]].to(torch.float32)
+    else:
+        fb = k_cache.reshape(-1, IDXK_FP8_ROW_BYTES)[rows[ok]]
+        out[ok] = e4m3_decode(fb[:, :128].contiguous()) * fb[:, 128:132].contiguous().view(torch.float32)
     return out
 
 
@@ -89,19 +86,22 @@ def latent_rows_fp16(kv_cache: torch.Tensor, rows: torch.Tensor) -> torch.Tensor
     (rows == -1 -> zeros).  fp8_ds_mla rows are dequantized as
     fp16_rn(e4m3 * tile_scale) for the 512 NoPE dims and copied for the 64
     fp16 RoPE dims (dsmla_load4, sm70_mla_decode.cu:81-100, then the fp16
-    store into the key tile at :1006-1012)."""
-    if kv_cache.dtype == torch.float16:
-        flat = kv_cache.reshape(-1, kv_cache.shape[-1])
-    else:
-        fb = kv_cache.reshape(-1, DSMLA_ROW_BYTES)
-        vals = e4m3_decode(fb[:, :512].contiguous()).view(-1, 4, 128)
-        sc = fb[:, 512:528].contiguous().view(torch.float32).view(-1, 4, 1)
-        nope = (vals * sc).reshape(-1, 512).to(torch.float16)
-        rope = fb[:, 528:656].contiguous().view(torch.float16)
-        flat = torch.cat([nope, rope], dim=1)
-    out = torch.zeros(rows.numel(), flat.shape[1], dtype=torch.float16)
+    store into the key tile at :1006-1012).  Only the gathered rows are
+    decoded."""
     ok = rows >= 0
-    out[ok] = flat[rows[ok]]
+    width = 576
+    out = torch.zeros(rows.numel(), width, dtype=torch.float16)
+    if not bool(ok.any()):
+        return out
+    if kv_cache.dtype == torch.float16:
+        out[ok] = kv_cache.reshape(-1, kv_cache.shape[-1])[rows[ok]]
+        return out
+    fb = kv_cache.reshape(-1, DSMLA_ROW_BYTES)[rows[ok]]
+    vals = e4m3_decode(fb[:, :512].contiguous()).view(-1, 4, 128)
+    sc = fb[:, 512:528].contiguous().view(torch.float32).view(-1, 4, 1)
+    nope = (vals * sc).reshape(-1, 512).to(torch.float16)
+    rope = fb[:, 528:656].contiguous().view(torch.float16)
+    out[ok] = torch.cat([nope, rope], dim=1)
     return out
 
 

@@ -70,8 +70,8 @@ def test_duplicate_keys_score_identically(ops, dev):
     g = torch.Generator().manual_seed(11)
     page, nblk = 64, 32
     k = torch.randn(nblk * page, 128, generator=g).to(torch.float16)
-    src = torch.randint(0, nblk * page, (300,), generator=g)
-    dst = torch.randint(0, nblk * page, (300,), generator=g)
+    perm = torch.randperm(nblk * page, generator=g)
+    src, dst = perm[:300], perm[300:600]  # disjoint: every copy is exact
     k[dst] = k[src]
     q = torch.randn(1, 32, 128, generator=g).to(torch.float16)
     w = torch.randn(1, 32, generator=g).to(torch.float16)
