@@ -149,6 +149,103 @@ def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
     return ms, flops
 
 
+def graph_time_per_call(torch, fn, n_calls, steps=10, warmup=2):
+    """Captures fn (n_calls launches) in a graph; returns microseconds per call."""
+    graph = capture(torch, fn)
+    ms = time_graph(torch, graph, steps, warmup)
+    del graph
+    return ms * 1000.0 / (steps * n_calls)
+
+
+def bench_indexer_decode(torch, pkg, dev, copies=5):
+    """Config C2: indexer logits (fused histogram) + decode top-k, B=4 x 64k
+    keys, fp16 indexer-K cache; `copies` distinct caches (> 256 MB MALL)."""
+    ops = pkg._sm70_ops
+    ins = [pkg.synthetic.indexer_decode_inputs(device=dev, seed=20 + i) for i in range(copies)]
+    B, max_kv = 4, ins[0]["max_kv"]
+    score = torch.empty(B, max_kv, device=dev)
+    hist = torch.zeros(B, 4096, dtype=torch.int32, device=dev)
+    idx = torch.empty(B, 2048, dtype=torch.int32, device=dev)
+
+    def logits_only():
+        for d in ins:
+            ops.sm70_indexer_logits(score, d["q"], d["kc"], d["w"], d["bt"], d["seq"], None)
+
+    def full():
+        for d in ins:
+            hist.zero_()
+            ops.sm70_indexer_logits(score, d["q"], d["kc"], d["w"], d["bt"], d["seq"], hist)
+            ops.sm70_decode_topk(idx, score, d["seq"], hist, 2048)
+
+    us_logits = graph_time_per_call(torch, logits_only, copies)
+    us_full = graph_time_per_call(torch, full, copies)
+    nbytes = 4 * 65536 * 256 + 4 * 65536 * 4 + 4 * 4096 * 4 + 4 * (32 * 128 + 32) * 2
+    return {
+        "logits_us": round(us_logits, 2),
+        "logits_gbps": round(nbytes / (us_logits * 1e-6) / 1e9, 1),
+        "logits_frac_hbm": round(nbytes / (us_logits * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        "logits_plus_topk_us": round(us_full, 2),
+        "workload": "C2: B=4, 65536 keys each, 32 heads x 128, fp16 indexer-K, top-2048",
+    }
+
+
+def bench_gemv(torch, pkg, dev):
+    """Config C5a: fp8 weight-only GEMV at the three projection shapes, M=1
+    and 4, rotating weight copies past the 256 MB MALL."""
+    ops = pkg._sm70_ops
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    for (N, K) in ((24576, 6144), (6144, 24576), (2112, 6144)):
+        copies = max(2, (600 << 20) // (N * K))
+        ws = [torch.randint(0, 0x7E, (N, K), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+              for _ in range(copies)]
+        ss = [torch.rand((N + 127) // 128, (K + 127) // 128, generator=g, device=dev) * 1e-3
+              for _ in range(copies)]
+        for M in (1, 4):
+            x = torch.randn(M, K, generator=g, device=dev).to(torch.float16)
+            y = torch.empty(M, N, dtype=torch.float16, device=dev)
+
+            def fn():
+                for w, s in zip(ws, ss):
+                    ops.sm70_attn_fp8_gemv(y, x, w, s)
+
+            us = graph_time_per_call(torch, fn, copies)
+            nbytes = N * K + 4 * ((N + 127) // 128) * ((K + 127) // 128) + 2 * M * K + 2 * M * N
+            gbps = nbytes / (us * 1e-6) / 1e9
+            out[f"{N}x{K}_M{M}"] = {"us": round(us, 2), "gbps": round(gbps, 1),
+                                    "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
+        del ws, ss
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_k_store(torch, pkg, dev, n_tok=65536, copies=8):
+    """Config C5b: indexer-K scatter of 64k tokens into random unique slots."""
+    ops = pkg._sm70_ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    out = {}
+    for fp8 in (False, True):
+        ks = [torch.randn(n_tok, 128, generator=g, device=dev).to(torch.float16) for _ in range(copies)]
+        slots = [torch.randperm(n_tok, generator=g, device=dev).to(torch.int32) for _ in range(copies)]
+        caches = [torch.zeros(n_tok // 64, 64, 132 if fp8 else 128,
+                              dtype=torch.uint8 if fp8 else torch.float16, device=dev)
+                  for _ in range(copies)]
+
+        def fn():
+            for k, sl, c in zip(ks, slots, caches):
+                ops.sm70_indexer_k_store(c, k, sl)
+
+        us = graph_time_per_call(torch, fn, copies)
+        nbytes = n_tok * (256 + (132 if fp8 else 256) + 4)
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out["fp8" if fp8 else "fp16"] = {"us": round(us, 2), "gbps": round(gbps, 1),
+                                         "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
+        del ks, slots, caches
+    return out
+
+
 def cpu_baseline(torch, d, idxs, qs, budget_s):
     """The oracle's PyTorch restatement (fp32) of the same decode layers on
     the host cores: gather -> dequant -> QK -> softmax -> PV."""
@@ -253,6 +350,14 @@ def main():
                          "K cache, 128-row sub-chunks, causal-triangle FLOPs only"),
         }
         log(f"indexer prefill: {ptf:.1f} TFLOPS ({pms:.2f} ms)")
+        torch.cuda.empty_cache()
+        line["indexer_decode_topk"] = bench_indexer_decode(torch, pkg, dev)
+        log(f"indexer decode: {line['indexer_decode_topk']}")
+        torch.cuda.empty_cache()
+        line["fp8_gemv"] = bench_gemv(torch, pkg, dev)
+        log(f"fp8 gemv: {line['fp8_gemv']}")
+        line["k_store"] = bench_k_store(torch, pkg, dev)
+        log(f"k store: {line['k_store']}")
         torch.cuda.empty_cache()
 
     if not args.no_cpu:

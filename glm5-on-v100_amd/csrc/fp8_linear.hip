@@ -68,39 +68,50 @@ __global__ void __launch_bounds__(WAVES * 64) fp8_gemv_kernel(
   const bool xrow = c < M;
   const f16* xr = x + (int64_t)(xrow ? c : 0) * K;
 
-  for (int kb = wave; kb < KB; kb += WAVES) {
+  // One 128-wide k block: x fragment (A operand) and NB weight fragments.
+  struct Frag {
+    f16x8 a[4];
+    u32x4 b0[NB], b1[NB];
+  };
+  auto load = [&](int kb, Frag& f) {
     const int kvalid = K - kb * 128;  // multiple of 16
     const int kofs = kb * 128 + 32 * g;
-    // A operand: x[c][kofs .. kofs+31]
-    f16x8 a[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      const bool ok = xrow && (32 * g + 8 * q) < kvalid;
-      if (ok)
-        a[q] = *reinterpret_cast<const f16x8*>(xr + kofs + 8 * q);
-      else
-        a[q] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      f.a[q] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      if (xrow && (32 * g + 8 * q) < kvalid)
+        f.a[q] = *reinterpret_cast<const f16x8*>(xr + kofs + 8 * q);
     }
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       const int n = n_base + 16 * j + c;
-      u32x4 b0 = {0u, 0u, 0u, 0u}, b1 = {0u, 0u, 0u, 0u};
+      f.b0[j] = (u32x4){0u, 0u, 0u, 0u};
+      f.b1[j] = (u32x4){0u, 0u, 0u, 0u};
       if (n < N) {
         const uint8_t* wr = w + (int64_t)n * K + kofs;
-        if (32 * g < kvalid) b0 = *reinterpret_cast<const u32x4*>(wr);
-        if (32 * g + 16 < kvalid) b1 = *reinterpret_cast<const u32x4*>(wr + 16);
+        if (32 * g < kvalid) f.b0[j] = *reinterpret_cast<const u32x4*>(wr);
+        if (32 * g + 16 < kvalid) f.b1[j] = *reinterpret_cast<const u32x4*>(wr + 16);
       }
+    }
+  };
+
+  Frag cur, nxt;
+  if (wave < KB) load(wave, cur);
+  for (int kb = wave; kb < KB; kb += WAVES) {
+    if (kb + WAVES < KB) load(kb + WAVES, nxt);  // in flight during compute
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
       f32x4 t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const uint32_t d0 = (q < 2) ? b0[2 * q] : b1[2 * (q - 2)];
-        const uint32_t d1 = (q < 2) ? b0[2 * q + 1] : b1[2 * (q - 2) + 1];
+        const uint32_t d0 = (q < 2) ? cur.b0[j][2 * q] : cur.b1[j][2 * (q - 2)];
+        const uint32_t d1 = (q < 2) ? cur.b0[j][2 * q + 1] : cur.b1[j][2 * (q - 2) + 1];
         u32x4 h;
         h[0] = e4m3x2_to_f16x2_div256(spread_lo(d0));
         h[1] = e4m3x2_to_f16x2_div256(spread_hi(d0));
         h[2] = e4m3x2_to_f16x2_div256(spread_lo(d1));
         h[3] = e4m3x2_to_f16x2_div256(spread_hi(d1));
-        t = mfma16x16x32(a[q], __builtin_bit_cast(f16x8, h), t);
+        t = mfma16x16x32(cur.a[q], __builtin_bit_cast(f16x8, h), t);
       }
       // every row of this 16-row column block shares one 128x128 scale block
       const int nb_row = (n_base + 16 * j) >> 7;
@@ -110,6 +121,7 @@ __global__ void __launch_bounds__(WAVES * 64) fp8_gemv_kernel(
 #pragma unroll
       for (int r = 0; r < 4; r++) acc[j][r] += sc * t[r];
     }
+    cur = nxt;
   }
 
   // reduce the WAVES partial sums through LDS
@@ -158,9 +170,8 @@ extern "C" int mi355_dsa_attn_fp8_gemv(void* y, const void* x, const uint8_t* w,
   hipStream_t st = as_stream(stream);
   const f16* xp = reinterpret_cast<const f16*>(x);
   f16* yp = reinterpret_cast<f16*>(y);
+  // >= ~384 workgroups of 8 waves at the BASELINE shapes
   if (N >= 16384)
-    launch_gemv<4>(xp, w, s, yp, M, N, K, KB, st);
-  else if (N >= 4096)
     launch_gemv<2>(xp, w, s, yp, M, N, K, KB, st);
   else
     launch_gemv<1>(xp, w, s, yp, M, N, K, KB, st);

@@ -304,18 +304,27 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
     }
   }
 
-  // packed Q of head h for this workgroup's 4 query tiles -> LDS buffer
+  // packed Q of head h for this workgroup's 4 query tiles: 1024 16-byte
+  // chunks, 2 per thread.  The next head's chunks are loaded into registers
+  // before the current head's MFMAs and written to LDS after them, so the
+  // loads overlap compute.
   const int qt0 = q_base >> 4;
-  auto stage_q = [&](int h, int buf) {
-    // 4 tiles x 2048 halves = 1024 16-byte chunks; 512 threads x 2
-    for (int i = threadIdx.x; i < 1024; i += blockDim.x) {
-      const int tile = i >> 8;  // 256 chunks per tile
-      const int qt = qt0 + tile;
-      f16x8 v = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+  constexpr int QPER = 1024 / (kPkWaves * 64);
+  auto load_q = [&](int h, f16x8* v) {
+#pragma unroll
+    for (int u = 0; u < QPER; u++) {
+      const int i = threadIdx.x + u * kPkWaves * 64;
+      const int qt = qt0 + (i >> 8);  // 256 chunks per tile
+      v[u] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
       if (qt < n_qt)
-        v = *reinterpret_cast<const f16x8*>(
-            Qp + ((int64_t)h * n_qt + qt) * 2048 + (i & 255) * 8);
-      *reinterpret_cast<f16x8*>(&s_q[buf][i * 8]) = v;
+        v[u] = *reinterpret_cast<const f16x8*>(Qp + ((int64_t)h * n_qt + qt) * 2048 + (i & 255) * 8);
+    }
+  };
+  auto store_q = [&](const f16x8* v, int buf) {
+#pragma unroll
+    for (int u = 0; u < QPER; u++) {
+      const int i = threadIdx.x + u * kPkWaves * 64;
+      *reinterpret_cast<f16x8*>(&s_q[buf][i * 8]) = v[u];
     }
   };
 
@@ -325,11 +334,13 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
 #pragma unroll
     for (int qb = 0; qb < 4; qb++) sacc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  stage_q(0, 0);
+  f16x8 qnext[QPER];
+  load_q(0, qnext);
+  store_q(qnext, 0);
   __syncthreads();
   for (int h = 0; h < kIdxHeads; h++) {
     const int buf = h & 1;
-    if (h + 1 < kIdxHeads) stage_q(h + 1, buf ^ 1);
+    if (h + 1 < kIdxHeads) load_q(h + 1, qnext);
 #pragma unroll
     for (int qb = 0; qb < 4; qb++) {
       // B operand: query column c of tile qb, dims 32s + 8g .. +8, i.e.
@@ -354,6 +365,7 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
           sacc[kb][qb][r] += (d > 0.f ? d : 0.f) * wq;
         }
     }
+    if (h + 1 < kIdxHeads) store_q(qnext, buf ^ 1);
     __syncthreads();
   }
 

@@ -11,26 +11,39 @@
 //     key is valid (merge convention, :1175-1183).
 //
 // MFMA formulation (one wave owns 16 heads):
-//   S^T[key][head] = K[key][:] . Qs[head][:]   (v_mfma_f32_16x16x32_f16,
-//                    18 steps over the 576 dims; D: lane = head, rows = keys)
-//   O^T[dim][head] += V^T[dim][key] . P^T[key][head]  (v_mfma_f32_16x16x16_f16)
-// S^T's accumulator layout (lane c = head, rows 4g..4g+3 = keys) is exactly
-// the B-operand layout of the x16 PV step, so P never leaves registers; the
-// softmax reductions over keys are two lane shuffles.  O^T lives in 32
-// accumulator tiles (128 fp32 per lane).
+//   S^T[key][head] = K[key][:] . Qs[head][:]      v_mfma_f32_16x16x32_f16
+//   O^T[dim][head] += V^T[dim][key] . P^T[key][head]
+// S^T's accumulator layout (lane c = head, rows 4g..4g+3 = keys) is the
+// B-operand layout of the PV step, so P never leaves registers and the
+// softmax reductions over keys are two lane shuffles.  V^T operands come
+// straight from the row-major key tile with ds_read_b64_tr_b16 (in a 16-lane
+// group, lane j element k = lane (4k + j/4)'s element j%4), one LDS
+// instruction per MFMA operand.  O^T lives in 32 accumulator tiles.
 //
-// Two launch configurations of one kernel template:
-//  * decode (HW=1, KW=4): workgroup = (split, 16-head group, token); its 4
-//    waves take interleaved 16-key tiles of the split's key range, each into
-//    its own LDS tile, and are merged in LDS at the end.  Splits write
-//    unnormalised partials that sparse_mla_merge_kernel combines (the
-//    flash-decode reduction of :1138-1184).  Workgroups sharing a (token,
-//    split) differ by a multiple of 8 in launch order, so they land on the
-//    same XCD and share its L2 for the gathered rows.
-//  * prefill (HW=4, KW=1): workgroup = token x 64 heads; the 4 waves share
-//    every gathered 32-key tile (each latent row crosses HBM/MALL once per
-//    token), and consecutive tokens are mapped to the same XCD so their
-//    overlapping top-k sets hit in L2.
+// fp8_ds_mla rows: the 512 e4m3 NoPE bytes become exact fp16 values with
+// v_cvt_scalef32_pk_f16_fp8 at scale 1 (2 values per instruction) and the
+// four fp32 tile scales are applied where they are linear: QK keeps one
+// accumulator per 128-dim scale tile (plus RoPE) and combines them with the
+// row's scales, PV multiplies P by the row's tile scale (one P^T operand per
+// scale tile).  Products are therefore exact; the reference instead rounds
+// e4m3*scale to fp16 before the dot (dsmla_load4 + half store), which the
+// tolerance of the parity tests covers.
+//
+// Memory pipeline: every workgroup first resolves idx -> block table ->
+// cache row for all its keys in one batched pass (rows kept in LDS), then
+// streams key tiles with the global loads of tile t+1 held in registers
+// while tile t is computed.
+//
+// Launch configurations of one kernel template:
+//  * decode (HW=1, KW=4, NB=1): workgroup = (split, 16-head group, token);
+//    its 4 waves take interleaved 16-key tiles of the split's range, each in
+//    its own LDS tile, and are merged in LDS; splits write unnormalised
+//    partials combined by sparse_mla_merge_kernel (flash-decode reduction,
+//    :1138-1184).  Workgroups of one (token, split) differ by a multiple of 8
+//    in launch order, so they share an XCD and its L2 for the gathered rows.
+//  * prefill (HW=4, KW=1, NB=2): workgroup = token x 64 heads; 4 waves share
+//    every gathered 32-key tile; consecutive tokens map to the same XCD so
+//    their overlapping top-k sets hit in L2.
 #include <float.h>
 
 #include "capi_internal.h"
@@ -38,8 +51,12 @@
 
 namespace mi355dsa {
 
-constexpr int kPitch = kLatentDim + 8;  // LDS row pitch (halves) of Q / key tiles
+constexpr int kPitch = kLatentDim + 8;   // LDS row pitch (halves) of Q / key tiles
 constexpr int kOTiles = kValueDim / 16;  // 32 O^T accumulator tiles
+constexpr int kSegKeys = 2048;           // keys resolved per segment
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 struct MlaParams {
   const f16* q;
@@ -59,76 +76,120 @@ struct MlaParams {
 template <int HW, int KW, int NB>
 struct MlaSmem {
   static constexpr int TN = 16 * NB;  // keys per tile per key-wave group
-  f16 q[HW * 16 * kPitch];
-  f16 k[KW * TN * kPitch];
-  int64_t row[KW * TN];
+  struct Main {
+    f16 q[HW * 16 * kPitch];
+    f16 k[KW * TN * kPitch];
+    float sc[KW * TN * 4];  // fp8 tile scales of the tile's rows
+  };
+  // key-wave merge: wave w owns dims [128w, 128w+128) (8 O^T tiles) and
+  // receives the other waves' tiles of that quarter: [quarter][source][tile][lane]
+  static constexpr int XSRC = KW > 1 ? KW - 1 : 1;
+  union {
+    Main main;
+    f32x4 xbuf[KW > 1 ? KW : 1][XSRC][kOTiles / (KW > 1 ? KW : 1)][64];
+  } u;
+  int32_t rows[kSegKeys];
   float m[KW * 16];
   float l[KW * 16];
 };
 
-// Gathers one tile (TN rows) into LDS as fp16, dequantising fp8_ds_mla rows
-// as fp16_rn(e4m3 * tile_scale).  Invalid rows become zeros.
-template <bool KVFP8, int TN>
-__device__ __forceinline__ void gather_tile(const void* kv, const int64_t* rows,
-                                            f16* dst, int t0, int nthreads) {
-  if constexpr (KVFP8) {
-    constexpr int NCH = 40;  // 32 e4m3 chunks + 8 RoPE chunks of 16 bytes
-    for (int i = t0; i < TN * NCH; i += nthreads) {
-      const int r = i / NCH, ch = i - r * NCH;
-      const int64_t row = rows[r];
-      f16* d = dst + r * kPitch;
+// Per-thread register stage of one tile's global loads.  Chunks of invalid
+// rows are loaded from row 0 and zeroed only when stored to LDS (bit u of
+// `bad`), so issuing the loads never waits for them.
+template <bool KVFP8, int TN, int GT>
+struct TileStage {
+  static constexpr int NCH = KVFP8 ? 41 : kLatentDim / 8;  // 16-B chunks per row
+  static constexpr int PER = (TN * NCH + GT - 1) / GT;
+  u32x4 v[PER];
+  uint32_t bad;
+};
+
+// Writes the staged chunks into the LDS key tile (and fp8 scales).
+template <bool KVFP8, int TN, int GT>
+__device__ __forceinline__ void tile_store(const TileStage<KVFP8, TN, GT>& st, f16* ktile,
+                                           float* sc, int t0) {
+  constexpr int NCH = TileStage<KVFP8, TN, GT>::NCH;
+  constexpr int PER = TileStage<KVFP8, TN, GT>::PER;
+#pragma unroll
+  for (int u = 0; u < PER; u++) {
+    const int i = t0 + u * GT;
+    if (i >= TN * NCH) continue;
+    const int r = i / NCH, ch = i - r * NCH;
+    f16* d = ktile + r * kPitch;
+    const u32x4 val = ((st.bad >> u) & 1u) ? (u32x4){0u, 0u, 0u, 0u} : st.v[u];
+    if constexpr (KVFP8) {
       if (ch < 32) {
-        f16x8 h0 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0}, h1 = h0;
-        if (row >= 0) {
-          const uint8_t* rp = reinterpret_cast<const uint8_t*>(kv) + row * (int64_t)kDsmlaRowBytes;
-          const u32x4 raw = *reinterpret_cast<const u32x4*>(rp + 16 * ch);
-          const float sc = *reinterpret_cast<const float*>(rp + 512 + 4 * (ch >> 3)) * 256.0f;
+        // 16 e4m3 bytes -> 16 exact fp16 values (dims 16ch .. 16ch+15)
+        u32x4 h0, h1;
 #pragma unroll
-          for (int w = 0; w < 4; w++) {
-            float v[4];
-            e4m3x4_to_f32_div256(raw[w], v);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-              const f16 h = (f16)(v[e] * sc);
-              if (w < 2) h0[4 * w + e] = h; else h1[4 * (w - 2) + e] = h;
-            }
+        for (int w = 0; w < 4; w++) {
+          const f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)val[w], 1.0f, false);
+          const f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)val[w], 1.0f, true);
+          const uint32_t a = __builtin_bit_cast(uint32_t, lo);
+          const uint32_t b = __builtin_bit_cast(uint32_t, hi);
+          if (w < 2) {
+            h0[2 * w] = a;
+            h0[2 * w + 1] = b;
+          } else {
+            h1[2 * (w - 2)] = a;
+            h1[2 * (w - 2) + 1] = b;
           }
         }
-        *reinterpret_cast<f16x8*>(d + 16 * ch) = h0;
-        *reinterpret_cast<f16x8*>(d + 16 * ch + 8) = h1;
+        *reinterpret_cast<u32x4*>(d + 16 * ch) = h0;
+        *reinterpret_cast<u32x4*>(d + 16 * ch + 8) = h1;
+      } else if (ch == 32) {
+        *reinterpret_cast<u32x4*>(sc + 4 * r) = val;  // 4 fp32 tile scales
       } else {
-        const int cc = ch - 32;
-        u32x4 raw = {0u, 0u, 0u, 0u};
-        if (row >= 0)
-          raw = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(kv) +
-                                               row * (int64_t)kDsmlaRowBytes + 528 + 16 * cc);
-        *reinterpret_cast<u32x4*>(d + 512 + 8 * cc) = raw;
+        *reinterpret_cast<u32x4*>(d + 512 + 8 * (ch - 33)) = val;  // RoPE fp16
       }
-    }
-  } else {
-    constexpr int NCH = kLatentDim / 8;  // 72 chunks of 16 bytes
-    for (int i = t0; i < TN * NCH; i += nthreads) {
-      const int r = i / NCH, ch = i - r * NCH;
-      const int64_t row = rows[r];
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (row >= 0)
-        raw = *reinterpret_cast<const u32x4*>(reinterpret_cast<const f16*>(kv) +
-                                             row * kLatentDim + 8 * ch);
-      *reinterpret_cast<u32x4*>(dst + r * kPitch + 8 * ch) = raw;
+    } else {
+      *reinterpret_cast<u32x4*>(d + 8 * ch) = val;
     }
   }
 }
 
-// Resolves the cache row of top-k slot j of token b (-1 if not used).
-__device__ __forceinline__ int64_t resolve_row(const MlaParams& p, int b, int j, int seq_len) {
-  if (j >= p.topk) return -1;
-  const int pos = p.idx[(int64_t)b * p.topk + j];
-  if (pos < 0 || pos >= seq_len) return -1;
-  const int pg = pos / p.page_size;
-  if (pg >= p.max_blocks) return -1;
-  const int blk = p.bt[(int64_t)b * p.max_blocks + pg];
-  const int64_t row = (int64_t)blk * p.page_size + (pos - pg * p.page_size);
-  return (blk < 0 || row >= p.n_kv_rows) ? -1 : row;
+// Resolves idx -> block table -> cache row for keys [j0, j0+n) of token b
+// into rows[0..n).  Work is done in batches of NT*8 keys; each batch issues
+// its eight idx loads per thread together, then the eight block-table loads.
+// resolve_idx / resolve_finish split one batch so that independent work (Q
+// staging) can run while the idx loads are in flight.
+constexpr int kResU = 8;
+
+template <int NT>
+__device__ __forceinline__ void resolve_idx(const MlaParams& p, int b, int j0, int n, int base,
+                                            int pos[kResU]) {
+  const int32_t* idx_row = p.idx + (int64_t)b * p.topk + j0;
+#pragma unroll
+  for (int u = 0; u < kResU; u++) {
+    const int j = base + u * NT + (int)threadIdx.x;
+    pos[u] = (j < n) ? idx_row[j] : -1;
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void resolve_bt(const MlaParams& p, int b, int seq_len,
+                                           const int pos[kResU], int pg[kResU], int blk[kResU]) {
+  const int32_t* bt_row = p.bt + (int64_t)b * p.max_blocks;
+#pragma unroll
+  for (int u = 0; u < kResU; u++) {
+    pg[u] = (pos[u] >= 0) ? pos[u] / p.page_size : 0;
+    const bool ok = pos[u] >= 0 && pos[u] < seq_len && pg[u] < p.max_blocks;
+    blk[u] = ok ? bt_row[pg[u]] : -1;
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void resolve_store(const MlaParams& p, int n, int base,
+                                              const int pos[kResU], const int pg[kResU],
+                                              const int blk[kResU], int32_t* rows) {
+#pragma unroll
+  for (int u = 0; u < kResU; u++) {
+    const int j = base + u * NT + (int)threadIdx.x;
+    if (j < n) {
+      const int64_t row = (int64_t)blk[u] * p.page_size + (pos[u] - pg[u] * p.page_size);
+      rows[j] = (blk[u] < 0 || row >= p.n_kv_rows) ? -1 : (int32_t)row;
+    }
+  }
 }
 
 template <bool KVFP8, int HW, int KW, int NB>
@@ -136,6 +197,8 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
   using Smem = MlaSmem<HW, KW, NB>;
   constexpr int TN = Smem::TN;
   constexpr int NT = HW * KW * 64;
+  constexpr int GT = HW * 64;  // gather team = the HW waves of a key-wave group
+  constexpr int NACC = KVFP8 ? 5 : 1;  // QK accumulators: 4 scale tiles + RoPE
   extern __shared__ __align__(16) unsigned char smem_raw[];
   Smem& sh = *reinterpret_cast<Smem*>(smem_raw);
 
@@ -161,118 +224,230 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
   }
   const int seq_len = p.seq_lens[b];
 
-  // ---- scaled Q of this workgroup's heads into LDS, then registers ----
+  // ---- this workgroup's key range (tiles of TN) ----
+  const int n_tiles_all = (p.topk + TN - 1) / TN;
+  const int tps = (n_tiles_all + p.n_splits - 1) / p.n_splits;  // tiles per split
+  const int tile_lo = split * tps;
+  const int tile_hi = min(tile_lo + tps, n_tiles_all);
+  constexpr int SEG_TILES = kSegKeys / TN;
+
+  // first index batch in flight while Q is staged
+  int pos0[kResU];
+  const int nkeys0 = tile_lo < tile_hi ? min(min(tile_lo + SEG_TILES, tile_hi) * TN, p.topk) - tile_lo * TN : 0;
+  resolve_idx<NT>(p, b, tile_lo * TN, nkeys0, 0, pos0);
+
+  // ---- scaled Q of this workgroup's heads into LDS; the block-table loads
+  // of the first index batch are issued between the Q loads and the Q
+  // stores so both latencies overlap ----
+  int pg0[kResU], blk0[kResU];
   {
+    constexpr int QCH = HW * 16 * (kLatentDim / 8);
+    constexpr int QPER = (QCH + NT - 1) / NT;
     const f16* qb = p.q + ((int64_t)b * p.n_head) * kLatentDim;
-    for (int i = threadIdx.x; i < HW * 16 * (kLatentDim / 8); i += NT) {
-      const int hh = i / (kLatentDim / 8), ch = i - hh * (kLatentDim / 8);
-      const int h = h0 + hh;
-      f16x8 v = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-      if (h < p.n_head) {
-        const f16x8 raw = *reinterpret_cast<const f16x8*>(qb + (int64_t)h * kLatentDim + 8 * ch);
+    f16x8 raw[QPER];
 #pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = (f16)((float)raw[e] * p.scale_h);
+    for (int u = 0; u < QPER; u++) {
+      const int i = threadIdx.x + u * NT;
+      const int hh = i / (kLatentDim / 8), ch = i - hh * (kLatentDim / 8);
+      raw[u] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      if (i < QCH && h0 + hh < p.n_head)
+        raw[u] = *reinterpret_cast<const f16x8*>(qb + (int64_t)(h0 + hh) * kLatentDim + 8 * ch);
+    }
+    resolve_bt<NT>(p, b, seq_len, pos0, pg0, blk0);
+#pragma unroll
+    for (int u = 0; u < QPER; u++) {
+      const int i = threadIdx.x + u * NT;
+      if (i < QCH) {
+        const int hh = i / (kLatentDim / 8), ch = i - hh * (kLatentDim / 8);
+        f16x8 v;
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (f16)((float)raw[u][e] * p.scale_h);
+        *reinterpret_cast<f16x8*>(&sh.u.main.q[hh * kPitch + 8 * ch]) = v;
       }
-      *reinterpret_cast<f16x8*>(&sh.q[hh * kPitch + 8 * ch]) = v;
     }
   }
-  __syncthreads();
-  // B operand of S^T: head column c of this wave, dims 32s + 8g .. +8
-  f16x8 qreg[kLatentDim / 32];
-#pragma unroll
-  for (int s = 0; s < kLatentDim / 32; s++)
-    qreg[s] = *reinterpret_cast<const f16x8*>(&sh.q[(16 * hw + c) * kPitch + 32 * s + 8 * g]);
 
   f32x4 oacc[kOTiles];
 #pragma unroll
   for (int t = 0; t < kOTiles; t++) oacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
   float m_run = -1e30f, l_run = 0.f;
 
-  // ---- key tiles of this workgroup ----
-  const int n_tiles_all = (p.topk + TN - 1) / TN;
-  const int tps = (n_tiles_all + p.n_splits - 1) / p.n_splits;  // tiles per split
-  const int tile_lo = split * tps;
-  const int tile_hi = min(tile_lo + tps, n_tiles_all);
-  const int rounds = (max(tile_hi - tile_lo, 0) + KW - 1) / KW;
+  f16* ktile = &sh.u.main.k[kw * TN * kPitch];
+  float* ksc = &sh.u.main.sc[kw * TN * 4];
+  const int gt = threadIdx.x - kw * GT;  // thread index inside the gather team
+  const f16* qrow = &sh.u.main.q[(16 * hw + c) * kPitch + 8 * g];
 
-  f16* ktile = &sh.k[kw * TN * kPitch];
-  int64_t* krow = &sh.row[kw * TN];
-  const int gt = threadIdx.x - kw * HW * 64;  // thread index inside the key-wave group
-
-  for (int rd = 0; rd < rounds; rd++) {
-    const int tile = tile_lo + rd * KW + kw;
-    const bool have = tile < tile_hi;
-    for (int r = gt; r < TN; r += HW * 64)
-      krow[r] = have ? resolve_row(p, b, tile * TN + r, seq_len) : -1;
-    __syncthreads();
-    gather_tile<KVFP8, TN>(p.kv, krow, ktile, gt, HW * 64);
-    __syncthreads();
-
-    // S^T blocks
-    f32x4 sacc[NB];
-    bool valid[NB][4];
-    float mt = -INFINITY;
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      const f16* krows = ktile + (16 * nb + c) * kPitch + 8 * g;
-#pragma unroll
-      for (int s = 0; s < kLatentDim / 32; s++)
-        acc = mfma16x16x32(*reinterpret_cast<const f16x8*>(krows + 32 * s), qreg[s], acc);
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        valid[nb][r] = krow[16 * nb + 4 * g + r] >= 0;
-        acc[r] = valid[nb][r] ? acc[r] : -INFINITY;
-        mt = fmaxf(mt, acc[r]);
+  for (int seg_lo = tile_lo; seg_lo < tile_hi; seg_lo += SEG_TILES) {
+    const int seg_hi = min(seg_lo + SEG_TILES, tile_hi);
+    const int j0 = seg_lo * TN;
+    const int nkeys = min(seg_hi * TN, p.topk) - j0;
+    __syncthreads();  // previous segment done with sh.rows
+    for (int base = 0; base < nkeys; base += NT * kResU) {
+      if (seg_lo == tile_lo && base == 0) {
+        resolve_store<NT>(p, nkeys, base, pos0, pg0, blk0, sh.rows);
+      } else {
+        int pos[kResU], pg[kResU], blk[kResU];
+        resolve_idx<NT>(p, b, j0, nkeys, base, pos);
+        resolve_bt<NT>(p, b, seq_len, pos, pg, blk);
+        resolve_store<NT>(p, nkeys, base, pos, pg, blk, sh.rows);
       }
-      sacc[nb] = acc;
     }
-    mt = fmaxf(mt, shfl_xor_f(mt, 16));
-    mt = fmaxf(mt, shfl_xor_f(mt, 32));
-    const float m_new = fmaxf(m_run, mt);
-    const float alpha = expf(m_run - m_new);
-    float ls = 0.f;
-    f16x4 pb[NB];
+    __syncthreads();
+    const int rounds = (seg_hi - seg_lo + KW - 1) / KW;
+    // The tile of round rd for this key-wave group is seg_lo + rd*KW + kw;
+    // its rows start at sh.rows[(rd*KW + kw) * TN].  Keys past the segment
+    // (or past nkeys) read as row -1.
+    auto tile_valid = [&](int rd) { return seg_lo + rd * KW + kw < seg_hi; };
+    TileStage<KVFP8, TN, GT> stage;
+    auto row_of = [&](int rd, int r) -> int {
+      const int kidx = (rd * KW + kw) * TN + r;
+      const int v = sh.rows[kidx < nkeys ? kidx : 0];  // unconditional LDS read
+      return (tile_valid(rd) && kidx < nkeys) ? v : -1;
+    };
+    // global loads of round rd's tile into the register stage
+    auto issue = [&](int rd) {
+      constexpr int NCH = TileStage<KVFP8, TN, GT>::NCH;
+      constexpr int PER = TileStage<KVFP8, TN, GT>::PER;
+      constexpr int RB = KVFP8 ? kDsmlaRowBytes : kLatentDim * 2;
+      int rowu[PER];
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const float pr = valid[nb][r] ? expf(sacc[nb][r] - m_new) : 0.f;
-        ls += pr;
-        pb[nb][r] = (f16)pr;
+      for (int u = 0; u < PER; u++) {
+        const int i = gt + u * GT;
+        const int r = i / NCH;
+        rowu[u] = (i < TN * NCH && p.n_kv_rows > 0) ? row_of(rd, r < TN ? r : 0) : -1;
       }
-    ls += shfl_xor_f(ls, 16);
-    ls += shfl_xor_f(ls, 32);
-    l_run = l_run * alpha + ls;
-    m_run = m_new;
-    if (__any(alpha != 1.0f)) {
+      // Every lane loads (row 0 stands in for an invalid row, so no branch
+      // guards the load) and invalid rows are zeroed afterwards: masked keys
+      // then carry finite zeros whatever the cache holds in unused pages.
+      if (p.n_kv_rows > 0) {  // uniform: an empty cache is never read
 #pragma unroll
-      for (int t = 0; t < kOTiles; t++)
+        for (int u = 0; u < PER; u++) {
+          const int i = gt + u * GT;
+          const int ch = i - (i / NCH) * NCH;
+          const int row = rowu[u] >= 0 ? rowu[u] : 0;
+          stage.v[u] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(p.kv) +
+                                                      (int64_t)row * RB + 16 * ch);
+        }
+      }
+      stage.bad = 0u;
 #pragma unroll
-        for (int r = 0; r < 4; r++) oacc[t][r] *= alpha;
-    }
-    // O^T += V^T P^T
+      for (int u = 0; u < PER; u++) stage.bad |= (rowu[u] < 0 ? 1u : 0u) << u;
+    };
+    issue(0);
+    for (int rd = 0; rd < rounds; rd++) {
+      tile_store<KVFP8, TN, GT>(stage, ktile, ksc, gt);
+      // validity of this tile's keys (before the rows array can change)
+      bool valid[NB][4];
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++) {
-      const f16* vk = ktile + (16 * nb + 4 * g) * kPitch + c;
+      for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) valid[nb][r] = row_of(rd, 16 * nb + 4 * g + r) >= 0;
+      if (rd + 1 < rounds) issue(rd + 1);
+      __syncthreads();
+
+      // ---- S^T blocks ----
+      f32x4 sacc[NB];
+      float mt = -INFINITY;
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) {
+        f32x4 acc[NACC];
+#pragma unroll
+        for (int a = 0; a < NACC; a++) acc[a] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        const f16* krow = ktile + (16 * nb + c) * kPitch + 8 * g;
+#pragma unroll
+        for (int s = 0; s < kLatentDim / 32; s++) {
+          const int a = KVFP8 ? (s < 16 ? s / 4 : 4) : 0;
+          acc[a] = mfma16x16x32(*reinterpret_cast<const f16x8*>(krow + 32 * s),
+                                *reinterpret_cast<const f16x8*>(qrow + 32 * s), acc[a]);
+        }
+        f32x4 sv;
+        if constexpr (KVFP8) {
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const f32x4 s4 = *reinterpret_cast<const f32x4*>(&ksc[4 * (16 * nb + 4 * g + r)]);
+            sv[r] = acc[4][r] + s4[0] * acc[0][r] + s4[1] * acc[1][r] + s4[2] * acc[2][r] +
+                    s4[3] * acc[3][r];
+          }
+        } else {
+          sv = acc[0];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          sv[r] = valid[nb][r] ? sv[r] : -INFINITY;
+          mt = fmaxf(mt, sv[r]);
+        }
+        sacc[nb] = sv;
+      }
+      mt = fmaxf(mt, shfl_xor_f(mt, 16));
+      mt = fmaxf(mt, shfl_xor_f(mt, 32));
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = expf(m_run - m_new);
+      float ls = 0.f;
+      float pr[NB][4];
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          pr[nb][r] = valid[nb][r] ? expf(sacc[nb][r] - m_new) : 0.f;
+          ls += pr[nb][r];
+        }
+      ls += shfl_xor_f(ls, 16);
+      ls += shfl_xor_f(ls, 32);
+      l_run = l_run * alpha + ls;
+      m_run = m_new;
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int t = 0; t < kOTiles; t++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) oacc[t][r] *= alpha;
+      }
+
+      // ---- O^T += V^T P^T ----
+      // P^T operands, one per fp8 scale tile (dims 128*st .. 128*st+127)
+      constexpr int NST = KVFP8 ? 4 : 1;
+      f16x4 pb[NST][NB];
+#pragma unroll
+      for (int st = 0; st < NST; st++)
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            float v = pr[nb][r];
+            if constexpr (KVFP8) v *= ksc[4 * (16 * nb + 4 * g + r) + st];
+            pb[st][nb][r] = (f16)v;
+          }
+      // transpose-read source: lane i of its 16-lane group supplies row
+      // (4g + i/4) (+16 per block), dims 16t + 4(i%4) .. +3
+      const f16* vsrc = ktile + (4 * g + (c >> 2)) * kPitch + 4 * (c & 3);
 #pragma unroll
       for (int t = 0; t < kOTiles; t++) {
-        f16x4 a;
-#pragma unroll
-        for (int e = 0; e < 4; e++) a[e] = vk[e * kPitch + 16 * t];
-        oacc[t] = mfma16x16x16(a, pb[nb], oacc[t]);
+        const int st = KVFP8 ? t / 8 : 0;
+        if constexpr (NB == 1) {
+          const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)(vsrc + 16 * t));
+          oacc[t] = mfma16x16x16(__builtin_bit_cast(f16x4, a), pb[st][0], oacc[t]);
+        } else {
+          const s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)(vsrc + 16 * t));
+          const s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)(vsrc + 16 * kPitch + 16 * t));
+          const f16x4 x0 = __builtin_bit_cast(f16x4, a0), x1 = __builtin_bit_cast(f16x4, a1);
+          const f16x8 av = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+          const f16x8 bv = {pb[st][0][0], pb[st][0][1], pb[st][0][2], pb[st][0][3],
+                            pb[st][1][0], pb[st][1][1], pb[st][1][2], pb[st][1][3]};
+          oacc[t] = mfma16x16x32(av, bv, oacc[t]);
+        }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
 
   // ---- finalize ----
   if constexpr (KW == 1) {
     const int h = h0 + 16 * hw + c;
-    if (h < p.n_head && g == 0) {
-      p.lse[(int64_t)b * p.n_head + h] = (l_run > 0.f) ? (m_run + logf(l_run)) : -INFINITY;
-    }
     if (h < p.n_head) {
+      if (g == 0)
+        p.lse[(int64_t)b * p.n_head + h] = (l_run > 0.f) ? (m_run + logf(l_run)) : -INFINITY;
       const float inv = (l_run > 0.f) ? 1.f / l_run : 0.f;
       f16* orow = p.o + ((int64_t)b * p.n_head + h) * kValueDim;
 #pragma unroll
@@ -284,7 +459,13 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
       }
     }
   } else {
-    // merge the KW key-waves in LDS (HW == 1: every wave holds the same 16 heads)
+    // Merge the KW key-waves (HW == 1: all waves hold the same 16 heads).
+    // Wave w owns O^T tiles [8w, 8w+8) (dims 128w .. 128w+127): every wave
+    // scales its accumulators by exp(m_w - M), writes the tiles of the other
+    // quarters to LDS, then adds the three received copies of its own
+    // quarter and stores it straight from registers.
+    constexpr int QT = kOTiles / KW;  // tiles per quarter
+    __syncthreads();
     if (g == 0) {
       sh.m[kw * 16 + c] = m_run;
       sh.l[kw * 16 + c] = l_run;
@@ -300,80 +481,91 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
       L += (lk > 0.f) ? lk * expf(sh.m[k2 * 16 + c] - M) : 0.f;
     }
     const float wgt = (l_run > 0.f) ? expf(m_run - M) : 0.f;
-    float* acc = reinterpret_cast<float*>(sh.k);  // [16 heads][512] fp32 (32 KB)
-    for (int k2 = 0; k2 < KW; k2++) {
-      if (kw == k2) {
 #pragma unroll
-        for (int t = 0; t < kOTiles; t++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            float* dst = &acc[c * kValueDim + 16 * t + 4 * g + r];
-            const float v = oacc[t][r] * wgt;
-            *dst = (k2 == 0) ? v : (*dst + v);
-          }
+    for (int t = 0; t < kOTiles; t++) {
+      const int qd = t / QT;
+      if (qd != kw) {
+        const int slot = kw < qd ? kw : kw - 1;
+        sh.u.xbuf[qd][slot][t % QT][lane] = oacc[t] * wgt;
       }
-      __syncthreads();
     }
-    // write out: thread -> (head, 4 dims)
+    __syncthreads();
     const bool final_out = (p.n_splits == 1);
-    for (int i = threadIdx.x; i < 16 * (kValueDim / 4); i += NT) {
-      const int hh = i / (kValueDim / 4), d4 = i - hh * (kValueDim / 4);
-      const int h = h0 + hh;
-      if (h >= p.n_head) continue;
-      const float Mh = [&] {
-        float mm = -1e30f;
-        for (int k2 = 0; k2 < KW; k2++) mm = fmaxf(mm, sh.m[k2 * 16 + hh]);
-        return mm;
-      }();
-      float Lh = 0.f;
-      for (int k2 = 0; k2 < KW; k2++) {
-        const float lk = sh.l[k2 * 16 + hh];
-        Lh += (lk > 0.f) ? lk * expf(sh.m[k2 * 16 + hh] - Mh) : 0.f;
-      }
-      const f32x4 v = *reinterpret_cast<const f32x4*>(&acc[hh * kValueDim + 4 * d4]);
-      const int64_t bh = (int64_t)b * p.n_head + h;
-      if (final_out) {
-        const float inv = (Lh > 0.f) ? 1.f / Lh : 0.f;
-        f16x4 o4;
+    const int h = h0 + c;
+    const int64_t bh = (int64_t)b * p.n_head + h;
+    const float inv = (L > 0.f) ? 1.f / L : 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; r++) o4[r] = (f16)(v[r] * inv);
-        *reinterpret_cast<f16x4*>(p.o + bh * kValueDim + 4 * d4) = o4;
-        if (d4 == 0) p.lse[bh] = (Lh > 0.f) ? (Mh + logf(Lh)) : -INFINITY;
-      } else {
-        const int64_t ps = bh * p.n_splits + split;
-        *reinterpret_cast<f32x4*>(p.part_o + ps * kValueDim + 4 * d4) = v;
-        if (d4 == 0) {
-          p.part_ml[ps * 2 + 0] = Mh;
-          p.part_ml[ps * 2 + 1] = Lh;
+    for (int t = 0; t < kOTiles; t++) {
+      if (t / QT == kw) {
+        f32x4 v = oacc[t] * wgt;
+#pragma unroll
+        for (int sl = 0; sl < KW - 1; sl++) v += sh.u.xbuf[kw][sl][t % QT][lane];
+        if (h < p.n_head) {
+          if (final_out) {
+            f16x4 o4;
+#pragma unroll
+            for (int r = 0; r < 4; r++) o4[r] = (f16)(v[r] * inv);
+            *reinterpret_cast<f16x4*>(p.o + bh * kValueDim + 16 * t + 4 * g) = o4;
+          } else {
+            const int64_t ps = bh * p.n_splits + split;
+            *reinterpret_cast<f32x4*>(p.part_o + ps * kValueDim + 16 * t + 4 * g) = v;
+          }
         }
       }
     }
-    (void)L;
+    if (kw == 0 && g == 0 && h < p.n_head) {
+      if (final_out) {
+        p.lse[bh] = (L > 0.f) ? (M + logf(L)) : -INFINITY;
+      } else {
+        const int64_t ps = bh * p.n_splits + split;
+        p.part_ml[ps * 2 + 0] = M;
+        p.part_ml[ps * 2 + 1] = L;
+      }
+    }
   }
 }
 
 // Flash-decode merge of S partial states (reference :1138-1184):
 // m = max_s m_s, w_s = l_s > 0 ? exp(m_s - m) : 0, o = sum w_s P_O_s / sum w_s l_s.
-// One workgroup per (token, head), 128 threads x 4 dims.
+// One workgroup per (token, head), 128 threads x 4 dims.  Splits are taken
+// 16 at a time with every (m, l) pair and partial row of the batch loaded
+// together (one memory latency per batch), combined online across batches.
+constexpr int kMergeMaxSplits = 128;
+constexpr int kMergeBatch = 16;
+
 __global__ void __launch_bounds__(128) sparse_mla_merge_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     f16* __restrict__ O, float* __restrict__ LSE, int n_splits) {
   const int64_t bh = blockIdx.x;
-  const float* ml = part_ml + bh * n_splits * 2;
-  float m = -1e30f;
-  for (int s = 0; s < n_splits; s++) m = fmaxf(m, ml[2 * s]);
-  float l = 0.f;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int d = 4 * threadIdx.x;
-  for (int s = 0; s < n_splits; s++) {
-    const float ls = ml[2 * s + 1];
-    if (ls > 0.f) {
-      const float w = expf(ml[2 * s] - m);
-      l += ls * w;
-      const f32x4 v = *reinterpret_cast<const f32x4*>(part_o + (bh * n_splits + s) * kValueDim + d);
+  const f32x2* ml = reinterpret_cast<const f32x2*>(part_ml + bh * n_splits * 2);
+  const float* po = part_o + bh * n_splits * kValueDim + d;
+  float m = -1e30f, l = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
+    f32x2 mlv[kMergeBatch];
+    f32x4 v[kMergeBatch];
 #pragma unroll
-      for (int r = 0; r < 4; r++) acc[r] += v[r] * w;
+    for (int u = 0; u < kMergeBatch; u++) {
+      const int s = s0 + u;
+      mlv[u] = (s < n_splits) ? ml[s] : (f32x2){-1e30f, 0.f};
+      v[u] = (s < n_splits) ? *reinterpret_cast<const f32x4*>(po + (int64_t)s * kValueDim)
+                            : (f32x4){0.f, 0.f, 0.f, 0.f};
     }
+    float mb = m;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; u++)
+      if (mlv[u][1] > 0.f) mb = fmaxf(mb, mlv[u][0]);
+    const float resc = (l > 0.f) ? expf(m - mb) : 0.f;
+    l *= resc;
+    acc *= resc;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; u++) {
+      const float w = (mlv[u][1] > 0.f) ? expf(mlv[u][0] - mb) : 0.f;
+      l += mlv[u][1] * w;
+      acc += v[u] * w;
+    }
+    m = mb;
   }
   const float inv = (l > 0.f) ? 1.f / l : 0.f;
   f16x4 o4;
@@ -386,7 +578,7 @@ __global__ void __launch_bounds__(128) sparse_mla_merge_kernel(
 // ---------------------------------------------------------------------------
 // launch configuration
 // ---------------------------------------------------------------------------
-constexpr int kDecKW = 4;       // decode: key-waves per workgroup
+constexpr int kDecKW = 4;        // decode: key-waves per workgroup
 constexpr int kTargetWGs = 256;  // one wave of workgroups over 256 CUs
 
 static bool use_prefill_config(int B, int n_head) {
@@ -399,6 +591,7 @@ static int decode_splits(int B, int n_head, int topk) {
   int s = kTargetWGs / (B * hg > 0 ? B * hg : 1);
   const int max_s = (tiles + kDecKW - 1) / kDecKW;  // >= one tile per key-wave
   if (s > max_s) s = max_s;
+  if (s > kMergeMaxSplits) s = kMergeMaxSplits;
   if (s < 1) s = 1;
   if (s >= 8) s = s / 8 * 8;  // multiple of 8: a (token, split)'s head groups share an XCD
   return s;
@@ -439,6 +632,7 @@ extern "C" int mi355_dsa_sparse_mla_decode(
   DSA_CHECK(B >= 0 && n_head > 0, "n_head must be > 0");
   DSA_CHECK(topk >= 0 && max_blocks >= 0 && n_kv_rows >= 0, "bad sizes");
   DSA_CHECK(page_size > 0, "page size must be > 0");
+  DSA_CHECK(n_kv_rows < ((int64_t)1 << 31), "cache has too many rows");
   if (B == 0) return MI355_DSA_OK;
   DSA_CHECK(o && lse && q && kv_cache && seq_lens, "null pointer argument");
   DSA_CHECK(topk == 0 || idx, "null idx");

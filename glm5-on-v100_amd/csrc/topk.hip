@@ -94,6 +94,28 @@ __device__ void find_threshold(TopkShared& sh, int nbins, uint32_t need, int* T,
   __syncthreads();
 }
 
+
+// Applies f(p, key) to every position p < L of the row; each thread keeps
+// kTkU independent loads in flight per step (a plain strided loop would
+// wait for one load per iteration).
+constexpr int kTkU = 16;
+template <typename F>
+__device__ __forceinline__ void row_pass(const float* __restrict__ row, int L, F f) {
+  for (int base = 0; base < L; base += kTkThreads * kTkU) {
+    float v[kTkU];
+#pragma unroll
+    for (int u = 0; u < kTkU; u++) {
+      const int p = base + u * kTkThreads + (int)threadIdx.x;
+      v[u] = (p < L) ? row[p] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kTkU; u++) {
+      const int p = base + u * kTkThreads + (int)threadIdx.x;
+      if (p < L) f(p, mono_key(v[u]));
+    }
+  }
+}
+
 template <bool HAVE_HIST>
 __global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
     const float* __restrict__ score, int64_t row_stride,
@@ -130,8 +152,7 @@ __global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
   if (rebuild) {
     for (int i = threadIdx.x; i < kTopkBins; i += kTkThreads) sh.hist[i] = 0u;
     __syncthreads();
-    for (int p = threadIdx.x; p < L; p += kTkThreads)
-      atomicAdd(&sh.hist[mono_key(row[p]) >> 20], 1u);
+    row_pass(row, L, [&](int, uint32_t key) { atomicAdd(&sh.hist[key >> 20], 1u); });
     __syncthreads();
   }
   int T;
@@ -147,10 +168,9 @@ __global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
     __syncthreads();
     for (int i = threadIdx.x; i < kTopkBins; i += kTkThreads) sh.hist[i] = 0u;
     __syncthreads();
-    for (int p = threadIdx.x; p < L; p += kTkThreads) {
-      const uint32_t key = mono_key(row[p]);
+    row_pass(row, L, [&](int, uint32_t key) {
       if ((key >> 20) == prefix) atomicAdd(&sh.hist[(key >> 8) & 0xfffu], 1u);
-    }
+    });
     __syncthreads();
     find_threshold(sh, kTopkBins, need, &T, &above);
     need -= above;
@@ -162,10 +182,9 @@ __global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
       __syncthreads();
       for (int i = threadIdx.x; i < 256; i += kTkThreads) sh.hist[i] = 0u;
       __syncthreads();
-      for (int p = threadIdx.x; p < L; p += kTkThreads) {
-        const uint32_t key = mono_key(row[p]);
+      row_pass(row, L, [&](int, uint32_t key) {
         if ((key >> 8) == prefix) atomicAdd(&sh.hist[key & 0xffu], 1u);
-      }
+      });
       __syncthreads();
       find_threshold(sh, 256, need, &T, &above);
       need -= above;
@@ -180,10 +199,18 @@ __global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
   uint32_t base_gt = 0, base_eq = 0;
   for (int c0 = 0; c0 < L; c0 += kTkChunk) {
     __syncthreads();
-    for (int i = 0; i < kTkV; i++) {
-      const int q = i * kTkThreads + threadIdx.x;  // coalesced
-      const int p = c0 + q;
-      sh.chunk[q + q / kTkV] = (p < L) ? row[p] : 0.f;
+    {
+      float v[kTkV];
+#pragma unroll
+      for (int i = 0; i < kTkV; i++) {
+        const int p = c0 + i * kTkThreads + (int)threadIdx.x;  // coalesced
+        v[i] = (p < L) ? row[p] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < kTkV; i++) {
+        const int q = i * kTkThreads + threadIdx.x;
+        sh.chunk[q + q / kTkV] = v[i];
+      }
     }
     __syncthreads();
     const int my0 = threadIdx.x * kTkV;
