@@ -52,6 +52,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="only the headline decode")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--calib-copy-mib", type=int, default=0,
+                   help="run one device copy of this many MiB first (a known-size "
+                        "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     return p.parse_args()
 
 
@@ -284,6 +287,14 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     log(f"device: {torch.cuda.get_device_name(dev)}")
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {n} bytes read, {n} bytes written")
+        del src, dst
 
     # ---- headline: C3 decode at 180k ----
     L = args.layers

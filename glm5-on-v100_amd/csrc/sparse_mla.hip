@@ -66,8 +66,8 @@ struct MlaParams {
   const int32_t* seq_lens;
   f16* o;
   float* lse;
-  float* part_o;   // [B, H, S, 512] unnormalised partial outputs (S > 1)
-  float* part_ml;  // [B, H, S, 2]   partial (m, l)
+  f16* part_o;     // [B, H, S, 512] per-split normalised outputs o_s (S > 1)
+  float* part_ml;  // [B, H, S, 2]   per-split (m_s, l_s)
   int B, n_head, topk, max_blocks, page_size, n_splits;
   int64_t n_kv_rows;
   float scale_h;  // fp16-rounded softmax scale
@@ -507,8 +507,12 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
             for (int r = 0; r < 4; r++) o4[r] = (f16)(v[r] * inv);
             *reinterpret_cast<f16x4*>(p.o + bh * kValueDim + 16 * t + 4 * g) = o4;
           } else {
+            // split partial stored normalised (|o_s| <= max|V|) in fp16
             const int64_t ps = bh * p.n_splits + split;
-            *reinterpret_cast<f32x4*>(p.part_o + ps * kValueDim + 16 * t + 4 * g) = v;
+            f16x4 o4;
+#pragma unroll
+            for (int r = 0; r < 4; r++) o4[r] = (f16)(v[r] * inv);
+            *reinterpret_cast<f16x4*>(p.part_o + ps * kValueDim + 16 * t + 4 * g) = o4;
           }
         }
       }
@@ -526,7 +530,8 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
 }
 
 // Flash-decode merge of S partial states (reference :1138-1184):
-// m = max_s m_s, w_s = l_s > 0 ? exp(m_s - m) : 0, o = sum w_s P_O_s / sum w_s l_s.
+// m = max_s m_s, w_s = l_s > 0 ? exp(m_s - m) l_s : 0, o = sum w_s o_s / sum w_s
+// (o_s is the split's own normalised output, stored in fp16).
 // One workgroup per (token, head), 128 threads x 4 dims.  Splits are taken
 // 16 at a time with every (m, l) pair and partial row of the batch loaded
 // together (one memory latency per batch), combined online across batches.
@@ -534,12 +539,12 @@ constexpr int kMergeMaxSplits = 128;
 constexpr int kMergeBatch = 16;
 
 __global__ void __launch_bounds__(128) sparse_mla_merge_kernel(
-    const float* __restrict__ part_o, const float* __restrict__ part_ml,
+    const f16* __restrict__ part_o, const float* __restrict__ part_ml,
     f16* __restrict__ O, float* __restrict__ LSE, int n_splits) {
   const int64_t bh = blockIdx.x;
   const int d = 4 * threadIdx.x;
   const f32x2* ml = reinterpret_cast<const f32x2*>(part_ml + bh * n_splits * 2);
-  const float* po = part_o + bh * n_splits * kValueDim + d;
+  const f16* po = part_o + bh * n_splits * kValueDim + d;
   float m = -1e30f, l = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
@@ -549,8 +554,10 @@ __global__ void __launch_bounds__(128) sparse_mla_merge_kernel(
     for (int u = 0; u < kMergeBatch; u++) {
       const int s = s0 + u;
       mlv[u] = (s < n_splits) ? ml[s] : (f32x2){-1e30f, 0.f};
-      v[u] = (s < n_splits) ? *reinterpret_cast<const f32x4*>(po + (int64_t)s * kValueDim)
-                            : (f32x4){0.f, 0.f, 0.f, 0.f};
+      const f16x4 h = (s < n_splits) ? *reinterpret_cast<const f16x4*>(po + (int64_t)s * kValueDim)
+                                     : (f16x4){0, 0, 0, 0};
+#pragma unroll
+      for (int r = 0; r < 4; r++) v[u][r] = (float)h[r];
     }
     float mb = m;
 #pragma unroll
@@ -561,8 +568,8 @@ __global__ void __launch_bounds__(128) sparse_mla_merge_kernel(
     acc *= resc;
 #pragma unroll
     for (int u = 0; u < kMergeBatch; u++) {
-      const float w = (mlv[u][1] > 0.f) ? expf(mlv[u][0] - mb) : 0.f;
-      l += mlv[u][1] * w;
+      const float w = (mlv[u][1] > 0.f) ? expf(mlv[u][0] - mb) * mlv[u][1] : 0.f;
+      l += w;
       acc += v[u] * w;
     }
     m = mb;
@@ -620,7 +627,7 @@ extern "C" size_t mi355_dsa_sparse_mla_workspace_size(int B, int n_head, int top
   if (use_prefill_config(B, n_head)) return 0;
   const int S = decode_splits(B, n_head, topk);
   if (S <= 1) return 0;
-  return (size_t)B * n_head * S * (kValueDim + 2) * sizeof(float);
+  return (size_t)B * n_head * S * (kValueDim * sizeof(f16) + 2 * sizeof(float));
 }
 
 extern "C" int mi355_dsa_sparse_mla_decode(
@@ -672,8 +679,8 @@ extern "C" int mi355_dsa_sparse_mla_decode(
     DSA_CHECK(workspace && workspace_bytes >= need,
               "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     DSA_CHECK(aligned_to(workspace, 16), "workspace must be 16-byte aligned");
-    prm.part_o = reinterpret_cast<float*>(workspace);
-    prm.part_ml = prm.part_o + (size_t)B * n_head * S * kValueDim;
+    prm.part_o = reinterpret_cast<f16*>(workspace);
+    prm.part_ml = reinterpret_cast<float*>(prm.part_o + (size_t)B * n_head * S * kValueDim);
   }
   const dim3 grid(S, (n_head + 15) / 16, B);
   int rc = kv_fp8 ? launch_mla<true, 1, kDecKW, 1>(prm, grid, st)

@@ -36,8 +36,11 @@ struct TopkShared {
   uint32_t above;
 };
 
-// Block-wide exclusive prefix sum over threads; *total gets the full sum.
-__device__ uint32_t block_excl_scan(uint32_t v, uint32_t* wsum, uint32_t* total) {
+// Block-wide exclusive prefix sum over NT threads; *total gets the full sum.
+// wsum needs NT/64 + 1 words.
+template <int NT>
+__device__ uint32_t block_excl_scan_n(uint32_t v, uint32_t* wsum, uint32_t* total) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   uint32_t x = v;
 #pragma unroll
@@ -49,18 +52,22 @@ __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* wsum, uint32_t* total)
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t run = 0;
-    for (int w = 0; w < kTkWaves; w++) {
+    for (int w = 0; w < NW; w++) {
       const uint32_t t = wsum[w];
       wsum[w] = run;
       run += t;
     }
-    wsum[kTkWaves] = run;
+    wsum[NW] = run;
   }
   __syncthreads();
   const uint32_t res = wsum[wave] + x - v;
-  *total = wsum[kTkWaves];
+  *total = wsum[NW];
   __syncthreads();
   return res;
+}
+
+__device__ uint32_t block_excl_scan(uint32_t v, uint32_t* wsum, uint32_t* total) {
+  return block_excl_scan_n<kTkThreads>(v, wsum, total);
 }
 
 // Bin T of an nbins histogram with above(T) < need <= above(T) + hist[T],
@@ -116,29 +123,16 @@ __device__ __forceinline__ void row_pass(const float* __restrict__ row, int L, F
   }
 }
 
-template <bool HAVE_HIST>
-__global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
-    const float* __restrict__ score, int64_t row_stride,
-    const int32_t* __restrict__ seq_lens, const uint32_t* __restrict__ hist_in,
-    int32_t* __restrict__ idx, int K) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  TopkShared& sh = *reinterpret_cast<TopkShared*>(smem_raw);
-  const int r = blockIdx.x;
-  const float* row = score + (int64_t)r * row_stride;
-  int32_t* out = idx + (int64_t)r * K;
-  int L = seq_lens[r];
-  if (L > row_stride) L = (int)row_stride;
-  if (L < 0) L = 0;
-
-  if (L <= K) {
-    for (int p = threadIdx.x; p < K; p += kTkThreads) out[p] = (p < L) ? p : -1;
-    return;
-  }
-
+// Whole-row selection by one 1024-thread workgroup (L > K): 3-level radix
+// select on LDS histograms, then an ordered compaction pass.  hist_row (may
+// be null) is the row's level-1 histogram; one that does not count exactly
+// L keys is rebuilt from the row.
+__device__ void topk_row_select(TopkShared& sh, const float* __restrict__ row, int L, int K,
+                                int32_t* __restrict__ out, const uint32_t* __restrict__ hist_row) {
   // ---- level 1: bits [20,32) ----
-  bool rebuild = !HAVE_HIST;
-  if (HAVE_HIST) {
-    const uint32_t* h = hist_in + (int64_t)r * kTopkBins;
+  bool rebuild = hist_row == nullptr;
+  if (hist_row != nullptr) {
+    const uint32_t* h = hist_row;
     uint32_t part = 0;
     for (int i = threadIdx.x; i < kTopkBins; i += kTkThreads) {
       sh.hist[i] = h[i];
@@ -250,6 +244,26 @@ __global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
     base_eq += tot >> 16;
   }
   // Exactly K positions were written (L > K); nothing to pad.
+}
+
+template <bool HAVE_HIST>
+__global__ void __launch_bounds__(kTkThreads) topk_row_kernel(
+    const float* __restrict__ score, int64_t row_stride,
+    const int32_t* __restrict__ seq_lens, const uint32_t* __restrict__ hist_in,
+    int32_t* __restrict__ idx, int K) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  TopkShared& sh = *reinterpret_cast<TopkShared*>(smem_raw);
+  const int r = blockIdx.x;
+  const float* row = score + (int64_t)r * row_stride;
+  int32_t* out = idx + (int64_t)r * K;
+  int L = seq_lens[r];
+  if (L > row_stride) L = (int)row_stride;
+  if (L < 0) L = 0;
+  if (L <= K) {
+    for (int p = threadIdx.x; p < K; p += kTkThreads) out[p] = (p < L) ? p : -1;
+    return;
+  }
+  topk_row_select(sh, row, L, K, out, HAVE_HIST ? hist_in + (int64_t)r * kTopkBins : nullptr);
 }
 
 template <bool HAVE_HIST>

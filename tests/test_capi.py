@@ -82,9 +82,9 @@ def test_empty_inputs_are_noops(pkg, lib):
 
 
 def test_sparse_workspace_size(lib):
-    # decode config at B=4, H=64, topk=2048: 16 splits of fp32 partials
+    # decode config at B=4, H=64, topk=2048: 16 splits of fp16 partials + (m, l)
     n = lib.mi355_dsa_sparse_mla_workspace_size(4, 64, 2048)
-    assert n == 4 * 64 * 16 * (512 + 2) * 4
+    assert n == 4 * 64 * 16 * (512 * 2 + 2 * 4)
     # prefill config (>= 256 workgroups) needs none
     assert lib.mi355_dsa_sparse_mla_workspace_size(4096, 64, 2048) == 0
 
