@@ -39,6 +39,22 @@ DECODE_BYTES = 5_997_568
 DECODE_FLOPS = 4 * 64 * 2048 * (576 + 512) * 2
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "sparse_mla_decode_c3_pmc.md")
+
+
+def measured_traffic():
+    """HBM bytes per decode layer from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE of both kernels, scaled by the copy-kernel
+    calibration); None when the summary is absent."""
+    try:
+        for ln in open(TRAFFIC_PROFILE):
+            if ln.startswith("traffic_bytes_per_layer:"):
+                return int(ln.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -334,7 +350,8 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/sparse_mla_decode_c3_pmc.md",
             "kernel": "sparse_mla_kernel (decode config) + sparse_mla_merge_kernel",
             "bytes_per_launch": DECODE_BYTES,
         },

@@ -35,14 +35,34 @@ int check_launch(const char* what) {
 
 // out[0..63]  : x32 MFMA probe results, out[64..127]: x16 probe results,
 // out[128..383]: bit-trick e4m3 decode of bytes 0..255 (value exactly),
-// out[384..639]: hardware v_cvt_pk_f32_fp8 decode of bytes 0..255.
+// out[384..639]: hardware v_cvt_pk_f32_fp8 decode of bytes 0..255,
+// out[640..895]: v_cvt_scalef32_pk_f16_fp8 (scale 1) decode of bytes 0..255,
+// the conversion the sparse attention gathers use.
+// mfma_bad bit 4: ds_read_b64_tr_b16 lane mapping differs from the one the
+// sparse attention PV step assumes (lane j of a 16-lane group whose lane i
+// points at row 4g + i/4, column 4(i%4) receives column j of rows 4g..4g+3).
 // Probe p uses a single non-zero k-slot (g = p/KPL, e = p%KPL) in both A and
 // B: A[row c] = c+1, B[col c] = c+101, so D[i][j] must be (i+1)(j+101) at
 // lane (col j, rows 4g'..) whatever k that slot maps to.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
 __global__ void selfcheck_kernel(float* out, int* mfma_bad) {
   const int lane = threadIdx.x;
   const int c = lane & 15, g = lane >> 4;
-  int bad32 = 0, bad16 = 0;
+  int bad32 = 0, bad16 = 0, badtr = 0;
+  // 16 x 16 fp16 tile with value 16*row + col (exact in fp16)
+  __shared__ __align__(16) f16 tile[16 * 16];
+  for (int i = lane; i < 256; i += 64) tile[i] = (f16)(float)i;
+  __syncthreads();
+  {
+    const f16* src = tile + (4 * g + (c >> 2)) * 16 + 4 * (c & 3);
+    const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)src);
+    const f16x4 h = __builtin_bit_cast(f16x4, t);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if ((float)h[k] != (float)(16 * (4 * g + k) + c)) badtr++;
+  }
   for (int p = 0; p < 32; p++) {
     f16x8 a, b;
 #pragma unroll
@@ -75,6 +95,7 @@ __global__ void selfcheck_kernel(float* out, int* mfma_bad) {
   }
   if (bad32) atomicOr(mfma_bad, 1);
   if (bad16) atomicOr(mfma_bad, 2);
+  if (badtr) atomicOr(mfma_bad, 4);
   // e4m3 decode of all 256 byte values, 4 per lane.
   const uint32_t w = (uint32_t)(4 * lane) | ((uint32_t)(4 * lane + 1) << 8) |
                      ((uint32_t)(4 * lane + 2) << 16) |
@@ -89,6 +110,12 @@ __global__ void selfcheck_kernel(float* out, int* mfma_bad) {
   out[384 + 4 * lane + 1] = h0[1];
   out[384 + 4 * lane + 2] = h1[0];
   out[384 + 4 * lane + 3] = h1[1];
+  const f16x2 s0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, false);
+  const f16x2 s1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, true);
+  out[640 + 4 * lane + 0] = (float)s0[0];
+  out[640 + 4 * lane + 1] = (float)s0[1];
+  out[640 + 4 * lane + 2] = (float)s1[0];
+  out[640 + 4 * lane + 3] = (float)s1[1];
 }
 
 // Exact OCP e4m3 value of a byte (0x7f / 0xff are NaN in e4m3fn; the
@@ -112,14 +139,14 @@ extern "C" int mi355_dsa_selfcheck(void* stream) {
   hipStream_t st = as_stream(stream);
   float* d_out = nullptr;
   int* d_bad = nullptr;
-  const size_t nout = 640;
+  const size_t nout = 896;
   if (hipMalloc(&d_out, nout * sizeof(float)) != hipSuccess ||
       hipMalloc(&d_bad, sizeof(int)) != hipSuccess) {
     if (d_out) hipFree(d_out);
     return set_error(MI355_DSA_EHIP, "selfcheck: hipMalloc failed");
   }
   int rc = MI355_DSA_OK;
-  float h_out[640];
+  float h_out[896];
   int h_bad = 0;
   if (hipMemsetAsync(d_bad, 0, sizeof(int), st) != hipSuccess) {
     rc = set_error(MI355_DSA_EHIP, "selfcheck: memset failed");
@@ -137,10 +164,12 @@ extern "C" int mi355_dsa_selfcheck(void* stream) {
   hipFree(d_out);
   hipFree(d_bad);
   if (rc != MI355_DSA_OK) return rc;
-  if (h_bad)
+  if (h_bad & 3)
     return set_error(MI355_DSA_ECHECK,
                      "selfcheck: MFMA accumulator placement mismatch (mask %d)",
                      h_bad);
+  if (h_bad & 4)
+    return set_error(MI355_DSA_ECHECK, "selfcheck: ds_read_b64_tr_b16 lane mapping mismatch");
   int hw_ok = 1;
   for (int b = 0; b < 256; b++) {
     if ((b & 0x7f) == 0x7f) continue;  // NaN codes
@@ -150,6 +179,10 @@ extern "C" int mi355_dsa_selfcheck(void* stream) {
                        "selfcheck: e4m3 decode of 0x%02x gave %g, want %g", b,
                        (double)h_out[128 + b], want);
     if ((double)h_out[384 + b] != want) hw_ok = 0;
+    if ((double)h_out[640 + b] != want)
+      return set_error(MI355_DSA_ECHECK,
+                       "selfcheck: scaled fp8->fp16 conversion of 0x%02x gave %g, want %g", b,
+                       (double)h_out[640 + b], want);
   }
   // Informational: whether v_cvt_pk_f32_fp8 decodes OCP e4m3 on this device.
   set_error(MI355_DSA_OK, "selfcheck ok; hw_cvt_pk_f32_fp8_ocp=%d", hw_ok);

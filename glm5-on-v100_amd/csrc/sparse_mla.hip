@@ -7,8 +7,11 @@
 //   * online softmax with m initialised to -1e30, masked scores -inf (:961,
 //     :1047-1067); P is rounded to fp16 for the PV product (:1068), the
 //     running sum uses the fp32 p;
-//   * o = PV / l in fp16, lse = m + ln l, or o = 0 and lse = -inf when no
-//     key is valid (merge convention, :1175-1183).
+//   * o = PV / l in fp16, lse = m + ln l, or o = 0 and lse = empty_lse when
+//     no key is valid: -inf on the reference's split-decode path (merge
+//     convention, :1175-1183) and -1e30 (= m_init + ln 1, :1789-1793) for the
+//     shapes the reference sends to its prefill kernel (B >= 32 and
+//     n_head <= 16, :2511).
 //
 // MFMA formulation (one wave owns 16 heads):
 //   S^T[key][head] = K[key][:] . Qs[head][:]      v_mfma_f32_16x16x32_f16
@@ -70,7 +73,8 @@ struct MlaParams {
   float* part_ml;  // [B, H, S, 2]   per-split (m_s, l_s)
   int B, n_head, topk, max_blocks, page_size, n_splits;
   int64_t n_kv_rows;
-  float scale_h;  // fp16-rounded softmax scale
+  float scale_h;    // fp16-rounded softmax scale
+  float empty_lse;  // lse of a (token, head) with no valid key
 };
 
 template <int HW, int KW, int NB>
@@ -447,7 +451,7 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
     const int h = h0 + 16 * hw + c;
     if (h < p.n_head) {
       if (g == 0)
-        p.lse[(int64_t)b * p.n_head + h] = (l_run > 0.f) ? (m_run + logf(l_run)) : -INFINITY;
+        p.lse[(int64_t)b * p.n_head + h] = (l_run > 0.f) ? (m_run + logf(l_run)) : p.empty_lse;
       const float inv = (l_run > 0.f) ? 1.f / l_run : 0.f;
       f16* orow = p.o + ((int64_t)b * p.n_head + h) * kValueDim;
 #pragma unroll
@@ -519,7 +523,7 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
     }
     if (kw == 0 && g == 0 && h < p.n_head) {
       if (final_out) {
-        p.lse[bh] = (L > 0.f) ? (M + logf(L)) : -INFINITY;
+        p.lse[bh] = (L > 0.f) ? (M + logf(L)) : p.empty_lse;
       } else {
         const int64_t ps = bh * p.n_splits + split;
         p.part_ml[ps * 2 + 0] = M;
@@ -540,7 +544,7 @@ constexpr int kMergeBatch = 16;
 
 __global__ void __launch_bounds__(128) sparse_mla_merge_kernel(
     const f16* __restrict__ part_o, const float* __restrict__ part_ml,
-    f16* __restrict__ O, float* __restrict__ LSE, int n_splits) {
+    f16* __restrict__ O, float* __restrict__ LSE, int n_splits, float empty_lse) {
   const int64_t bh = blockIdx.x;
   const int d = 4 * threadIdx.x;
   const f32x2* ml = reinterpret_cast<const f32x2*>(part_ml + bh * n_splits * 2);
@@ -579,7 +583,7 @@ __global__ void __launch_bounds__(128) sparse_mla_merge_kernel(
 #pragma unroll
   for (int r = 0; r < 4; r++) o4[r] = (f16)(acc[r] * inv);
   *reinterpret_cast<f16x4*>(O + bh * kValueDim + d) = o4;
-  if (threadIdx.x == 0) LSE[bh] = (l > 0.f) ? (m + logf(l)) : -INFINITY;
+  if (threadIdx.x == 0) LSE[bh] = (l > 0.f) ? (m + logf(l)) : empty_lse;
 }
 
 // ---------------------------------------------------------------------------
@@ -664,6 +668,9 @@ extern "C" int mi355_dsa_sparse_mla_decode(
   prm.page_size = page_size;
   prm.n_kv_rows = n_kv_rows;
   prm.scale_h = (float)(f16)scale;
+  // the reference's prefill kernel (taken for B >= 32 && n_head <= 16,
+  // sm70_mla_decode.cu:2511) leaves lse = -1e30 + ln 1 for an empty token
+  prm.empty_lse = (B >= 32 && n_head <= 16) ? -1e30f : -INFINITY;
   hipStream_t st = as_stream(stream);
 
   if (use_prefill_config(B, n_head)) {
@@ -687,6 +694,6 @@ extern "C" int mi355_dsa_sparse_mla_decode(
                   : launch_mla<false, 1, kDecKW, 1>(prm, grid, st);
   if (rc != MI355_DSA_OK || S == 1) return rc;
   sparse_mla_merge_kernel<<<dim3((unsigned)((int64_t)B * n_head)), 128, 0, st>>>(
-      prm.part_o, prm.part_ml, prm.o, prm.lse, S);
+      prm.part_o, prm.part_ml, prm.o, prm.lse, S, prm.empty_lse);
   return check_launch("sparse_mla_merge");
 }

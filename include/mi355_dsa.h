@@ -42,7 +42,10 @@ int mi355_dsa_abi_version(void);
 
 /*
  * Device self-check, synchronous on `stream`: verifies the MFMA accumulator
- * placement the kernels assume and the e4m3 decode used in the gathers.
+ * placement the kernels assume, the ds_read_b64_tr_b16 lane mapping of the
+ * attention PV step, and both e4m3 decodes used in the gathers.  Unlike the
+ * other entry points it allocates (and frees) a few KB of device memory and
+ * synchronises the stream; call it once at start-up, outside graph capture.
  * Replaces the reference's first-launch WMMA layout probe
  * (csrc/attention/sm70_mla_decode.cu:511-540, :2807-2818).
  * Returns MI355_DSA_ECHECK on a mismatch.

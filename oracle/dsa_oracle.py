@@ -249,18 +249,22 @@ def scaled_q(q: torch.Tensor, scale: float) -> torch.Tensor:
 
 def sparse_mla(q: torch.Tensor, kv_cache: torch.Tensor, idx: torch.Tensor,
                bt: torch.Tensor, seq_lens: torch.Tensor, scale: float,
-               dtype=torch.float64):
+               dtype=torch.float64, empty_lse: float | None = None):
     """Reference sparse attention for every token/head.  A selected entry j
     is used iff 0 <= idx < seq_len and its row resolves inside the cache
     (sm70_mla_decode.cu:977-992).  Returns (o fp32 [B,H,512], lse fp32
-    [B,H]); tokens with no valid key get o = 0 and lse = -inf (merge
-    convention, sm70_mla_decode.cu:1175-1183)."""
+    [B,H]); tokens with no valid key get o = 0 and lse = empty_lse, by
+    default the op's: -1e30 when the reference dispatches to its prefill
+    kernel (B >= 32 and H <= 16, sm70_mla_decode.cu:2511, lse = m_init + ln 1
+    at :1789-1793), else -inf (merge convention, :1175-1183)."""
     B, H, D = q.shape
     page = kv_cache.shape[-2]
     row_w = kv_cache.shape[-1]
     n_rows = kv_cache.numel() // row_w
     o = torch.zeros(B, H, 512, dtype=torch.float32)
-    lse = torch.full((B, H), float("-inf"), dtype=torch.float32)
+    if empty_lse is None:
+        empty_lse = -1e30 if (B >= 32 and H <= 16) else float("-inf")
+    lse = torch.full((B, H), empty_lse, dtype=torch.float32)
     qs = scaled_q(q, scale).to(dtype)
     for b in range(B):
         sel = idx[b].to(torch.int64)

@@ -67,6 +67,7 @@ DECODE = [
     (3, 3, 8, 20, 16, False, 256, [300, 200, 17]),   # partial head tile
     (4, 4, 64, 60, 64, True, 2048, [3800, 3800, 3800, 3800]),
     (5, 1, 128, 40, 64, False, 1024, [2400]),         # two 64-head groups
+    (6, 2, 16, 30, 48, True, 512, [1400, 500]),      # page size not a power of two
 ]
 
 
@@ -87,6 +88,22 @@ def test_decode_invalid_entries(ops, dev):
     ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
     check(o, lse, ro, rl)
     assert torch.all(o[2] == 0) and torch.all(torch.isinf(lse[2]))
+
+
+@pytest.mark.parametrize("B,H,expect", [(40, 16, -1e30), (300, 16, -1e30), (40, 64, -math.inf),
+                                         (31, 16, -math.inf)])
+def test_empty_token_lse_convention(ops, dev, B, H, expect):
+    """A token with no valid key gets o = 0 and the reference's lse: -1e30
+    where the reference runs its prefill kernel (B >= 32, H <= 16), -inf on
+    its split-decode path."""
+    seqs = [90 + (i % 7) for i in range(B)]
+    q, kv, idx, bt, seq = make(30 + B + H, B, H, 12, 16, True, 64, seqs)
+    idx[3] = -1
+    o, lse = run(ops, dev, q, kv, idx, bt, seq)
+    ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
+    check(o, lse, ro, rl)
+    assert torch.all(o[3] == 0)
+    assert torch.all(lse[3] == expect) and torch.all(rl[3] == expect)
 
 
 def test_prefill_config(ops, dev):

@@ -122,3 +122,19 @@ def test_dsmla_per_tile_layout():
     assert sc[0] == 4.0 / 448 and sc[1] == 8.0 / 448
     assert sc[2] == O.FLT_MIN and sc[3] == O.FLT_MIN
     assert int(rows[0, 0]) == 0x7E and int(rows[0, 200]) == 0xFE
+
+
+@pytest.mark.parametrize("B,H,expect", [(32, 16, -1e30), (31, 16, -math.inf), (32, 17, -math.inf)])
+def test_empty_token_lse_follows_reference_dispatch(B, H, expect):
+    """An empty token's lse is -1e30 exactly when the reference's op takes its
+    prefill kernel (B >= 32 and H <= 16, sm70_mla_decode.cu:2511, whose
+    epilogue writes m_init + ln 1, :1789-1793), else -inf (:1175-1183)."""
+    g = torch.Generator().manual_seed(9)
+    kv, _ = make_cache(g)
+    bt = torch.randperm(6, generator=g).to(torch.int32).expand(B, 6).contiguous()
+    q = torch.randn(B, H, 576, generator=g).to(torch.float16)
+    idx = torch.full((B, 4), -1, dtype=torch.int32)
+    idx[1:, 0] = 5
+    o, lse = O.sparse_mla(q, kv, idx, bt, torch.full((B,), 40, dtype=torch.int32), SCALE)
+    assert torch.all(o[0] == 0) and torch.all(lse[0] == expect)
+    assert torch.isfinite(lse[1:]).all() and (lse[1:] > -1e29).all()
