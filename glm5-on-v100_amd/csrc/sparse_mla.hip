@@ -533,6 +533,327 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp8_ds_mla split decode with LDS-DMA gathers.
+//
+// Workgroup = (split, 16-head group, token), 4 waves; every wave owns the
+// same 16 heads and takes 16 of each 64-key chunk.  Differences from the
+// register-staged kernel above, all aimed at the latency chain of a small
+// decode batch:
+//  * the block-table row of the token is staged in LDS together with the
+//    idx loads, so resolving idx -> cache row costs no second dependent
+//    global round trip;
+//  * rows are gathered with global_load_lds_dwordx4 straight into LDS as
+//    raw 656-B rows (no staging registers, no conversion pass), two chunks
+//    in flight; masked keys read a zero row, so they carry finite zeros;
+//  * scaled Q lives in registers in the k-slot order of the QK operands;
+//  * the e4m3 bytes are converted to exact fp16 at operand load: 16-byte
+//    reads for QK, ds_read_b64_tr_b8 for the V^T operands of PV (one
+//    transpose read gives two 16-dim tiles of 4 keys).
+// Barriers that must not wait for in-flight gathers are raw s_barrier with
+// an explicit LDS wait (__syncthreads would also drain the LDS-DMA queue).
+// ---------------------------------------------------------------------------
+constexpr int kDmaKeys = 64;                                  // keys per chunk
+constexpr int kDmaPieces = kDmaKeys * (kDsmlaRowBytes / 16);  // 2624 16-B pieces
+constexpr int kDmaRounds = (kDmaPieces + 255) / 256;          // LDS-DMA ops per thread
+constexpr int kDmaBufBytes = kDmaRounds * 256 * 16;           // one chunk buffer
+constexpr int kBtStage = 4096;                                 // block-table entries in LDS
+constexpr int kDmaSplitKeys = 2 * kDmaKeys;                    // keys per split (max)
+
+__device__ __align__(16) const uint8_t kZeroRow[kDsmlaRowBytes] = {};
+
+struct DmaSmem {
+  union {
+    struct {
+      uint8_t buf[2][kDmaBufBytes];
+      int32_t bt[kBtStage];
+    } main;
+    f32x4 xbuf[4][3][kOTiles / 4][64];  // key-wave merge (as MlaSmem, KW = 4)
+  } u;
+  int32_t rows[kDmaSplitKeys];
+  float m[4 * 16];
+  float l[4 * 16];
+};
+
+typedef int s32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) s32x2 lds_s32x2;
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// 4 e4m3 bytes -> 4 exact fp16 values
+__device__ __forceinline__ f16x4 e4m3x4_to_f16x4(uint32_t w) {
+  const f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, false);
+  const f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, true);
+  const u32x2 pk = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+  return __builtin_bit_cast(f16x4, pk);
+}
+
+// Issues the LDS-DMA gather of one 64-key chunk (rows[0..64), -1 = masked)
+// into buf: piece q = 256u + 64*wave + lane lands at buf + 16q, i.e. key
+// q / 41, 16-byte chunk q % 41 of its 656-byte row.  Every thread issues
+// exactly kDmaRounds operations (padding pieces read the zero row).
+__device__ __forceinline__ void dma_chunk(const uint8_t* __restrict__ kv, const int32_t* rows,
+                                          uint8_t* buf) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int u = 0; u < kDmaRounds; u++) {
+    const int q = 256 * u + 64 * wave + lane;
+    const int r = q / 41, ch = q - r * 41;
+    const int row = (q < kDmaPieces) ? rows[r < kDmaKeys ? r : 0] : -1;
+    const uint8_t* src = (row >= 0) ? kv + (int64_t)row * kDsmlaRowBytes + 16 * ch
+                                    : kZeroRow + 16 * (q < kDmaPieces ? ch : 0);
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)(buf + 16 * (256 * u + 64 * wave)), 16, 0,
+                                     0);
+  }
+}
+
+// QK of one wave's 16 keys of a chunk: returns the masked scores of keys
+// kbase + 4g + r (r = 0..3, accumulator rows) for head c, and their tile scales.
+__device__ __forceinline__ f32x4 dma_qk(const uint8_t* cb, int kbase, const int32_t* rows,
+                                        const f16x8 (&qf)[18], f32x4 (&ksc)[4]) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  // All LDS operands are read first (in-order returns let each MFMA wait only
+  // for its own operand).
+  const uint8_t* krow = cb + (kbase + c) * kDsmlaRowBytes;
+  u32x4 kraw[8];
+  f16x8 krope[2];
+  int4 vr;
+#pragma unroll
+  for (int s2 = 0; s2 < 8; s2++) kraw[s2] = *reinterpret_cast<const u32x4*>(krow + 64 * s2 + 16 * g);
+#pragma unroll
+  for (int s3 = 0; s3 < 2; s3++)
+    krope[s3] = *reinterpret_cast<const f16x8*>(krow + 528 + 64 * s3 + 16 * g);
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+    ksc[r] = *reinterpret_cast<const f32x4*>(cb + (kbase + 4 * g + r) * kDsmlaRowBytes + 512);
+  vr = *reinterpret_cast<const int4*>(rows + kbase + 4 * g);
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4 acc[5];
+#pragma unroll
+  for (int a = 0; a < 5; a++) acc[a] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s2 = 0; s2 < 8; s2++) {
+    const f16x4 a0 = e4m3x4_to_f16x4(kraw[s2][0]), a1 = e4m3x4_to_f16x4(kraw[s2][1]);
+    const f16x4 a2 = e4m3x4_to_f16x4(kraw[s2][2]), a3 = e4m3x4_to_f16x4(kraw[s2][3]);
+    const f16x8 k0 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+    const f16x8 k1 = {a2[0], a2[1], a2[2], a2[3], a3[0], a3[1], a3[2], a3[3]};
+    acc[s2 >> 1] = mfma16x16x32(k0, qf[2 * s2], acc[s2 >> 1]);
+    acc[s2 >> 1] = mfma16x16x32(k1, qf[2 * s2 + 1], acc[s2 >> 1]);
+  }
+#pragma unroll
+  for (int s3 = 0; s3 < 2; s3++) acc[4] = mfma16x16x32(krope[s3], qf[16 + s3], acc[4]);
+  f32x4 sv;
+  const int vv[4] = {vr.x, vr.y, vr.z, vr.w};
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const float v = acc[4][r] + ksc[r][0] * acc[0][r] + ksc[r][1] * acc[1][r] +
+                    ksc[r][2] * acc[2][r] + ksc[r][3] * acc[3][r];
+    sv[r] = vv[r] >= 0 ? v : -INFINITY;
+  }
+  return sv;
+}
+
+// O^T += V^T (P x tile scale)^T for one wave's 16 keys of a chunk.
+__device__ __forceinline__ void dma_pv(const uint8_t* cb, int kbase, const float (&pr)[4],
+                                       const f32x4 (&ksc)[4], f32x4 (&oacc)[kOTiles]) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  // transpose read: lane i of a 16-lane group points at key
+  // kbase + 4g + (i/2)%4, dims 16*(2tt + i/8) + 8*(i%2); lane j then holds
+  // keys 4g..4g+3 at dim 32tt + j (bytes 0-3) and 32tt + 16 + j (bytes 4-7)
+  const uint8_t* vsrc =
+      cb + (kbase + 4 * g + ((c >> 1) & 3)) * kDsmlaRowBytes + 16 * (c >> 3) + 8 * (c & 1);
+  s32x2 vt[kOTiles / 2];
+#pragma unroll
+  for (int tt = 0; tt < kOTiles / 2; tt++)
+    vt[tt] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_s32x2*)(vsrc + 32 * tt));
+  f16x4 pb[4];
+#pragma unroll
+  for (int st = 0; st < 4; st++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) pb[st][r] = (f16)(pr[r] * ksc[r][st]);
+#pragma unroll
+  for (int tt = 0; tt < kOTiles / 2; tt++) {
+    const int st = tt >> 2;
+    oacc[2 * tt] = mfma16x16x16(e4m3x4_to_f16x4((uint32_t)vt[tt][0]), pb[st], oacc[2 * tt]);
+    oacc[2 * tt + 1] = mfma16x16x16(e4m3x4_to_f16x4((uint32_t)vt[tt][1]), pb[st], oacc[2 * tt + 1]);
+  }
+}
+
+// Decode for splits of at most two chunks (128 keys): both chunks are
+// resident in LDS, so each wave computes all its scores first and the
+// softmax needs no running rescale of O.
+__global__ void __launch_bounds__(256) sparse_mla_decode_dma_kernel(MlaParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  DmaSmem& sh = *reinterpret_cast<DmaSmem*>(smem_raw);
+  const int lane = threadIdx.x & 63;
+  const int kw = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int split = blockIdx.x, h0 = blockIdx.y * 16, b = blockIdx.z;
+  const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
+  const int seq_len = p.seq_lens[b];
+
+  // this split's key range: at most kDmaSplitKeys keys (host-guaranteed)
+  const int n_chunks_all = (p.topk + kDmaKeys - 1) / kDmaKeys;
+  const int cps = (n_chunks_all + p.n_splits - 1) / p.n_splits;
+  const int key_lo = min(split * cps * kDmaKeys, p.topk);
+  const int nkeys = min(key_lo + cps * kDmaKeys, p.topk) - key_lo;
+  const int nchunks = (nkeys + kDmaKeys - 1) / kDmaKeys;  // 0, 1 or 2
+  const bool bt_in_lds = p.max_blocks <= kBtStage;
+  const int32_t* bt_row = p.bt + (int64_t)b * p.max_blocks;
+
+  // ---- independent loads: idx, block-table row, Q ----
+  static_assert(kDmaSplitKeys <= 256, "one key per thread");
+  const int jk = threadIdx.x;  // the key this thread resolves
+  const int pos = (jk < nkeys) ? p.idx[(int64_t)b * p.topk + key_lo + jk] : -1;
+  if (bt_in_lds) {
+    int btv[kBtStage / 256];
+#pragma unroll
+    for (int u = 0; u < kBtStage / 256; u++) {
+      const int i = threadIdx.x + 256 * u;
+      btv[u] = (i < p.max_blocks) ? bt_row[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kBtStage / 256; u++) {
+      const int i = threadIdx.x + 256 * u;
+      if (i < p.max_blocks) sh.u.main.bt[i] = btv[u];
+    }
+  }
+  // Q fragments (B operand of S^T = K Q^T):
+  // step 2s'+e2 (s' < 8): lane group g holds dims 64s' + 16g + 8e2 .. +7
+  // step 16+s'':          lane group g holds dims 512 + 32s'' + 8g .. +7
+  f16x8 qf[18];
+  {
+    const int hq = h0 + c < p.n_head ? h0 + c : h0;
+    const f16* qr = p.q + ((int64_t)b * p.n_head + hq) * kLatentDim;
+#pragma unroll
+    for (int s2 = 0; s2 < 8; s2++) {
+      qf[2 * s2] = *reinterpret_cast<const f16x8*>(qr + 64 * s2 + 16 * g);
+      qf[2 * s2 + 1] = *reinterpret_cast<const f16x8*>(qr + 64 * s2 + 16 * g + 8);
+    }
+#pragma unroll
+    for (int s3 = 0; s3 < 2; s3++)
+      qf[16 + s3] = *reinterpret_cast<const f16x8*>(qr + 512 + 32 * s3 + 8 * g);
+  }
+  lds_barrier();
+
+  // ---- resolve idx -> cache row (masked keys and chunk padding: -1) ----
+  if (jk < kDmaSplitKeys) {
+    const int pg = (pos >= 0) ? pos / p.page_size : 0;
+    const bool ok = jk < nkeys && pos >= 0 && pos < seq_len && pg < p.max_blocks;
+    const int blk = ok ? (bt_in_lds ? sh.u.main.bt[pg] : bt_row[pg]) : -1;
+    const int64_t row = (int64_t)blk * p.page_size + (pos - pg * p.page_size);
+    sh.rows[jk] = (blk < 0 || row >= p.n_kv_rows) ? -1 : (int32_t)row;
+  }
+  lds_barrier();
+  if (nchunks > 0) dma_chunk(kv, sh.rows, sh.u.main.buf[0]);
+  if (nchunks > 1) dma_chunk(kv, sh.rows + kDmaKeys, sh.u.main.buf[1]);
+
+#pragma unroll
+  for (int s = 0; s < 18; s++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) qf[s][e] = (f16)((float)qf[s][e] * p.scale_h);
+
+  f32x4 oacc[kOTiles];
+#pragma unroll
+  for (int t = 0; t < kOTiles; t++) oacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float m_run = -1e30f, l_run = 0.f;
+  const int kbase = 16 * kw;  // this wave's keys inside each chunk
+
+  if (nchunks > 0) {
+    f32x4 ksc0[4], ksc1[4];
+    f32x4 sv0, sv1 = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    if (nchunks > 1)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaRounds) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    sv0 = dma_qk(sh.u.main.buf[0], kbase, sh.rows, qf, ksc0);
+    if (nchunks > 1) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      lds_barrier();
+      sv1 = dma_qk(sh.u.main.buf[1], kbase, sh.rows + kDmaKeys, qf, ksc1);
+    }
+    float mt = -1e30f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) mt = fmaxf(mt, fmaxf(sv0[r], sv1[r]));
+    mt = fmaxf(mt, shfl_xor_f(mt, 16));
+    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    m_run = mt;
+    float pr0[4], pr1[4], ls = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      pr0[r] = (sv0[r] > -INFINITY) ? __expf(sv0[r] - mt) : 0.f;
+      pr1[r] = (sv1[r] > -INFINITY) ? __expf(sv1[r] - mt) : 0.f;
+      ls += pr0[r] + pr1[r];
+    }
+    ls += shfl_xor_f(ls, 16);
+    ls += shfl_xor_f(ls, 32);
+    l_run = ls;
+    dma_pv(sh.u.main.buf[0], kbase, pr0, ksc0, oacc);
+    if (nchunks > 1) dma_pv(sh.u.main.buf[1], kbase, pr1, ksc1, oacc);
+  }
+
+  // ---- merge the 4 key-waves: wave w owns dims [128w, 128w+128) ----
+  constexpr int QT = kOTiles / 4;
+  lds_barrier();
+  if (g == 0) {
+    sh.m[kw * 16 + c] = m_run;
+    sh.l[kw * 16 + c] = l_run;
+  }
+  lds_barrier();
+  float M = -1e30f;
+#pragma unroll
+  for (int k2 = 0; k2 < 4; k2++) M = fmaxf(M, sh.m[k2 * 16 + c]);
+  float L = 0.f;
+#pragma unroll
+  for (int k2 = 0; k2 < 4; k2++) {
+    const float lk = sh.l[k2 * 16 + c];
+    L += (lk > 0.f) ? lk * __expf(sh.m[k2 * 16 + c] - M) : 0.f;
+  }
+  const float wgt = (l_run > 0.f) ? __expf(m_run - M) : 0.f;
+#pragma unroll
+  for (int t = 0; t < kOTiles; t++) {
+    const int qd = t / QT;
+    if (qd != kw) {
+      const int slot = kw < qd ? kw : kw - 1;
+      sh.u.xbuf[qd][slot][t % QT][lane] = oacc[t] * wgt;
+    }
+  }
+  lds_barrier();
+  const bool final_out = (p.n_splits == 1);
+  const int h = h0 + c;
+  const int64_t bh = (int64_t)b * p.n_head + h;
+  const float inv = (L > 0.f) ? 1.f / L : 0.f;
+#pragma unroll
+  for (int t = 0; t < kOTiles; t++) {
+    if (t / QT == kw) {
+      f32x4 v = oacc[t] * wgt;
+#pragma unroll
+      for (int sl = 0; sl < 3; sl++) v += sh.u.xbuf[kw][sl][t % QT][lane];
+      if (h < p.n_head) {
+        f16x4 o4;
+#pragma unroll
+        for (int r = 0; r < 4; r++) o4[r] = (f16)(v[r] * inv);
+        f16* dst = final_out ? p.o + bh * kValueDim
+                             : p.part_o + (bh * p.n_splits + split) * kValueDim;
+        *reinterpret_cast<f16x4*>(dst + 16 * t + 4 * g) = o4;
+      }
+    }
+  }
+  if (kw == 0 && g == 0 && h < p.n_head) {
+    if (final_out) {
+      p.lse[bh] = (L > 0.f) ? (M + logf(L)) : p.empty_lse;
+    } else {
+      const int64_t ps = bh * p.n_splits + split;
+      p.part_ml[ps * 2 + 0] = M;
+      p.part_ml[ps * 2 + 1] = L;
+    }
+  }
+}
+
 // Flash-decode merge of S partial states (reference :1138-1184):
 // m = max_s m_s, w_s = l_s > 0 ? exp(m_s - m) l_s : 0, o = sum w_s o_s / sum w_s
 // (o_s is the split's own normalised output, stored in fp16).
@@ -596,6 +917,24 @@ static bool use_prefill_config(int B, int n_head) {
   return (int64_t)B * ((n_head + 63) / 64) >= kTargetWGs;
 }
 
+// fp8 decode with LDS-DMA gathers: every split holds at most two 64-key
+// chunks, so the split count is raised to ceil(topk / 128) when needed.
+static bool use_dma_decode(int topk) {
+  return (topk + kDmaSplitKeys - 1) / kDmaSplitKeys <= kMergeMaxSplits;
+}
+
+static int dma_decode_splits(int B, int n_head, int topk) {
+  const int hg = (n_head + 15) / 16;
+  const int chunks = (topk + kDmaKeys - 1) / kDmaKeys;
+  int s = kTargetWGs / (B * hg > 0 ? B * hg : 1);
+  if (s >= 8) s = s / 8 * 8;  // a (token, split)'s head groups then share an XCD
+  const int min_s = (chunks + 1) / 2;  // <= 2 chunks per split
+  if (s < min_s) s = min_s;
+  if (s > chunks) s = chunks;
+  if (s < 1) s = 1;
+  return s;
+}
+
 static int decode_splits(int B, int n_head, int topk) {
   const int hg = (n_head + 15) / 16;
   const int tiles = (topk + 15) / 16;
@@ -626,10 +965,17 @@ static int launch_mla(const MlaParams& prm, dim3 grid, hipStream_t st) {
 
 using namespace mi355dsa;
 
+static int splits_for(int B, int n_head, int topk, int kv_fp8) {
+  return (kv_fp8 && use_dma_decode(topk)) ? dma_decode_splits(B, n_head, topk)
+                                          : decode_splits(B, n_head, topk);
+}
+
 extern "C" size_t mi355_dsa_sparse_mla_workspace_size(int B, int n_head, int topk) {
   if (B <= 0 || n_head <= 0 || topk <= 0) return 0;
   if (use_prefill_config(B, n_head)) return 0;
-  const int S = decode_splits(B, n_head, topk);
+  // the larger of the fp16 and fp8 split counts, so one size serves both
+  const int s16 = splits_for(B, n_head, topk, 0), s8 = splits_for(B, n_head, topk, 1);
+  const int S = s16 > s8 ? s16 : s8;
   if (S <= 1) return 0;
   return (size_t)B * n_head * S * (kValueDim * sizeof(f16) + 2 * sizeof(float));
 }
@@ -679,7 +1025,8 @@ extern "C" int mi355_dsa_sparse_mla_decode(
     return kv_fp8 ? launch_mla<true, 4, 1, 2>(prm, grid, st)
                   : launch_mla<false, 4, 1, 2>(prm, grid, st);
   }
-  const int S = decode_splits(B, n_head, topk);
+  const bool dma = kv_fp8 && use_dma_decode(topk);
+  const int S = splits_for(B, n_head, topk, kv_fp8);
   prm.n_splits = S;
   if (S > 1) {
     const size_t need = mi355_dsa_sparse_mla_workspace_size(B, n_head, topk);
@@ -690,8 +1037,20 @@ extern "C" int mi355_dsa_sparse_mla_decode(
     prm.part_ml = reinterpret_cast<float*>(prm.part_o + (size_t)B * n_head * S * kValueDim);
   }
   const dim3 grid(S, (n_head + 15) / 16, B);
-  int rc = kv_fp8 ? launch_mla<true, 1, kDecKW, 1>(prm, grid, st)
-                  : launch_mla<false, 1, kDecKW, 1>(prm, grid, st);
+  int rc;
+  if (dma) {
+    static bool attr = false;
+    if (!attr) {
+      hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_mla_decode_dma_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DmaSmem));
+      attr = true;
+    }
+    sparse_mla_decode_dma_kernel<<<grid, 256, sizeof(DmaSmem), st>>>(prm);
+    rc = check_launch("sparse_mla_decode");
+  } else {
+    rc = kv_fp8 ? launch_mla<true, 1, kDecKW, 1>(prm, grid, st)
+                : launch_mla<false, 1, kDecKW, 1>(prm, grid, st);
+  }
   if (rc != MI355_DSA_OK || S == 1) return rc;
   sparse_mla_merge_kernel<<<dim3((unsigned)((int64_t)B * n_head)), 128, 0, st>>>(
       prm.part_o, prm.part_ml, prm.o, prm.lse, S, prm.empty_lse);
