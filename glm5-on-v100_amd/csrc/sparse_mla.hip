@@ -72,6 +72,7 @@ struct MlaParams {
   f16* part_o;     // [B, H, S, 512] per-split normalised outputs o_s (S > 1)
   float* part_ml;  // [B, H, S, 2]   per-split (m_s, l_s)
   int B, n_head, topk, max_blocks, page_size, n_splits;
+  int page_shift;  // log2(page_size) when it is a power of two, else -1
   int64_t n_kv_rows;
   float scale_h;    // fp16-rounded softmax scale
   float empty_lse;  // lse of a (token, head) with no valid key
@@ -536,43 +537,52 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
 // ---------------------------------------------------------------------------
 // fp8_ds_mla split decode with LDS-DMA gathers.
 //
-// Workgroup = (split, 16-head group, token), 4 waves; every wave owns the
-// same 16 heads and takes 16 of each 64-key chunk.  Differences from the
-// register-staged kernel above, all aimed at the latency chain of a small
+// Workgroup = (split, 16-head group, token), 8 waves, at most two 64-key
+// chunks (128 keys) per split.  Aimed at the latency chain of a small
 // decode batch:
-//  * the block-table row of the token is staged in LDS together with the
-//    idx loads, so resolving idx -> cache row costs no second dependent
-//    global round trip;
+//  * Q rows, idx and the token's block-table row are fetched together (the
+//    block table is staged in LDS), so resolving idx -> cache row costs no
+//    second dependent global round trip;
 //  * rows are gathered with global_load_lds_dwordx4 straight into LDS as
-//    raw 656-B rows (no staging registers, no conversion pass), two chunks
+//    raw 656-B rows (no staging registers, no conversion pass), both chunks
 //    in flight; masked keys read a zero row, so they carry finite zeros;
-//  * scaled Q lives in registers in the k-slot order of the QK operands;
-//  * the e4m3 bytes are converted to exact fp16 at operand load: 16-byte
-//    reads for QK, ds_read_b64_tr_b8 for the V^T operands of PV (one
-//    transpose read gives two 16-dim tiles of 4 keys).
+//  * the e4m3 bytes become exact fp16 at operand load (16-byte reads for QK,
+//    ds_read_b64_tr_b8 transpose reads for the V^T operands of PV);
+//  * both chunks stay resident, so the softmax is exact two-phase:
+//      1. wave w computes S for keys 16(w%4) .. +15 of chunk w/4 (16 heads);
+//      2. split max / sum go through LDS and every wave writes its
+//         exp(S - M) into a [head][key] fp32 table;
+//      3. wave w computes O^T for value dims [64w, 64w+64) over all keys
+//         (v_mfma_f32_16x16x32_f16), so the waves' outputs are disjoint and
+//         need no merge; those dims lie in fp8 scale tile w/2, so P^T takes
+//         one scale per key.
 // Barriers that must not wait for in-flight gathers are raw s_barrier with
 // an explicit LDS wait (__syncthreads would also drain the LDS-DMA queue).
 // ---------------------------------------------------------------------------
-constexpr int kDmaKeys = 64;                                  // keys per chunk
-constexpr int kDmaPieces = kDmaKeys * (kDsmlaRowBytes / 16);  // 2624 16-B pieces
-constexpr int kDmaRounds = (kDmaPieces + 255) / 256;          // LDS-DMA ops per thread
-constexpr int kDmaBufBytes = kDmaRounds * 256 * 16;           // one chunk buffer
-constexpr int kBtStage = 4096;                                 // block-table entries in LDS
-constexpr int kDmaSplitKeys = 2 * kDmaKeys;                    // keys per split (max)
+constexpr int kDmaWaves = 8;
+constexpr int kDmaThreads = 64 * kDmaWaves;
+constexpr int kDmaKeys = 64;                                            // keys per chunk
+constexpr int kDmaPieces = kDmaKeys * (kDsmlaRowBytes / 16);            // 2624 16-B pieces
+constexpr int kDmaRounds = (kDmaPieces + kDmaThreads - 1) / kDmaThreads;  // 6 per thread
+constexpr int kDmaBufBytes = kDmaRounds * kDmaThreads * 16;             // one chunk buffer
+constexpr int kBtStage = 4096;                                           // block-table entries in LDS
+constexpr int kDmaSplitKeys = 2 * kDmaKeys;                              // keys per split (max)
+constexpr int kQPitchPieces = kLatentDim / 8 + 1;                        // 73 x 16 B: padded Q row
+constexpr int kQRounds = (16 * kQPitchPieces + kDmaThreads - 1) / kDmaThreads;  // 3
+constexpr int kPPitch = kDmaSplitKeys + 4;                               // fp32 P row pitch (floats)
+constexpr int kDimsPerWave = kValueDim / kDmaWaves;                      // 64
+constexpr int kTilesPerWave = kDimsPerWave / 16;                         // 4
 
 __device__ __align__(16) const uint8_t kZeroRow[kDsmlaRowBytes] = {};
 
 struct DmaSmem {
-  union {
-    struct {
-      uint8_t buf[2][kDmaBufBytes];
-      int32_t bt[kBtStage];
-    } main;
-    f32x4 xbuf[4][3][kOTiles / 4][64];  // key-wave merge (as MlaSmem, KW = 4)
-  } u;
+  uint8_t buf[2][kDmaBufBytes];          // raw rows of the split's two chunks
+  int32_t bt[kBtStage];                  // the token's block-table row
+  uint8_t q[kQRounds * kDmaThreads * 16];  // 16 Q rows (fp16, pitch 73 x 16 B)
+  float pt[16 * kPPitch];                // P[head][key] of the whole split
   int32_t rows[kDmaSplitKeys];
-  float m[4 * 16];
-  float l[4 * 16];
+  float m[kDmaWaves * 16];
+  float l[kDmaWaves * 16];
 };
 
 typedef int s32x2 __attribute__((ext_vector_type(2)));
@@ -592,35 +602,42 @@ __device__ __forceinline__ f16x4 e4m3x4_to_f16x4(uint32_t w) {
 }
 
 // Issues the LDS-DMA gather of one 64-key chunk (rows[0..64), -1 = masked)
-// into buf: piece q = 256u + 64*wave + lane lands at buf + 16q, i.e. key
+// into buf: piece q = 512u + 64*wave + lane lands at buf + 16q, i.e. key
 // q / 41, 16-byte chunk q % 41 of its 656-byte row.  Every thread issues
 // exactly kDmaRounds operations (padding pieces read the zero row).
 __device__ __forceinline__ void dma_chunk(const uint8_t* __restrict__ kv, const int32_t* rows,
                                           uint8_t* buf) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int row[kDmaRounds];
+#pragma unroll
+  for (int u = 0; u < kDmaRounds; u++) {  // all row lookups in flight together
+    const int q = kDmaThreads * u + 64 * wave + lane;
+    const int r = q / 41;
+    row[u] = rows[r < kDmaKeys ? r : 0];
+  }
 #pragma unroll
   for (int u = 0; u < kDmaRounds; u++) {
-    const int q = 256 * u + 64 * wave + lane;
+    const int q = kDmaThreads * u + 64 * wave + lane;
     const int r = q / 41, ch = q - r * 41;
-    const int row = (q < kDmaPieces) ? rows[r < kDmaKeys ? r : 0] : -1;
-    const uint8_t* src = (row >= 0) ? kv + (int64_t)row * kDsmlaRowBytes + 16 * ch
-                                    : kZeroRow + 16 * (q < kDmaPieces ? ch : 0);
-    __builtin_amdgcn_global_load_lds(src, (lds_void*)(buf + 16 * (256 * u + 64 * wave)), 16, 0,
-                                     0);
+    const bool ok = q < kDmaPieces && row[u] >= 0;
+    const uint8_t* src = ok ? kv + (int64_t)row[u] * kDsmlaRowBytes + 16 * ch
+                            : kZeroRow + 16 * (q < kDmaPieces ? ch : 0);
+    __builtin_amdgcn_global_load_lds(
+        src, (lds_void*)(buf + 16 * (kDmaThreads * u + 64 * wave)), 16, 0, 0);
   }
 }
 
 // QK of one wave's 16 keys of a chunk: returns the masked scores of keys
-// kbase + 4g + r (r = 0..3, accumulator rows) for head c, and their tile scales.
+// kbase + 4g + r (r = 0..3, accumulator rows) for head c.
 __device__ __forceinline__ f32x4 dma_qk(const uint8_t* cb, int kbase, const int32_t* rows,
-                                        const f16x8 (&qf)[18], f32x4 (&ksc)[4]) {
+                                        const f16x8 (&qf)[18]) {
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
   // All LDS operands are read first (in-order returns let each MFMA wait only
   // for its own operand).
   const uint8_t* krow = cb + (kbase + c) * kDsmlaRowBytes;
   u32x4 kraw[8];
   f16x8 krope[2];
-  int4 vr;
+  f32x4 ksc[4];
 #pragma unroll
   for (int s2 = 0; s2 < 8; s2++) kraw[s2] = *reinterpret_cast<const u32x4*>(krow + 64 * s2 + 16 * g);
 #pragma unroll
@@ -629,7 +646,7 @@ __device__ __forceinline__ f32x4 dma_qk(const uint8_t* cb, int kbase, const int3
 #pragma unroll
   for (int r = 0; r < 4; r++)
     ksc[r] = *reinterpret_cast<const f32x4*>(cb + (kbase + 4 * g + r) * kDsmlaRowBytes + 512);
-  vr = *reinterpret_cast<const int4*>(rows + kbase + 4 * g);
+  const int4 vr = *reinterpret_cast<const int4*>(rows + kbase + 4 * g);
   __builtin_amdgcn_sched_barrier(0);
   f32x4 acc[5];
 #pragma unroll
@@ -656,40 +673,11 @@ __device__ __forceinline__ f32x4 dma_qk(const uint8_t* cb, int kbase, const int3
   return sv;
 }
 
-// O^T += V^T (P x tile scale)^T for one wave's 16 keys of a chunk.
-__device__ __forceinline__ void dma_pv(const uint8_t* cb, int kbase, const float (&pr)[4],
-                                       const f32x4 (&ksc)[4], f32x4 (&oacc)[kOTiles]) {
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  // transpose read: lane i of a 16-lane group points at key
-  // kbase + 4g + (i/2)%4, dims 16*(2tt + i/8) + 8*(i%2); lane j then holds
-  // keys 4g..4g+3 at dim 32tt + j (bytes 0-3) and 32tt + 16 + j (bytes 4-7)
-  const uint8_t* vsrc =
-      cb + (kbase + 4 * g + ((c >> 1) & 3)) * kDsmlaRowBytes + 16 * (c >> 3) + 8 * (c & 1);
-  s32x2 vt[kOTiles / 2];
-#pragma unroll
-  for (int tt = 0; tt < kOTiles / 2; tt++)
-    vt[tt] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_s32x2*)(vsrc + 32 * tt));
-  f16x4 pb[4];
-#pragma unroll
-  for (int st = 0; st < 4; st++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) pb[st][r] = (f16)(pr[r] * ksc[r][st]);
-#pragma unroll
-  for (int tt = 0; tt < kOTiles / 2; tt++) {
-    const int st = tt >> 2;
-    oacc[2 * tt] = mfma16x16x16(e4m3x4_to_f16x4((uint32_t)vt[tt][0]), pb[st], oacc[2 * tt]);
-    oacc[2 * tt + 1] = mfma16x16x16(e4m3x4_to_f16x4((uint32_t)vt[tt][1]), pb[st], oacc[2 * tt + 1]);
-  }
-}
-
-// Decode for splits of at most two chunks (128 keys): both chunks are
-// resident in LDS, so each wave computes all its scores first and the
-// softmax needs no running rescale of O.
-__global__ void __launch_bounds__(256) sparse_mla_decode_dma_kernel(MlaParams p) {
+__global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   DmaSmem& sh = *reinterpret_cast<DmaSmem*>(smem_raw);
   const int lane = threadIdx.x & 63;
-  const int kw = threadIdx.x >> 6;
+  const int w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
   const int split = blockIdx.x, h0 = blockIdx.y * 16, b = blockIdx.z;
   const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
@@ -701,155 +689,172 @@ __global__ void __launch_bounds__(256) sparse_mla_decode_dma_kernel(MlaParams p)
   const int key_lo = min(split * cps * kDmaKeys, p.topk);
   const int nkeys = min(key_lo + cps * kDmaKeys, p.topk) - key_lo;
   const int nchunks = (nkeys + kDmaKeys - 1) / kDmaKeys;  // 0, 1 or 2
-  const bool bt_in_lds = p.max_blocks <= kBtStage;
+  const bool bt_in_lds = p.max_blocks >= 1 && p.max_blocks <= kBtStage;
   const int32_t* bt_row = p.bt + (int64_t)b * p.max_blocks;
 
-  // ---- independent loads: idx, block-table row, Q ----
-  static_assert(kDmaSplitKeys <= 256, "one key per thread");
+  // ---- independent loads: Q rows (LDS-DMA), idx, block-table row ----
+  {
+    const uint8_t* qb = reinterpret_cast<const uint8_t*>(p.q + (int64_t)b * p.n_head * kLatentDim);
+#pragma unroll
+    for (int u = 0; u < kQRounds; u++) {
+      const int q = kDmaThreads * u + 64 * w + lane;
+      const int r = q / kQPitchPieces, ch = q - r * kQPitchPieces;
+      const int hq = (r < 16 && h0 + r < p.n_head) ? h0 + r : h0;
+      const int chq = (r < 16 && ch < kLatentDim / 8) ? ch : 0;
+      __builtin_amdgcn_global_load_lds(qb + (int64_t)hq * kLatentDim * 2 + 16 * chq,
+                                       (lds_void*)(sh.q + 16 * (kDmaThreads * u + 64 * w)), 16,
+                                       0, 0);
+    }
+  }
+  static_assert(kDmaSplitKeys <= kDmaThreads, "one key per thread");
   const int jk = threadIdx.x;  // the key this thread resolves
   const int pos = (jk < nkeys) ? p.idx[(int64_t)b * p.topk + key_lo + jk] : -1;
   if (bt_in_lds) {
-    int btv[kBtStage / 256];
+    constexpr int BTU = kBtStage / kDmaThreads;
+    int btv[BTU];
 #pragma unroll
-    for (int u = 0; u < kBtStage / 256; u++) {
-      const int i = threadIdx.x + 256 * u;
-      btv[u] = (i < p.max_blocks) ? bt_row[i] : -1;
+    for (int u = 0; u < BTU; u++) {
+      const int i = threadIdx.x + kDmaThreads * u;
+      if (kDmaThreads * u < p.max_blocks) btv[u] = bt_row[i < p.max_blocks ? i : 0];
     }
 #pragma unroll
-    for (int u = 0; u < kBtStage / 256; u++) {
-      const int i = threadIdx.x + 256 * u;
-      if (i < p.max_blocks) sh.u.main.bt[i] = btv[u];
-    }
+    for (int u = 0; u < BTU; u++)
+      if (kDmaThreads * u < p.max_blocks) sh.bt[threadIdx.x + kDmaThreads * u] = btv[u];
   }
-  // Q fragments (B operand of S^T = K Q^T):
-  // step 2s'+e2 (s' < 8): lane group g holds dims 64s' + 16g + 8e2 .. +7
-  // step 16+s'':          lane group g holds dims 512 + 32s'' + 8g .. +7
-  f16x8 qf[18];
-  {
-    const int hq = h0 + c < p.n_head ? h0 + c : h0;
-    const f16* qr = p.q + ((int64_t)b * p.n_head + hq) * kLatentDim;
-#pragma unroll
-    for (int s2 = 0; s2 < 8; s2++) {
-      qf[2 * s2] = *reinterpret_cast<const f16x8*>(qr + 64 * s2 + 16 * g);
-      qf[2 * s2 + 1] = *reinterpret_cast<const f16x8*>(qr + 64 * s2 + 16 * g + 8);
-    }
-#pragma unroll
-    for (int s3 = 0; s3 < 2; s3++)
-      qf[16 + s3] = *reinterpret_cast<const f16x8*>(qr + 512 + 32 * s3 + 8 * g);
-  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   lds_barrier();
 
   // ---- resolve idx -> cache row (masked keys and chunk padding: -1) ----
   if (jk < kDmaSplitKeys) {
-    const int pg = (pos >= 0) ? pos / p.page_size : 0;
+    const int pg = (pos >= 0) ? (p.page_shift >= 0 ? pos >> p.page_shift : pos / p.page_size) : 0;
     const bool ok = jk < nkeys && pos >= 0 && pos < seq_len && pg < p.max_blocks;
-    const int blk = ok ? (bt_in_lds ? sh.u.main.bt[pg] : bt_row[pg]) : -1;
+    const int blk = ok ? (bt_in_lds ? sh.bt[pg] : bt_row[pg]) : -1;
     const int64_t row = (int64_t)blk * p.page_size + (pos - pg * p.page_size);
     sh.rows[jk] = (blk < 0 || row >= p.n_kv_rows) ? -1 : (int32_t)row;
   }
   lds_barrier();
-  if (nchunks > 0) dma_chunk(kv, sh.rows, sh.u.main.buf[0]);
-  if (nchunks > 1) dma_chunk(kv, sh.rows + kDmaKeys, sh.u.main.buf[1]);
+  if (nchunks > 0) dma_chunk(kv, sh.rows, sh.buf[0]);
+  if (nchunks > 1) dma_chunk(kv, sh.rows + kDmaKeys, sh.buf[1]);
 
+  // ---- Q fragments (B operand of S^T = K Q^T), scaled in fp16 ----
+  // step 2s'+e2 (s' < 8): lane group g holds dims 64s' + 16g + 8e2 .. +7
+  // step 16+s'':          lane group g holds dims 512 + 32s'' + 8g .. +7
+  f16x8 qf[18];
+  {
+    const f16* qr = reinterpret_cast<const f16*>(sh.q + c * kQPitchPieces * 16);
+    const f16 sc = (f16)p.scale_h;
+    const f16x8 sc8 = {sc, sc, sc, sc, sc, sc, sc, sc};
 #pragma unroll
-  for (int s = 0; s < 18; s++)
-#pragma unroll
-    for (int e = 0; e < 8; e++) qf[s][e] = (f16)((float)qf[s][e] * p.scale_h);
-
-  f32x4 oacc[kOTiles];
-#pragma unroll
-  for (int t = 0; t < kOTiles; t++) oacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float m_run = -1e30f, l_run = 0.f;
-  const int kbase = 16 * kw;  // this wave's keys inside each chunk
-
-  if (nchunks > 0) {
-    f32x4 ksc0[4], ksc1[4];
-    f32x4 sv0, sv1 = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    if (nchunks > 1)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaRounds) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    lds_barrier();
-    sv0 = dma_qk(sh.u.main.buf[0], kbase, sh.rows, qf, ksc0);
-    if (nchunks > 1) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      lds_barrier();
-      sv1 = dma_qk(sh.u.main.buf[1], kbase, sh.rows + kDmaKeys, qf, ksc1);
+    for (int s2 = 0; s2 < 8; s2++) {
+      qf[2 * s2] = *reinterpret_cast<const f16x8*>(qr + 64 * s2 + 16 * g) * sc8;
+      qf[2 * s2 + 1] = *reinterpret_cast<const f16x8*>(qr + 64 * s2 + 16 * g + 8) * sc8;
     }
-    float mt = -1e30f;
 #pragma unroll
-    for (int r = 0; r < 4; r++) mt = fmaxf(mt, fmaxf(sv0[r], sv1[r]));
-    mt = fmaxf(mt, shfl_xor_f(mt, 16));
-    mt = fmaxf(mt, shfl_xor_f(mt, 32));
-    m_run = mt;
-    float pr0[4], pr1[4], ls = 0.f;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      pr0[r] = (sv0[r] > -INFINITY) ? __expf(sv0[r] - mt) : 0.f;
-      pr1[r] = (sv1[r] > -INFINITY) ? __expf(sv1[r] - mt) : 0.f;
-      ls += pr0[r] + pr1[r];
-    }
-    ls += shfl_xor_f(ls, 16);
-    ls += shfl_xor_f(ls, 32);
-    l_run = ls;
-    dma_pv(sh.u.main.buf[0], kbase, pr0, ksc0, oacc);
-    if (nchunks > 1) dma_pv(sh.u.main.buf[1], kbase, pr1, ksc1, oacc);
+    for (int s3 = 0; s3 < 2; s3++)
+      qf[16 + s3] = *reinterpret_cast<const f16x8*>(qr + 512 + 32 * s3 + 8 * g) * sc8;
   }
 
-  // ---- merge the 4 key-waves: wave w owns dims [128w, 128w+128) ----
-  constexpr int QT = kOTiles / 4;
+  // ---- S for this wave's 16 keys: chunk w/4, keys 16(w%4) .. +15 ----
+  const int my_chunk = w >> 2, kbase = 16 * (w & 3);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   lds_barrier();
-  if (g == 0) {
-    sh.m[kw * 16 + c] = m_run;
-    sh.l[kw * 16 + c] = l_run;
-  }
-  lds_barrier();
-  float M = -1e30f;
+  f32x4 sv = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  if (my_chunk < nchunks)
+    sv = dma_qk(sh.buf[my_chunk], kbase, sh.rows + my_chunk * kDmaKeys, qf);
+
+  // ---- softmax statistics of the split (per head c) ----
+  float mt = -1e30f;
 #pragma unroll
-  for (int k2 = 0; k2 < 4; k2++) M = fmaxf(M, sh.m[k2 * 16 + c]);
+  for (int r = 0; r < 4; r++) mt = fmaxf(mt, sv[r]);
+  mt = fmaxf(mt, shfl_xor_f(mt, 16));
+  mt = fmaxf(mt, shfl_xor_f(mt, 32));
+  if (g == 0) sh.m[w * 16 + c] = mt;
+  lds_barrier();
+  float M = sh.m[c];
+#pragma unroll
+  for (int w2 = 1; w2 < kDmaWaves; w2++) M = fmaxf(M, sh.m[w2 * 16 + c]);
+  f32x4 pr;
+  float ls = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    pr[r] = (sv[r] > -INFINITY) ? __expf(sv[r] - M) : 0.f;
+    ls += pr[r];
+  }
+  ls += shfl_xor_f(ls, 16);
+  ls += shfl_xor_f(ls, 32);
+  if (g == 0) sh.l[w * 16 + c] = ls;
+  // P[head c][key]: keys 64 * my_chunk + kbase + 4g + r
+  *reinterpret_cast<f32x4*>(&sh.pt[c * kPPitch + my_chunk * kDmaKeys + kbase + 4 * g]) = pr;
+  lds_barrier();
   float L = 0.f;
 #pragma unroll
-  for (int k2 = 0; k2 < 4; k2++) {
-    const float lk = sh.l[k2 * 16 + c];
-    L += (lk > 0.f) ? lk * __expf(sh.m[k2 * 16 + c] - M) : 0.f;
-  }
-  const float wgt = (l_run > 0.f) ? __expf(m_run - M) : 0.f;
+  for (int w2 = 0; w2 < kDmaWaves; w2++) L += sh.l[w2 * 16 + c];
+
+  // ---- O^T[dims 64w .. +64][head] over the split's keys ----
+  const int st = (kDimsPerWave * w) / 128;  // fp8 scale tile of these dims
+  f32x4 oacc[kTilesPerWave];
 #pragma unroll
-  for (int t = 0; t < kOTiles; t++) {
-    const int qd = t / QT;
-    if (qd != kw) {
-      const int slot = kw < qd ? kw : kw - 1;
-      sh.u.xbuf[qd][slot][t % QT][lane] = oacc[t] * wgt;
+  for (int t = 0; t < kTilesPerWave; t++) oacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < kDmaSplitKeys / 32; kb++) {
+    if (kb * 32 >= nchunks * kDmaKeys) break;  // uniform
+    const uint8_t* cb = sh.buf[kb >> 1];
+    const int k0 = (kb & 1) * 32;  // first key of the block inside its chunk
+    // P^T operand: keys k0 + 8g + e of head c, times the key's scale of tile st
+    const f32x4 pa = *reinterpret_cast<const f32x4*>(&sh.pt[c * kPPitch + 32 * kb + 8 * g]);
+    const f32x4 pc = *reinterpret_cast<const f32x4*>(&sh.pt[c * kPPitch + 32 * kb + 8 * g + 4]);
+    float ks[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+      ks[e] = *reinterpret_cast<const float*>(cb + (k0 + 8 * g + e) * kDsmlaRowBytes + 512 + 4 * st);
+    // V^T transpose reads: lane i of a 16-lane group points at key
+    // k0 + 8g + i/2, dims 64w + 16t + 8(i%2); lane j receives the 8 keys
+    // k0 + 8g .. +7 at dim 64w + 16t + j
+    const uint8_t* vsrc =
+        cb + (k0 + 8 * g + (c >> 1)) * kDsmlaRowBytes + kDimsPerWave * w + 8 * (c & 1);
+    s32x2 vt[kTilesPerWave];
+#pragma unroll
+    for (int t = 0; t < kTilesPerWave; t++)
+      vt[t] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_s32x2*)(vsrc + 16 * t));
+    f16x8 pb;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      pb[e] = (f16)(pa[e] * ks[e]);
+      pb[4 + e] = (f16)(pc[e] * ks[4 + e]);
+    }
+#pragma unroll
+    for (int t = 0; t < kTilesPerWave; t++) {
+      const f16x4 lo = e4m3x4_to_f16x4((uint32_t)vt[t][0]);
+      const f16x4 hi = e4m3x4_to_f16x4((uint32_t)vt[t][1]);
+      const f16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      oacc[t] = mfma16x16x32(av, pb, oacc[t]);
     }
   }
-  lds_barrier();
+
+  // ---- outputs: rows 4g + r of tile t are dims 64w + 16t + 4g + r ----
   const bool final_out = (p.n_splits == 1);
   const int h = h0 + c;
   const int64_t bh = (int64_t)b * p.n_head + h;
   const float inv = (L > 0.f) ? 1.f / L : 0.f;
+  if (h < p.n_head) {
+    f16* dst = final_out ? p.o + bh * kValueDim : p.part_o + (bh * p.n_splits + split) * kValueDim;
 #pragma unroll
-  for (int t = 0; t < kOTiles; t++) {
-    if (t / QT == kw) {
-      f32x4 v = oacc[t] * wgt;
+    for (int t = 0; t < kTilesPerWave; t++) {
+      f16x4 o4;
 #pragma unroll
-      for (int sl = 0; sl < 3; sl++) v += sh.u.xbuf[kw][sl][t % QT][lane];
-      if (h < p.n_head) {
-        f16x4 o4;
-#pragma unroll
-        for (int r = 0; r < 4; r++) o4[r] = (f16)(v[r] * inv);
-        f16* dst = final_out ? p.o + bh * kValueDim
-                             : p.part_o + (bh * p.n_splits + split) * kValueDim;
-        *reinterpret_cast<f16x4*>(dst + 16 * t + 4 * g) = o4;
-      }
+      for (int r = 0; r < 4; r++) o4[r] = (f16)(oacc[t][r] * inv);
+      // streaming store: the partials are read once, by the merge kernel
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x2, o4),
+                                  reinterpret_cast<u32x2*>(dst + kDimsPerWave * w + 16 * t + 4 * g));
     }
-  }
-  if (kw == 0 && g == 0 && h < p.n_head) {
-    if (final_out) {
-      p.lse[bh] = (L > 0.f) ? (M + logf(L)) : p.empty_lse;
-    } else {
-      const int64_t ps = bh * p.n_splits + split;
-      p.part_ml[ps * 2 + 0] = M;
-      p.part_ml[ps * 2 + 1] = L;
+    if (w == 0 && g == 0) {
+      if (final_out) {
+        p.lse[bh] = (L > 0.f) ? (M + logf(L)) : p.empty_lse;
+      } else {
+        const int64_t ps = bh * p.n_splits + split;
+        p.part_ml[ps * 2 + 0] = M;
+        p.part_ml[ps * 2 + 1] = L;
+      }
     }
   }
 }
@@ -1012,6 +1017,7 @@ extern "C" int mi355_dsa_sparse_mla_decode(
   prm.topk = topk;
   prm.max_blocks = max_blocks;
   prm.page_size = page_size;
+  prm.page_shift = (page_size & (page_size - 1)) == 0 ? ilog2_pow2(page_size) : -1;
   prm.n_kv_rows = n_kv_rows;
   prm.scale_h = (float)(f16)scale;
   // the reference's prefill kernel (taken for B >= 32 && n_head <= 16,
@@ -1045,7 +1051,7 @@ extern "C" int mi355_dsa_sparse_mla_decode(
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DmaSmem));
       attr = true;
     }
-    sparse_mla_decode_dma_kernel<<<grid, 256, sizeof(DmaSmem), st>>>(prm);
+    sparse_mla_decode_dma_kernel<<<grid, kDmaThreads, sizeof(DmaSmem), st>>>(prm);
     rc = check_launch("sparse_mla_decode");
   } else {
     rc = kv_fp8 ? launch_mla<true, 1, kDecKW, 1>(prm, grid, st)
