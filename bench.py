@@ -67,6 +67,9 @@ def parse():
     p.add_argument("--layers", type=int, default=78)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="only the headline decode")
+    p.add_argument("--extra", default="all",
+                   help="comma list of extra records: sweep, indexer_prefill, sparse_prefill, "
+                        "indexer_decode, gemv, k_store (default all)")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--calib-copy-mib", type=int, default=0,
                    help="run one device copy of this many MiB first (a known-size "
@@ -166,6 +169,69 @@ def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
     flops = 8192.0 * T * (T + 1) / 2
     del graph
     return ms, flops
+
+
+SPARSE_PREFILL_T = 65536
+EXTRAS = ("sweep", "indexer_prefill", "sparse_prefill", "indexer_decode", "gemv", "k_store")
+
+
+def sparse_prefill_flops(T=SPARSE_PREFILL_T, topk=2048, heads=64):
+    keys = sum(min(t + 1, topk) for t in range(T))
+    return keys * heads * (576 + 512) * 2, keys
+
+
+def bench_sparse_prefill(torch, pkg, dev, fp8=True, T=SPARSE_PREFILL_T, sub=4096, steps=2):
+    """Config C4 sparse MLA prefill: one 64k-token causal sequence, 64 heads,
+    top-2048 keys per token (causally masked: token t selects min(t+1, 2048)
+    distinct positions < t+1), latent cache of the sequence (MALL-resident),
+    run in 4096-token launches of the op (B = 4096 takes the 64-head prefill
+    configuration).  FLOPs count only the selected keys."""
+    S = pkg.synthetic
+    ops = pkg._sm70_ops
+    page = 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    npg = T // page
+    kv = S.latent_cache(T, fp8, g, dev)
+    bt_row = torch.randperm(npg, generator=g, device=dev).to(torch.int32)
+    bt = bt_row[None].expand(sub, npg).contiguous()
+    q = (torch.randn(sub, 64, 576, generator=g, device=dev) / 24.0).to(torch.float16)
+    j = torch.arange(2048, device=dev, dtype=torch.float64)
+    chunks = []
+    for lo in range(0, T, sub):
+        t = torch.arange(lo, lo + sub, device=dev, dtype=torch.float64)
+        n = t + 1
+        u = torch.rand(sub, 1, generator=g, device=dev, dtype=torch.float64)
+        spread = torch.floor((j[None] + u) * n[:, None] / 2048.0)
+        idx = torch.where(n[:, None] <= 2048, torch.where(j[None] < n[:, None], j[None], -1.0), spread)
+        chunks.append((idx.to(torch.int32), (t + 1).to(torch.int32)))
+    o = torch.empty(sub, 64, 512, dtype=torch.float16, device=dev)
+    lse = torch.empty(sub, 64, device=dev)
+    scale = 576 ** -0.5
+
+    def run():
+        for idx, seq in chunks:
+            ops.sm70_sparse_mla_decode(o, lse, q, kv, idx, bt, seq, scale)
+
+    run()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        run()
+    e1.record(st)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all()
+    ms = e0.elapsed_time(e1) / steps
+    flops, keys = sparse_prefill_flops(T)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"tflops": round(tf, 2), "ms": round(ms, 3), "flops": flops, "selected_keys": keys,
+            "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4),
+            "workload": ("65536-token causal prefill, 64 heads, qk 576 / v 512, top-2048 per "
+                         "token, %s latent cache, 4096-token launches, selected-key FLOPs only"
+                         % ("fp8_ds_mla" if fp8 else "fp16"))}
 
 
 def graph_time_per_call(torch, fn, n_calls, steps=10, warmup=2):
@@ -357,7 +423,10 @@ def main():
         },
     }
 
-    if not args.no_extra:
+    extras = set(EXTRAS if args.extra == "all" else args.extra.split(","))
+    if args.no_extra:
+        extras = set()
+    if "sweep" in extras:
         sweep = {}
         for ctx in (4096, 16384, 65536):
             ms_c, *_ = bench_decode(torch, pkg, dev, ctx, L, max(args.steps // 2, 3),
@@ -367,6 +436,7 @@ def main():
         sweep["184320"] = line["value"]
         line["ctx_sweep_us_per_layer"] = sweep
         log(f"ctx sweep: {sweep}")
+    if "indexer_prefill" in extras:
         pms, pflops = bench_indexer_prefill(torch, pkg, dev)
         ptf = pflops / (pms * 1e-3) / 1e12
         line["indexer_prefill"] = {
@@ -379,11 +449,20 @@ def main():
         }
         log(f"indexer prefill: {ptf:.1f} TFLOPS ({pms:.2f} ms)")
         torch.cuda.empty_cache()
+    if "sparse_prefill" in extras:
+        for fp8 in (True, False):
+            key = "sparse_prefill_fp8" if fp8 else "sparse_prefill_fp16"
+            line[key] = bench_sparse_prefill(torch, pkg, dev, fp8=fp8)
+            log(f"sparse prefill ({key}): {line[key]['tflops']} TFLOPS ({line[key]['ms']} ms)")
+            torch.cuda.empty_cache()
+    if "indexer_decode" in extras:
         line["indexer_decode_topk"] = bench_indexer_decode(torch, pkg, dev)
         log(f"indexer decode: {line['indexer_decode_topk']}")
         torch.cuda.empty_cache()
+    if "gemv" in extras:
         line["fp8_gemv"] = bench_gemv(torch, pkg, dev)
         log(f"fp8 gemv: {line['fp8_gemv']}")
+    if "k_store" in extras:
         line["k_store"] = bench_k_store(torch, pkg, dev)
         log(f"k store: {line['k_store']}")
         torch.cuda.empty_cache()
