@@ -859,6 +859,291 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp8_ds_mla prefill with an LDS-DMA ring.
+//
+// Workgroup = one token x 64 heads, 8 waves (two per SIMD).  The token's
+// rows are resolved once, then 32-key tiles stream through a ring of
+// kPfRing LDS slots filled by global_load_lds_dwordx4, so up to kPfRing
+// tiles of gather latency are hidden behind the MFMA work on the others.
+// Wave w = (head group w%4, half w/4):
+//   * QK: S for keys [16 half, +16) of the tile and the group's 16 heads;
+//   * the pair of waves of a head group exchange tile maxima and exp(S - m)
+//     through LDS;
+//   * PV: O^T for value dims [256 half, +256) over all 32 keys of the tile
+//     (v_mfma_f32_16x16x32_f16; k-slots 0-3 = keys 4g..4g+3, 4-7 =
+//     16+4g..16+4g+3, V^T by 8-row transpose reads).
+// The softmax is online with a lazy running max shared by the pair: O and
+// l are rescaled only when a head's tile max exceeds the running max by more
+// than kPfLazyMax, so p = exp(s - m) <= e^8 (well inside fp16) and rescales
+// are rare; o = O / l and lse = m + ln l are unchanged by the choice of m.
+// ---------------------------------------------------------------------------
+constexpr int kPfWaves = 8;
+constexpr int kPfThreads = 64 * kPfWaves;
+constexpr int kPfTileKeys = 32;
+constexpr int kPfPieces = kPfTileKeys * (kDsmlaRowBytes / 16);          // 1312
+constexpr int kPfRounds = (kPfPieces + kPfThreads - 1) / kPfThreads;    // 3 LDS-DMA ops per thread
+constexpr int kPfSlotBytes = kPfRounds * kPfThreads * 16;
+constexpr int kPfRing = 5;
+constexpr int kPfPPitch = kPfTileKeys + 4;  // fp32 P row pitch (floats)
+constexpr float kPfLazyMax = 8.0f;
+
+struct PfSmem {
+  uint8_t ring[kPfRing][kPfSlotBytes];
+  int32_t rows[kSegKeys];
+  float pt[4][16 * kPfPPitch];  // per head group: P[head][tile key]
+  float tmax[kPfWaves * 16];
+  float lsum[kPfWaves * 16];
+};
+
+// LDS-DMA gather of one 32-key tile (rows[0..32), -1 = masked) into a slot.
+__device__ __forceinline__ void pf_dma_tile(const uint8_t* __restrict__ kv, const int32_t* rows,
+                                            uint8_t* slot) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int row[kPfRounds];
+#pragma unroll
+  for (int u = 0; u < kPfRounds; u++) {
+    const int q = kPfThreads * u + 64 * wave + lane;
+    const int r = q / 41;
+    row[u] = rows[r < kPfTileKeys ? r : 0];
+  }
+#pragma unroll
+  for (int u = 0; u < kPfRounds; u++) {
+    const int q = kPfThreads * u + 64 * wave + lane;
+    const int r = q / 41, ch = q - r * 41;
+    const bool ok = q < kPfPieces && row[u] >= 0;
+    const uint8_t* src = ok ? kv + (int64_t)row[u] * kDsmlaRowBytes + 16 * ch
+                            : kZeroRow + 16 * (q < kPfPieces ? ch : 0);
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)(slot + 16 * (kPfThreads * u + 64 * wave)),
+                                     16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void pf_wait(int k) {  // at most k tiles still in flight
+  switch (k) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(1 * kPfRounds) : "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kPfRounds) : "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * kPfRounds) : "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kPfRounds) : "memory"); break;
+  }
+}
+static_assert(kPfRing <= 5, "pf_wait covers up to 4 tiles in flight");
+
+__global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_dma_kernel(MlaParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  PfSmem& sh = *reinterpret_cast<PfSmem*>(smem_raw);
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int hg = w & 3, half = w >> 2;
+  const int c = lane & 15, g = lane >> 4;
+  // XCD-aware token order: consecutive tokens (overlapping top-k sets) share an XCD
+  int b;
+  {
+    const int nx = gridDim.x, bid = blockIdx.x;
+    const int xcd = bid & 7, j = bid >> 3;
+    const int per = nx >> 3, rem = nx & 7;
+    b = xcd * per + (xcd < rem ? xcd : rem) + j;
+  }
+  const int h0 = blockIdx.y * 64 + 16 * hg;
+  const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
+  const int seq_len = p.seq_lens[b];
+
+  // ---- Q fragments of the head group, k-slot order of dma_qk ----
+  f16x8 qf[18];
+  {
+    const int hq = h0 + c < p.n_head ? h0 + c : 0;
+    const f16* qr = p.q + ((int64_t)b * p.n_head + hq) * kLatentDim;
+    const f16 sc = (f16)p.scale_h;
+    const f16x8 sc8 = {sc, sc, sc, sc, sc, sc, sc, sc};
+#pragma unroll
+    for (int s2 = 0; s2 < 8; s2++) {
+      qf[2 * s2] = *reinterpret_cast<const f16x8*>(qr + 64 * s2 + 16 * g) * sc8;
+      qf[2 * s2 + 1] = *reinterpret_cast<const f16x8*>(qr + 64 * s2 + 16 * g + 8) * sc8;
+    }
+#pragma unroll
+    for (int s3 = 0; s3 < 2; s3++)
+      qf[16 + s3] = *reinterpret_cast<const f16x8*>(qr + 512 + 32 * s3 + 8 * g) * sc8;
+  }
+
+  constexpr int NT = kOTiles / 2;  // 16 O^T tiles: dims 256 half + 16t
+  f32x4 oacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) oacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float m_run = -1e30f, l_run = 0.f;  // l_run: this wave's keys only
+  bool first = true;
+  float* ptab = sh.pt[hg];
+
+  for (int seg_lo = 0; seg_lo < p.topk; seg_lo += kSegKeys) {
+    const int nkeys = min(p.topk - seg_lo, kSegKeys);
+    const int ntiles = (nkeys + kPfTileKeys - 1) / kPfTileKeys;
+    lds_barrier();  // previous segment done with rows and the ring
+    // ---- resolve idx -> block table -> row for the segment, batched ----
+    for (int base = 0; base < ntiles * kPfTileKeys; base += kPfThreads * kResU) {
+      int pos[kResU], pg[kResU], blk[kResU];
+#pragma unroll
+      for (int u = 0; u < kResU; u++) {
+        const int j = base + u * kPfThreads + (int)threadIdx.x;
+        pos[u] = (j < nkeys) ? p.idx[(int64_t)b * p.topk + seg_lo + j] : -1;
+      }
+      resolve_bt<kPfThreads>(p, b, seq_len, pos, pg, blk);
+#pragma unroll
+      for (int u = 0; u < kResU; u++) {
+        const int j = base + u * kPfThreads + (int)threadIdx.x;
+        if (j < ntiles * kPfTileKeys) {
+          const int64_t row = (int64_t)blk[u] * p.page_size + (pos[u] - pg[u] * p.page_size);
+          sh.rows[j] = (blk[u] < 0 || row >= p.n_kv_rows) ? -1 : (int32_t)row;
+        }
+      }
+    }
+    lds_barrier();
+    // kPfRing - 1 tiles ahead; the last slot is refilled at the top of each
+    // iteration with the slot the previous tile used
+    const int ahead = min(kPfRing - 1, ntiles);
+    for (int i = 0; i < ahead; i++) pf_dma_tile(kv, sh.rows + i * kPfTileKeys, sh.ring[i]);
+
+    for (int i = 0; i < ntiles; i++) {
+      pf_wait(min(ntiles, kPfRing - 1 + i) - 1 - i);
+      lds_barrier();  // tile i landed; every wave is done with tile i - 1
+      if (i + kPfRing - 1 < ntiles)
+        pf_dma_tile(kv, sh.rows + (i + kPfRing - 1) * kPfTileKeys,
+                    sh.ring[(i + kPfRing - 1) % kPfRing]);
+      const uint8_t* cb = sh.ring[i % kPfRing];
+      const int32_t* trows = sh.rows + i * kPfTileKeys;
+
+      // ---- S^T for keys [16 half, +16) ----
+      f32x4 sv;
+      {
+        const int kbase = 16 * half;
+        const uint8_t* krow = cb + (kbase + c) * kDsmlaRowBytes;
+        u32x4 kraw[8];
+        f16x8 krope[2];
+        f32x4 ksc[4];
+#pragma unroll
+        for (int s2 = 0; s2 < 8; s2++)
+          kraw[s2] = *reinterpret_cast<const u32x4*>(krow + 64 * s2 + 16 * g);
+#pragma unroll
+        for (int s3 = 0; s3 < 2; s3++)
+          krope[s3] = *reinterpret_cast<const f16x8*>(krow + 528 + 64 * s3 + 16 * g);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          ksc[r] = *reinterpret_cast<const f32x4*>(cb + (kbase + 4 * g + r) * kDsmlaRowBytes + 512);
+        const int4 vr = *reinterpret_cast<const int4*>(trows + kbase + 4 * g);
+        f32x4 acc[5];
+#pragma unroll
+        for (int a = 0; a < 5; a++) acc[a] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s2 = 0; s2 < 8; s2++) {
+          const f16x4 a0 = e4m3x4_to_f16x4(kraw[s2][0]), a1 = e4m3x4_to_f16x4(kraw[s2][1]);
+          const f16x4 a2 = e4m3x4_to_f16x4(kraw[s2][2]), a3 = e4m3x4_to_f16x4(kraw[s2][3]);
+          const f16x8 k0 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+          const f16x8 k1 = {a2[0], a2[1], a2[2], a2[3], a3[0], a3[1], a3[2], a3[3]};
+          acc[s2 >> 1] = mfma16x16x32(k0, qf[2 * s2], acc[s2 >> 1]);
+          acc[s2 >> 1] = mfma16x16x32(k1, qf[2 * s2 + 1], acc[s2 >> 1]);
+        }
+#pragma unroll
+        for (int s3 = 0; s3 < 2; s3++) acc[4] = mfma16x16x32(krope[s3], qf[16 + s3], acc[4]);
+        const int vv[4] = {vr.x, vr.y, vr.z, vr.w};
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float v = acc[4][r] + ksc[r][0] * acc[0][r] + ksc[r][1] * acc[1][r] +
+                          ksc[r][2] * acc[2][r] + ksc[r][3] * acc[3][r];
+          sv[r] = vv[r] >= 0 ? v : -INFINITY;
+        }
+      }
+      // ---- tile max of the head group (both halves) ----
+      float mt = -1e30f;
+#pragma unroll
+      for (int r = 0; r < 4; r++) mt = fmaxf(mt, sv[r]);
+      mt = fmaxf(mt, shfl_xor_f(mt, 16));
+      mt = fmaxf(mt, shfl_xor_f(mt, 32));
+      if (g == 0) sh.tmax[w * 16 + c] = mt;
+      lds_barrier();
+      mt = fmaxf(sh.tmax[hg * 16 + c], sh.tmax[(hg + 4) * 16 + c]);
+      // lazy running max (the pair sees the same values, so both decide alike)
+      if (__any(mt > m_run + kPfLazyMax)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = __expf(m_run - m_new);
+        l_run *= alpha;
+        m_run = m_new;
+        if (!first) {
+#pragma unroll
+          for (int t = 0; t < NT; t++) oacc[t] *= alpha;
+        }
+      }
+      first = false;
+      f32x4 pr;
+      float ls = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        pr[r] = (sv[r] > -INFINITY) ? __expf(sv[r] - m_run) : 0.f;
+        ls += pr[r];
+      }
+      ls += shfl_xor_f(ls, 16);
+      ls += shfl_xor_f(ls, 32);
+      l_run += ls;
+      *reinterpret_cast<f32x4*>(&ptab[c * kPfPPitch + 16 * half + 4 * g]) = pr;
+      lds_barrier();
+
+      // ---- O^T[dims 256 half + .. ] += V^T (P x tile scale)^T ----
+      const f32x4 p0 = *reinterpret_cast<const f32x4*>(&ptab[c * kPfPPitch + 4 * g]);
+      const f32x4 p1 = *reinterpret_cast<const f32x4*>(&ptab[c * kPfPPitch + 16 + 4 * g]);
+      // scales of this half's two tiles (2 half, 2 half + 1) for keys 4g+r, 16+4g+r
+      f32x2 s0[4], s1[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        s0[r] = *reinterpret_cast<const f32x2*>(cb + (4 * g + r) * kDsmlaRowBytes + 512 + 8 * half);
+        s1[r] = *reinterpret_cast<const f32x2*>(cb + (16 + 4 * g + r) * kDsmlaRowBytes + 512 + 8 * half);
+      }
+      f16x8 pb[2];
+#pragma unroll
+      for (int sl = 0; sl < 2; sl++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          pb[sl][r] = (f16)(p0[r] * s0[r][sl]);
+          pb[sl][4 + r] = (f16)(p1[r] * s1[r][sl]);
+        }
+      // transpose source: lane i of a 16-lane group points at row i/2 of
+      // {4g..4g+3, 16+4g..16+4g+3}, bytes 256 half + 16t + 8(i%2)
+      const int vkey = ((c >> 1) < 4) ? 4 * g + (c >> 1) : 16 + 4 * g + ((c >> 1) - 4);
+      const uint8_t* vsrc = cb + vkey * kDsmlaRowBytes + 256 * half + 8 * (c & 1);
+#pragma unroll
+      for (int t0 = 0; t0 < NT; t0 += 8) {
+        s32x2 vt[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+          vt[t] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_s32x2*)(vsrc + 16 * (t0 + t)));
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          const f16x4 lo = e4m3x4_to_f16x4((uint32_t)vt[t][0]);
+          const f16x4 hi = e4m3x4_to_f16x4((uint32_t)vt[t][1]);
+          const f16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          oacc[t0 + t] = mfma16x16x32(av, pb[(t0 + t) >> 3], oacc[t0 + t]);
+        }
+      }
+    }
+  }
+
+  // ---- l over both halves, then o = O / l for dims 256 half + 16t + 4g + r ----
+  if (g == 0) sh.lsum[w * 16 + c] = l_run;
+  lds_barrier();
+  const float L = sh.lsum[hg * 16 + c] + sh.lsum[(hg + 4) * 16 + c];
+  const int h = h0 + c;
+  if (h < p.n_head) {
+    const int64_t bh = (int64_t)b * p.n_head + h;
+    if (half == 0 && g == 0) p.lse[bh] = (L > 0.f) ? (m_run + logf(L)) : p.empty_lse;
+    const float inv = (L > 0.f) ? 1.f / L : 0.f;
+    f16* orow = p.o + bh * kValueDim + 256 * half;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      f16x4 v;
+#pragma unroll
+      for (int r = 0; r < 4; r++) v[r] = (f16)(oacc[t][r] * inv);
+      *reinterpret_cast<f16x4*>(orow + 16 * t + 4 * g) = v;
+    }
+  }
+}
+
 // Flash-decode merge of S partial states (reference :1138-1184):
 // m = max_s m_s, w_s = l_s > 0 ? exp(m_s - m) l_s : 0, o = sum w_s o_s / sum w_s
 // (o_s is the split's own normalised output, stored in fp16).
@@ -1028,8 +1313,17 @@ extern "C" int mi355_dsa_sparse_mla_decode(
   if (use_prefill_config(B, n_head)) {
     prm.n_splits = 1;
     const dim3 grid(B, (n_head + 63) / 64);
-    return kv_fp8 ? launch_mla<true, 4, 1, 2>(prm, grid, st)
-                  : launch_mla<false, 4, 1, 2>(prm, grid, st);
+    if (kv_fp8) {
+      static bool pattr = false;
+      if (!pattr) {
+        hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_mla_prefill_dma_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(PfSmem));
+        pattr = true;
+      }
+      sparse_mla_prefill_dma_kernel<<<grid, kPfThreads, sizeof(PfSmem), st>>>(prm);
+      return check_launch("sparse_mla_decode");
+    }
+    return launch_mla<false, 4, 1, 2>(prm, grid, st);
   }
   const bool dma = kv_fp8 && use_dma_decode(topk);
   const int S = splits_for(B, n_head, topk, kv_fp8);
