@@ -593,6 +593,16 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// global_load_lds_dwordx4: lane l's 16 bytes at gptr land at lds + 16 l (the
+// LDS base goes through M0, so it must be wave-uniform).  Issued as inline
+// asm so the compiler does not treat every later LDS read as depending on
+// the gathers in flight (it would otherwise wait for all of them): callers
+// wait for completion themselves with s_waitcnt vmcnt before a barrier.
+__device__ __forceinline__ void dma16(const void* gptr, const void* lds) {
+  const uint32_t off = (uint32_t)(uintptr_t)lds;
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(off) : "memory");
+}
+
 // 4 e4m3 bytes -> 4 exact fp16 values
 __device__ __forceinline__ f16x4 e4m3x4_to_f16x4(uint32_t w) {
   const f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, false);
@@ -622,22 +632,22 @@ __device__ __forceinline__ void dma_chunk(const uint8_t* __restrict__ kv, const 
     const bool ok = q < kDmaPieces && row[u] >= 0;
     const uint8_t* src = ok ? kv + (int64_t)row[u] * kDsmlaRowBytes + 16 * ch
                             : kZeroRow + 16 * (q < kDmaPieces ? ch : 0);
-    __builtin_amdgcn_global_load_lds(
-        src, (lds_void*)(buf + 16 * (kDmaThreads * u + 64 * wave)), 16, 0, 0);
+    dma16(src, buf + 16 * (kDmaThreads * u + 64 * wave));
   }
 }
 
-// QK of one wave's 16 keys of a chunk: returns the masked scores of keys
-// kbase + 4g + r (r = 0..3, accumulator rows) for head c.
+// QK of one wave's 16 keys of a chunk of raw fp8_ds_mla rows: returns the
+// masked scores of keys kbase + 4g + r (r = 0..3, accumulator rows) for head
+// c, and in ksc those keys' four tile scales.
+template <bool BATCH_ALL = true>
 __device__ __forceinline__ f32x4 dma_qk(const uint8_t* cb, int kbase, const int32_t* rows,
-                                        const f16x8 (&qf)[18]) {
+                                        const f16x8 (&qf)[18], f32x4 (&ksc)[4]) {
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
   // All LDS operands are read first (in-order returns let each MFMA wait only
   // for its own operand).
   const uint8_t* krow = cb + (kbase + c) * kDsmlaRowBytes;
   u32x4 kraw[8];
   f16x8 krope[2];
-  f32x4 ksc[4];
 #pragma unroll
   for (int s2 = 0; s2 < 8; s2++) kraw[s2] = *reinterpret_cast<const u32x4*>(krow + 64 * s2 + 16 * g);
 #pragma unroll
@@ -647,21 +657,27 @@ __device__ __forceinline__ f32x4 dma_qk(const uint8_t* cb, int kbase, const int3
   for (int r = 0; r < 4; r++)
     ksc[r] = *reinterpret_cast<const f32x4*>(cb + (kbase + 4 * g + r) * kDsmlaRowBytes + 512);
   const int4 vr = *reinterpret_cast<const int4*>(rows + kbase + 4 * g);
-  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (BATCH_ALL) __builtin_amdgcn_sched_barrier(0);
   f32x4 acc[5];
 #pragma unroll
   for (int a = 0; a < 5; a++) acc[a] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // step order interleaves the accumulators (consecutive MFMAs independent):
+  // read pair s2 holds steps 2s2, 2s2+1 of scale tile s2/2
 #pragma unroll
-  for (int s2 = 0; s2 < 8; s2++) {
-    const f16x4 a0 = e4m3x4_to_f16x4(kraw[s2][0]), a1 = e4m3x4_to_f16x4(kraw[s2][1]);
-    const f16x4 a2 = e4m3x4_to_f16x4(kraw[s2][2]), a3 = e4m3x4_to_f16x4(kraw[s2][3]);
-    const f16x8 k0 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-    const f16x8 k1 = {a2[0], a2[1], a2[2], a2[3], a3[0], a3[1], a3[2], a3[3]};
-    acc[s2 >> 1] = mfma16x16x32(k0, qf[2 * s2], acc[s2 >> 1]);
-    acc[s2 >> 1] = mfma16x16x32(k1, qf[2 * s2 + 1], acc[s2 >> 1]);
+  for (int j = 0; j < 2; j++) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const int s2 = 2 * t + j;
+      const f16x4 a0 = e4m3x4_to_f16x4(kraw[s2][0]), a1 = e4m3x4_to_f16x4(kraw[s2][1]);
+      const f16x4 a2 = e4m3x4_to_f16x4(kraw[s2][2]), a3 = e4m3x4_to_f16x4(kraw[s2][3]);
+      const f16x8 k0 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      const f16x8 k1 = {a2[0], a2[1], a2[2], a2[3], a3[0], a3[1], a3[2], a3[3]};
+      acc[t] = mfma16x16x32(k0, qf[2 * s2], acc[t]);
+      acc[4] = (j == 0 && t == 1) ? mfma16x16x32(krope[0], qf[16], acc[4])
+             : (j == 1 && t == 1) ? mfma16x16x32(krope[1], qf[17], acc[4]) : acc[4];
+      acc[t] = mfma16x16x32(k1, qf[2 * s2 + 1], acc[t]);
+    }
   }
-#pragma unroll
-  for (int s3 = 0; s3 < 2; s3++) acc[4] = mfma16x16x32(krope[s3], qf[16 + s3], acc[4]);
   f32x4 sv;
   const int vv[4] = {vr.x, vr.y, vr.z, vr.w};
 #pragma unroll
@@ -701,9 +717,7 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
       const int r = q / kQPitchPieces, ch = q - r * kQPitchPieces;
       const int hq = (r < 16 && h0 + r < p.n_head) ? h0 + r : h0;
       const int chq = (r < 16 && ch < kLatentDim / 8) ? ch : 0;
-      __builtin_amdgcn_global_load_lds(qb + (int64_t)hq * kLatentDim * 2 + 16 * chq,
-                                       (lds_void*)(sh.q + 16 * (kDmaThreads * u + 64 * w)), 16,
-                                       0, 0);
+      dma16(qb + (int64_t)hq * kLatentDim * 2 + 16 * chq, sh.q + 16 * (kDmaThreads * u + 64 * w));
     }
   }
   static_assert(kDmaSplitKeys <= kDmaThreads, "one key per thread");
@@ -759,8 +773,10 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   lds_barrier();
   f32x4 sv = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  if (my_chunk < nchunks)
-    sv = dma_qk(sh.buf[my_chunk], kbase, sh.rows + my_chunk * kDmaKeys, qf);
+  if (my_chunk < nchunks) {
+    f32x4 ksc[4];
+    sv = dma_qk(sh.buf[my_chunk], kbase, sh.rows + my_chunk * kDmaKeys, qf, ksc);
+  }
 
   // ---- softmax statistics of the split (per head c) ----
   float mt = -1e30f;
@@ -914,8 +930,7 @@ __device__ __forceinline__ void pf_dma_tile(const uint8_t* __restrict__ kv, cons
     const bool ok = q < kPfPieces && row[u] >= 0;
     const uint8_t* src = ok ? kv + (int64_t)row[u] * kDsmlaRowBytes + 16 * ch
                             : kZeroRow + 16 * (q < kPfPieces ? ch : 0);
-    __builtin_amdgcn_global_load_lds(src, (lds_void*)(slot + 16 * (kPfThreads * u + 64 * wave)),
-                                     16, 0, 0);
+    dma16(src, slot + 16 * (kPfThreads * u + 64 * wave));
   }
 }
 
@@ -1012,45 +1027,8 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_dma_kernel(MlaP
       const int32_t* trows = sh.rows + i * kPfTileKeys;
 
       // ---- S^T for keys [16 half, +16) ----
-      f32x4 sv;
-      {
-        const int kbase = 16 * half;
-        const uint8_t* krow = cb + (kbase + c) * kDsmlaRowBytes;
-        u32x4 kraw[8];
-        f16x8 krope[2];
-        f32x4 ksc[4];
-#pragma unroll
-        for (int s2 = 0; s2 < 8; s2++)
-          kraw[s2] = *reinterpret_cast<const u32x4*>(krow + 64 * s2 + 16 * g);
-#pragma unroll
-        for (int s3 = 0; s3 < 2; s3++)
-          krope[s3] = *reinterpret_cast<const f16x8*>(krow + 528 + 64 * s3 + 16 * g);
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-          ksc[r] = *reinterpret_cast<const f32x4*>(cb + (kbase + 4 * g + r) * kDsmlaRowBytes + 512);
-        const int4 vr = *reinterpret_cast<const int4*>(trows + kbase + 4 * g);
-        f32x4 acc[5];
-#pragma unroll
-        for (int a = 0; a < 5; a++) acc[a] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s2 = 0; s2 < 8; s2++) {
-          const f16x4 a0 = e4m3x4_to_f16x4(kraw[s2][0]), a1 = e4m3x4_to_f16x4(kraw[s2][1]);
-          const f16x4 a2 = e4m3x4_to_f16x4(kraw[s2][2]), a3 = e4m3x4_to_f16x4(kraw[s2][3]);
-          const f16x8 k0 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-          const f16x8 k1 = {a2[0], a2[1], a2[2], a2[3], a3[0], a3[1], a3[2], a3[3]};
-          acc[s2 >> 1] = mfma16x16x32(k0, qf[2 * s2], acc[s2 >> 1]);
-          acc[s2 >> 1] = mfma16x16x32(k1, qf[2 * s2 + 1], acc[s2 >> 1]);
-        }
-#pragma unroll
-        for (int s3 = 0; s3 < 2; s3++) acc[4] = mfma16x16x32(krope[s3], qf[16 + s3], acc[4]);
-        const int vv[4] = {vr.x, vr.y, vr.z, vr.w};
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const float v = acc[4][r] + ksc[r][0] * acc[0][r] + ksc[r][1] * acc[1][r] +
-                          ksc[r][2] * acc[2][r] + ksc[r][3] * acc[3][r];
-          sv[r] = vv[r] >= 0 ? v : -INFINITY;
-        }
-      }
+      f32x4 ksc[4];
+      const f32x4 sv = dma_qk<false>(cb, 16 * half, trows, qf, ksc);
       // ---- tile max of the head group (both halves) ----
       float mt = -1e30f;
 #pragma unroll
