@@ -140,4 +140,20 @@ __host__ __device__ __forceinline__ int ilog2_pow2(int v) {
   return s;
 }
 
+// Workgroup barrier that waits only for this wave's LDS operations (not for
+// vector-memory loads in flight, which __syncthreads would drain).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// global_load_lds_dwordx4: lane l's 16 bytes at gptr land at lds + 16 l (the
+// LDS base goes through M0, so it must be wave-uniform).  Issued as inline
+// asm so the compiler does not treat every later LDS read as depending on
+// the gathers in flight (it would otherwise wait for all of them): callers
+// wait for completion themselves with s_waitcnt vmcnt before a barrier.
+__device__ __forceinline__ void dma16(const void* gptr, const void* lds) {
+  const uint32_t off = (uint32_t)(uintptr_t)lds;
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(off) : "memory");
+}
+
 }  // namespace mi355dsa

@@ -212,10 +212,44 @@ __global__ void __launch_bounds__(kIdxWaves * 64) indexer_logits_kernel(
 
 // ===========================================================================
 // packed (prefill) kernel
+//
+// Workgroup tile = 64 queries (4 x 16) x 256 keys, 8 waves of 32 keys each.
+// The tile balances two limits: it is small enough that the caller's
+// 128-row sub-chunks launch ~256 workgroups at average causal reach, and
+// wide enough in keys (256 FLOP per byte of streamed Q) that the L2 -> CU
+// stream of Q stays below what one CU can ingest.  A wave keeps its 32 keys
+// (2 blocks x 128 dims, fp16) resident as
+// MFMA A operands for all 32 heads; the packed Q of each head (16 KB for the
+// 64 queries, contiguous in the packed layout) streams through a 4-slot LDS
+// ring filled by LDS-DMA three heads ahead, so the Q fetch latency hides
+// behind three heads of MFMA work.  relu(S) * w is summed over heads in
+// registers.
 // ===========================================================================
 constexpr int kPkWaves = 8;
-constexpr int kPkQT = 64;                 // queries per workgroup (4 x 16)
-constexpr int kPkKT = 64 * kPkWaves;      // keys per workgroup (64 per wave)
+constexpr int kPkQT = 64;                  // queries per workgroup (4 x 16)
+constexpr int kPkKT = 32 * kPkWaves;       // keys per workgroup (32 per wave)
+constexpr int kPkRing = 8;                 // Q ring slots (heads): 4 pairs
+constexpr int kPkQHead = 4 * 2048;         // halves of one head's Q for 4 query tiles
+constexpr int kPkQRounds = kPkQHead * 2 / 16 / (kPkWaves * 64);  // 4 LDS-DMA ops per thread
+
+struct PkSmem {
+  f16 q[kPkRing][kPkQHead];
+  float w[kIdxHeads][kPkQT];
+  int32_t sl[kPkQT];
+  int maxsl;
+};
+
+// relu in one instruction (v_med3_f32 clamp to [0, FLT_MAX]; fmaxf would
+// first canonicalise its input under IEEE mode)
+__device__ __forceinline__ float relu1(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, FLT_MAX); }
+
+__device__ __forceinline__ void pk_wait(int k) {  // at most k head pairs in flight
+  switch (k) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kPkQRounds) : "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kPkQRounds) : "memory"); break;
+  }
+}
 
 template <bool KFP8>
 __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
@@ -223,6 +257,7 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
     const f16* __restrict__ W, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ seq_lens, float* __restrict__ score, int B,
     int64_t n_kv_rows, int max_blocks, int page_shift, int max_kv) {
+  __shared__ PkSmem sh;
   const int q_base = blockIdx.y * kPkQT;
   const int p_base = blockIdx.x * kPkKT;
   const int n_qt = (B + 15) >> 4;
@@ -230,58 +265,62 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
 
-  __shared__ f16 s_q[2][4 * 8 * 256];   // packed Q of one head, 4 query tiles
-  __shared__ float s_w[kIdxHeads][kPkQT];
-  __shared__ int32_t s_sl[kPkQT];
-  __shared__ int s_maxsl;
-
-  if (threadIdx.x == 0) s_maxsl = 0;
-  __syncthreads();
-  for (int i = threadIdx.x; i < kPkQT; i += blockDim.x) {
-    const int q = q_base + i;
-    const int sl = (q < B) ? seq_lens[q] : 0;
-    s_sl[i] = sl;
-    atomicMax(&s_maxsl, sl);
-  }
-  for (int i = threadIdx.x; i < kIdxHeads * kPkQT; i += blockDim.x) {
-    const int h = i / kPkQT, qi = i % kPkQT;
-    const int q = q_base + qi;
-    s_w[h][qi] = (q < B) ? (float)W[(int64_t)q * kIdxHeads + h] : 0.f;
-  }
-  __syncthreads();
-
-  const int key0 = p_base + 64 * wave;  // this wave's 64 keys
-  if (p_base >= s_maxsl) {
-    // no query of this tile reaches these keys: -inf padding only
-    for (int e = threadIdx.x; e < kPkQT * kPkKT; e += blockDim.x) {
-      const int qi = e / kPkKT, p = p_base + e % kPkKT;
-      const int q = q_base + qi;
-      if (q < B && p < max_kv) score[(int64_t)q * max_kv + p] = -INFINITY;
-    }
-    return;
-  }
-
-  // A operands: this wave's keys (4 blocks of 16) for the 4 x32 steps.
-  // Keys are gathered with the block-table row of the tile's first query
-  // (all rows of a call share one table, see the C-ABI contract).
-  const int32_t* bt_row = block_table + (int64_t)q_base * max_blocks;
-  f16x8 ka[4][4];
-  const int page = 1 << page_shift;
+  // Q ring: head h of the 4 query tiles [qt0, qt0 + 4) is 16 KB contiguous
+  // in the packed layout; tiles past the last one read tile 0 (their score
+  // columns are never written).  The first pairs go out before anything
+  // else so their latency overlaps the prologue.
+  const int qt0 = q_base >> 4;
+  auto issue_q = [&](int h) {
+    const bool full = qt0 + 4 <= n_qt;
 #pragma unroll
-  for (int kb = 0; kb < 4; kb++) {
-    const int p = key0 + 16 * kb + c;
-    int64_t row = -1;
-    if (p < max_kv) {
-      const int pg = p >> page_shift;
-      if (pg < max_blocks) {
-        const int32_t pb = bt_row[pg];
-        const int64_t r = ((int64_t)pb << page_shift) + (p & (page - 1));
-        if (pb >= 0 && r < n_kv_rows) row = r;
-      }
+    for (int u = 0; u < kPkQRounds; u++) {
+      const int i = threadIdx.x + u * kPkWaves * 64;  // 16-byte piece
+      const int qt = qt0 + (i >> 8);                  // 256 pieces per tile
+      const int64_t src = ((int64_t)h * n_qt + ((full || qt < n_qt) ? qt : 0)) * 2048 + (i & 255) * 8;
+      dma16(Qp + src, &sh.q[h % kPkRing][(u * kPkWaves * 64 + 64 * wave) * 8]);
     }
+  };
+  constexpr int kAhead = kPkRing / 2 - 1;  // head pairs issued ahead
+#pragma unroll
+  for (int h = 0; h < 2 * kAhead; h++) issue_q(h);
+
+  // ---- prologue: seq lens, head weights and block-table entries are
+  // independent loads; the key rows follow the block-table entries ----
+  int sl_v = 0;  // wave 0: query q_base + lane
+  if (threadIdx.x < kPkQT) {
+    const int q = q_base + threadIdx.x;
+    sl_v = (q < B) ? seq_lens[q] : 0;
+  }
+  constexpr int WPT = kIdxHeads * kPkQT / (kPkWaves * 64);
+  float wv[WPT];
+#pragma unroll
+  for (int u = 0; u < WPT; u++) {
+    const int i = threadIdx.x + u * kPkWaves * 64;
+    const int h = i / kPkQT, q = q_base + i % kPkQT;
+    wv[u] = (q < B) ? (float)W[(int64_t)q * kIdxHeads + h] : 0.f;
+  }
+  const int key0 = p_base + 32 * wave;  // this wave's 32 keys
+  // Keys are gathered with the block-table row of the tile's first query
+  // (all rows of a call share one table).
+  const int32_t* bt_row = block_table + (int64_t)q_base * max_blocks;
+  const int page = 1 << page_shift;
+  int32_t pbk[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; kb++) {
+    const int p = key0 + 16 * kb + c;
+    const int pg = p >> page_shift;
+    pbk[kb] = (p < max_kv && pg < max_blocks) ? bt_row[pg] : -1;
+  }
+  // A operands: this wave's keys (2 blocks of 16), dims 32s + 8g .. +8 for
+  // the 4 x32 steps.
+  f16x8 ka[2][4];
+#pragma unroll
+  for (int kb = 0; kb < 2; kb++) {
+    const int p = key0 + 16 * kb + c;
+    const int64_t r = ((int64_t)pbk[kb] << page_shift) + (p & (page - 1));
+    const int64_t row = (pbk[kb] >= 0 && r < n_kv_rows) ? r : -1;
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-      // dims 32s + 8g .. +8
       if (row < 0) {
         ka[kb][s] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
       } else if constexpr (KFP8) {
@@ -303,70 +342,108 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
       }
     }
   }
-
-  // packed Q of head h for this workgroup's 4 query tiles: 1024 16-byte
-  // chunks, 2 per thread.  The next head's chunks are loaded into registers
-  // before the current head's MFMAs and written to LDS after them, so the
-  // loads overlap compute.
-  const int qt0 = q_base >> 4;
-  constexpr int QPER = 1024 / (kPkWaves * 64);
-  auto load_q = [&](int h, f16x8* v) {
 #pragma unroll
-    for (int u = 0; u < QPER; u++) {
-      const int i = threadIdx.x + u * kPkWaves * 64;
-      const int qt = qt0 + (i >> 8);  // 256 chunks per tile
-      v[u] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-      if (qt < n_qt)
-        v[u] = *reinterpret_cast<const f16x8*>(Qp + ((int64_t)h * n_qt + qt) * 2048 + (i & 255) * 8);
-    }
-  };
-  auto store_q = [&](const f16x8* v, int buf) {
+  for (int u = 0; u < WPT; u++) {
+    const int i = threadIdx.x + u * kPkWaves * 64;
+    sh.w[i / kPkQT][i % kPkQT] = wv[u];
+  }
+  if (wave == 0) {
+    sh.sl[lane] = sl_v;
+    int m = sl_v;
 #pragma unroll
-    for (int u = 0; u < QPER; u++) {
-      const int i = threadIdx.x + u * kPkWaves * 64;
-      *reinterpret_cast<f16x8*>(&s_q[buf][i * 8]) = v[u];
-    }
-  };
-
-  f32x4 sacc[4][4];  // [key block][query block], relu*w summed over heads
-#pragma unroll
-  for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-    for (int qb = 0; qb < 4; qb++) sacc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  f16x8 qnext[QPER];
-  load_q(0, qnext);
-  store_q(qnext, 0);
+    for (int o = 32; o >= 1; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
+    if (lane == 0) sh.maxsl = m;
+  }
   __syncthreads();
-  for (int h = 0; h < kIdxHeads; h++) {
-    const int buf = h & 1;
-    if (h + 1 < kIdxHeads) load_q(h + 1, qnext);
+
+  if (p_base >= sh.maxsl) {
+    // no query of this tile reaches these keys: -inf padding only
+    for (int e = threadIdx.x; e < kPkQT * kPkKT; e += blockDim.x) {
+      const int qi = e / kPkKT, p = p_base + e % kPkKT;
+      const int q = q_base + qi;
+      if (q < B && p < max_kv) score[(int64_t)q * max_kv + p] = -INFINITY;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS-DMA may outlive the LDS
+    return;
+  }
+
+  f32x4 sacc[2][4];  // [key block][query block], relu*w summed over heads
+  f32x4 accp[2][4];  // S of the previous head, epilogue pending
+#pragma unroll
+  for (int kb = 0; kb < 2; kb++)
 #pragma unroll
     for (int qb = 0; qb < 4; qb++) {
-      // B operand: query column c of tile qb, dims 32s + 8g .. +8, i.e.
-      // packed chunk (kt = 2s + g/2, row c, half 8*(g&1))
-      f32x4 acc[4];
-#pragma unroll
-      for (int kb = 0; kb < 4; kb++) acc[kb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; s++) {
-        const int kt = 2 * s + (g >> 1);
-        const f16x8 bq = *reinterpret_cast<const f16x8*>(
-            &s_q[buf][qb * 2048 + kt * 256 + c * 16 + 8 * (g & 1)]);
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++) acc[kb] = mfma16x16x32(ka[kb][s], bq, acc[kb]);
-      }
-      const float wq = s_w[h][16 * qb + c];
-#pragma unroll
-      for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const float d = acc[kb][r];
-          sacc[kb][qb][r] += (d > 0.f ? d : 0.f) * wq;
-        }
+      sacc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      accp[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
     }
-    if (h + 1 < kIdxHeads) store_q(qnext, buf ^ 1);
-    __syncthreads();
+
+  for (int h0 = 0; h0 < kIdxHeads; h0 += 2) {
+    const int j = h0 >> 1;
+    pk_wait(min(kIdxHeads / 2 - 1 - j, kAhead - 1));
+    lds_barrier();  // pair j landed; every wave is done with pair j - 1
+    if (j + kAhead < kIdxHeads / 2) {
+      issue_q(h0 + 2 * kAhead);
+      issue_q(h0 + 2 * kAhead + 1);
+    }
+    // Software pipeline: the relu * w epilogue of head h - 1 is interleaved
+    // with the MFMAs of head h (independent instructions), so the VALU work
+    // overlaps the matrix cores instead of following them.
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      const int h = h0 + hh;
+      const f16* qs = sh.q[h % kPkRing];
+      f16x8 bq[4][4];
+#pragma unroll
+      for (int st = 0; st < 4; st++)
+#pragma unroll
+        for (int qb = 0; qb < 4; qb++)
+          // B operand: query column c of tile qb, dims 32st + 8g .. +8, i.e.
+          // packed chunk (kt = 2st + g/2, row c, half 8*(g&1))
+          bq[st][qb] = *reinterpret_cast<const f16x8*>(
+              &qs[qb * 2048 + (2 * st + (g >> 1)) * 256 + c * 16 + 8 * (g & 1)]);
+      float wq[4];
+      const int hp = h - 1;
+#pragma unroll
+      for (int qb = 0; qb < 4; qb++) wq[qb] = (hp >= 0) ? sh.w[hp][16 * qb + c] : 0.f;
+      f32x4 acc[2][4];
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int qb = 0; qb < 4; qb++) acc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 4; st++)
+#pragma unroll
+        for (int qb = 0; qb < 4; qb++)
+#pragma unroll
+          for (int kb = 0; kb < 2; kb++) acc[kb][qb] = mfma16x16x32(ka[kb][st], bq[st][qb], acc[kb][qb]);
+      // epilogue of the previous head (accp holds zeros before head 0)
+#pragma unroll
+      for (int qb = 0; qb < 4; qb++)
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) sacc[kb][qb][r] += relu1(accp[kb][qb][r]) * wq[qb];
+      // one MFMA, then two VALU, repeated
+#pragma unroll
+      for (int i = 0; i < 32; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int qb = 0; qb < 4; qb++) accp[kb][qb] = acc[kb][qb];
+    }
+  }
+  {
+#pragma unroll
+    for (int qb = 0; qb < 4; qb++) {
+      const float wl = sh.w[kIdxHeads - 1][16 * qb + c];
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sacc[kb][qb][r] += relu1(accp[kb][qb][r]) * wl;
+    }
   }
 
   // D layout: lane (query col c, key rows 4g+r) -> 4 consecutive keys.
@@ -375,10 +452,10 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
     const int qi = 16 * qb + c;
     const int q = q_base + qi;
     if (q >= B) continue;
-    const int sl = s_sl[qi];
+    const int sl = sh.sl[qi];
     float* srow = score + (int64_t)q * max_kv;
 #pragma unroll
-    for (int kb = 0; kb < 4; kb++) {
+    for (int kb = 0; kb < 2; kb++) {
       const int p0 = key0 + 16 * kb + 4 * g;
       f32x4 v;
 #pragma unroll

@@ -589,20 +589,6 @@ typedef int s32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) s32x2 lds_s32x2;
 typedef __attribute__((address_space(3))) void lds_void;
 
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// global_load_lds_dwordx4: lane l's 16 bytes at gptr land at lds + 16 l (the
-// LDS base goes through M0, so it must be wave-uniform).  Issued as inline
-// asm so the compiler does not treat every later LDS read as depending on
-// the gathers in flight (it would otherwise wait for all of them): callers
-// wait for completion themselves with s_waitcnt vmcnt before a barrier.
-__device__ __forceinline__ void dma16(const void* gptr, const void* lds) {
-  const uint32_t off = (uint32_t)(uintptr_t)lds;
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(off) : "memory");
-}
-
 // 4 e4m3 bytes -> 4 exact fp16 values
 __device__ __forceinline__ f16x4 e4m3x4_to_f16x4(uint32_t w) {
   const f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, false);
