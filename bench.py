@@ -418,7 +418,7 @@ def main():
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
             "traffic": measured_traffic(),
             "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/sparse_mla_decode_c3_pmc.md",
-            "kernel": "sparse_mla_kernel (decode config) + sparse_mla_merge_kernel",
+            "kernel": "sparse_mla_decode_dma_kernel + sparse_mla_merge_kernel",
             "bytes_per_launch": DECODE_BYTES,
         },
     }
