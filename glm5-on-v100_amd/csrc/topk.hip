@@ -282,15 +282,295 @@ static int launch_topk(const float* score, int n_rows, int64_t row_stride,
   return check_launch("topk");
 }
 
+// ===========================================================================
+// Decode top-k from the indexer histogram, in two kernels (no inter-
+// workgroup synchronisation):
+//  * topk_scan_kernel, grid (tiles of 1024 positions, rows): every workgroup
+//    derives the level-1 threshold bin T1 from the row's histogram (bins
+//    above T1 hold fewer than K keys, bins >= T1 at least K), then writes
+//    its candidates -- positions with bin >= T1 -- with their keys, in
+//    position order, and their count.
+//  * topk_select_kernel, one workgroup per row: the candidates (about K plus
+//    the keys sharing bin T1) are gathered into LDS, the exact threshold key
+//    among the T1 keys is found by a two-level radix select on their low 20
+//    bits, and one packed scan over the candidates in position order writes
+//    the K positions, ascending.
+// A histogram that does not count exactly L keys, or a candidate set larger
+// than kTkCandCap, falls back to the whole-row selection in the select
+// kernel.  Workspace per row: 4 meta words, the tile counts and
+// 1024 (key, position) candidate slots per tile.
+// ===========================================================================
+constexpr int kScanTile = 1024;
+constexpr int kScanThreads = 256;
+constexpr int kTkCandCap = 14336;
+constexpr int kSelBins = 1024;
+
+struct ScanShared {
+  float v[kScanTile];
+  uint32_t wsum[kScanThreads / 64 + 1];
+  int T;
+  int status;
+};
+
+struct TopkWs {
+  int32_t* meta;     // [B][4]: T1, keys above T1, status (0 ok, 1 bad histogram)
+  int32_t* counts;   // [B][n_tiles]
+  uint32_t* ckey;    // [B][n_tiles][kScanTile]
+  int32_t* cpos;     // [B][n_tiles][kScanTile]
+};
+
+__host__ __device__ inline TopkWs topk_ws(void* base, int B, int n_tiles) {
+  TopkWs w;
+  char* p = reinterpret_cast<char*>(base);
+  w.meta = reinterpret_cast<int32_t*>(p);
+  p += (size_t)B * 4 * sizeof(int32_t);
+  w.counts = reinterpret_cast<int32_t*>(p);
+  p += ((size_t)B * n_tiles * sizeof(int32_t) + 15) / 16 * 16;
+  w.ckey = reinterpret_cast<uint32_t*>(p);
+  p += (size_t)B * n_tiles * kScanTile * sizeof(uint32_t);
+  w.cpos = reinterpret_cast<int32_t*>(p);
+  return w;
+}
+
+static size_t topk_ws_bytes(int B, int n_tiles) {
+  return (size_t)B * 4 * sizeof(int32_t) + ((size_t)B * n_tiles * sizeof(int32_t) + 15) / 16 * 16 +
+         (size_t)B * n_tiles * kScanTile * (sizeof(uint32_t) + sizeof(int32_t));
+}
+
+__global__ void __launch_bounds__(kScanThreads) topk_scan_kernel(
+    const float* __restrict__ score, int max_kv, const int32_t* __restrict__ seq_lens,
+    const uint32_t* __restrict__ hist, int K, TopkWs ws) {
+  __shared__ ScanShared sh;
+  const int b = blockIdx.y, tile = blockIdx.x, n_tiles = gridDim.x;
+  const int p0 = tile * kScanTile;
+  int L = seq_lens[b];
+  L = L < 0 ? 0 : (L > max_kv ? max_kv : L);
+  if (L <= K) return;  // the select kernel takes every position
+  int32_t* cnt = ws.counts + (int64_t)b * n_tiles + tile;
+  if (p0 >= L) {
+    if (threadIdx.x == 0) *cnt = 0;
+    return;
+  }
+  // positions of the tile, coalesced, staged in LDS
+  const float* row = score + (int64_t)b * max_kv;
+#pragma unroll
+  for (int e = 0; e < kScanTile / kScanThreads; e++) {
+    const int p = p0 + e * kScanThreads + (int)threadIdx.x;
+    sh.v[e * kScanThreads + threadIdx.x] = (p < L) ? row[p] : 0.f;
+  }
+  // ---- T1 from the histogram: thread t owns bins [16t, 16t+16) ----
+  const uint32_t* h = hist + (int64_t)b * kTopkBins;
+  constexpr int PER = kTopkBins / kScanThreads;
+  uint32_t hb[PER], cs = 0;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    hb[i] = h[PER * threadIdx.x + i];
+    cs += hb[i];
+  }
+  uint32_t total;
+  const uint32_t excl = block_excl_scan_n<kScanThreads>(cs, sh.wsum, &total);
+  if (threadIdx.x == 0) {
+    sh.T = -1;
+    sh.status = (total == (uint32_t)L) ? 0 : 1;
+  }
+  __syncthreads();
+  if (sh.status != 0) {
+    if (tile == 0 && threadIdx.x == 0) ws.meta[(int64_t)b * 4 + 2] = 1;
+    return;
+  }
+  {
+    uint32_t a = total - excl - cs;  // keys in bins above this thread's bins
+    for (int i = PER - 1; i >= 0; i--) {
+      if (a < (uint32_t)K && a + hb[i] >= (uint32_t)K) {
+        sh.T = PER * threadIdx.x + i;
+        if (tile == 0) {
+          ws.meta[(int64_t)b * 4 + 0] = sh.T;
+          ws.meta[(int64_t)b * 4 + 1] = (int)a;
+          ws.meta[(int64_t)b * 4 + 2] = 0;
+        }
+      }
+      a += hb[i];
+    }
+  }
+  __syncthreads();
+  const uint32_t T1 = (uint32_t)sh.T;
+  // ---- candidates of 4 consecutive positions per thread, position order ----
+  uint32_t key[4];
+  uint32_t n = 0;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int p = p0 + 4 * threadIdx.x + e;
+    key[e] = mono_key(sh.v[4 * threadIdx.x + e]);
+    const bool cand = p < L && (key[e] >> 20) >= T1;
+    n += cand ? 1u : 0u;
+  }
+  uint32_t tot;
+  uint32_t off = block_excl_scan_n<kScanThreads>(n, sh.wsum, &tot);
+  const int64_t slot0 = ((int64_t)b * n_tiles + tile) * kScanTile;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int p = p0 + 4 * threadIdx.x + e;
+    if (p < L && (key[e] >> 20) >= T1) {
+      ws.ckey[slot0 + off] = key[e];
+      ws.cpos[slot0 + off] = p;
+      off++;
+    }
+  }
+  if (threadIdx.x == 0) *cnt = (int)tot;
+}
+
+struct SelShared {
+  union {
+    TopkShared full;
+    struct {
+      uint32_t ckey[kTkCandCap];
+      int32_t cpos[kTkCandCap];
+      uint32_t hist[kSelBins];
+      int32_t toff[1024 + 1];
+    } c;
+  } u;
+  uint32_t wsum[kTkWaves + 1];
+  int T;
+  uint32_t above;
+  int n_cand;
+};
+
+// Bin T of an nbins (<= 1024) LDS histogram with above(T) < need <=
+// above(T) + hist[T]; one bin per thread.
+__device__ void sel_threshold(SelShared& sh, const uint32_t* hist, int nbins, uint32_t need,
+                              int* T, uint32_t* above) {
+  const uint32_t hv = (int)threadIdx.x < nbins ? hist[threadIdx.x] : 0u;
+  uint32_t total;
+  const uint32_t excl = block_excl_scan_n<kTkThreads>(hv, sh.wsum, &total);
+  const uint32_t a = total - excl - hv;  // keys in higher bins
+  if ((int)threadIdx.x < nbins && a < need && a + hv >= need) {
+    sh.T = threadIdx.x;
+    sh.above = a;
+  }
+  __syncthreads();
+  *T = sh.T;
+  *above = sh.above;
+  __syncthreads();
+}
+
+__global__ void __launch_bounds__(kTkThreads) topk_select_kernel(
+    const float* __restrict__ score, int max_kv, const int32_t* __restrict__ seq_lens,
+    const uint32_t* __restrict__ hist, int32_t* __restrict__ idx, int K, int n_tiles,
+    TopkWs ws) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  SelShared& sh = *reinterpret_cast<SelShared*>(smem_raw);
+  const int b = blockIdx.x;
+  int32_t* out = idx + (int64_t)b * K;
+  int L = seq_lens[b];
+  L = L < 0 ? 0 : (L > max_kv ? max_kv : L);
+  if (L <= K) {
+    for (int p = threadIdx.x; p < K; p += kTkThreads) out[p] = (p < L) ? p : -1;
+    return;
+  }
+  const float* row = score + (int64_t)b * max_kv;
+  const uint32_t* hrow = hist + (int64_t)b * kTopkBins;
+  const int status = ws.meta[(int64_t)b * 4 + 2];
+  if (status != 0) {  // histogram inconsistent with L: rebuild from the row
+    topk_row_select(sh.u.full, row, L, K, out, nullptr);
+    return;
+  }
+  const int used_tiles = (L + kScanTile - 1) / kScanTile;
+  const uint32_t above1 = (uint32_t)ws.meta[(int64_t)b * 4 + 1];
+  // ---- tile offsets of the candidate lists ----
+  int total_c = 0;
+  for (int t0 = 0; t0 < used_tiles; t0 += kTkThreads) {
+    const int t = t0 + threadIdx.x;
+    const uint32_t n = (t < used_tiles) ? (uint32_t)ws.counts[(int64_t)b * n_tiles + t] : 0u;
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan_n<kTkThreads>(n, sh.wsum, &tot);
+    if (t < used_tiles && t <= 1024) sh.u.c.toff[t] = total_c + (int)ex;
+    total_c += (int)tot;
+  }
+  if (total_c > kTkCandCap || used_tiles > 1024) {
+    __syncthreads();
+    topk_row_select(sh.u.full, row, L, K, out, hrow);
+    return;
+  }
+  __syncthreads();
+  // ---- gather the candidates into LDS (tile lists are position ordered) ----
+  for (int t = threadIdx.x >> 6; t < used_tiles; t += kTkWaves) {
+    const int n = ws.counts[(int64_t)b * n_tiles + t];
+    const int o = sh.u.c.toff[t];
+    const int64_t s0 = ((int64_t)b * n_tiles + t) * kScanTile;
+    for (int i = threadIdx.x & 63; i < n; i += 64) {
+      sh.u.c.ckey[o + i] = ws.ckey[s0 + i];
+      sh.u.c.cpos[o + i] = ws.cpos[s0 + i];
+    }
+  }
+  for (int i = threadIdx.x; i < kSelBins; i += kTkThreads) sh.u.c.hist[i] = 0u;
+  __syncthreads();
+  // ---- exact threshold among the T1 keys: bits [10,20), then [0,10) ----
+  const int T1 = ws.meta[(int64_t)b * 4 + 0];
+  const uint32_t need1 = (uint32_t)K - above1;  // keys to take from bin T1
+  for (int i = threadIdx.x; i < total_c; i += kTkThreads) {
+    const uint32_t k = sh.u.c.ckey[i];
+    if ((int)(k >> 20) == T1) atomicAdd(&sh.u.c.hist[(k >> 10) & 1023], 1u);
+  }
+  __syncthreads();
+  int T2;
+  uint32_t above2;
+  sel_threshold(sh, sh.u.c.hist, kSelBins, need1, &T2, &above2);
+  const uint32_t need2 = need1 - above2;
+  for (int i = threadIdx.x; i < kSelBins; i += kTkThreads) sh.u.c.hist[i] = 0u;
+  __syncthreads();
+  const uint32_t pre2 = ((uint32_t)T1 << 10) | (uint32_t)T2;  // top 22 bits
+  for (int i = threadIdx.x; i < total_c; i += kTkThreads) {
+    const uint32_t k = sh.u.c.ckey[i];
+    if ((k >> 10) == pre2) atomicAdd(&sh.u.c.hist[k & 1023], 1u);
+  }
+  __syncthreads();
+  int T3;
+  uint32_t above3;
+  sel_threshold(sh, sh.u.c.hist, kSelBins, need2, &T3, &above3);
+  const uint32_t tau = (pre2 << 10) | (uint32_t)T3;
+  const uint32_t take_eq = need2 - above3;  // keys equal to tau to take, lowest positions
+  // ---- ordered compaction over the candidates: packed (gt | eq << 16) scan ----
+  const int per = (total_c + kTkThreads - 1) / kTkThreads;
+  const int i0 = threadIdx.x * per, i1 = min(i0 + per, total_c);
+  uint32_t packed = 0;
+  for (int i = i0; i < i1; i++) {
+    const uint32_t k = sh.u.c.ckey[i];
+    packed += (k > tau ? 1u : 0u) + (k == tau ? (1u << 16) : 0u);
+  }
+  uint32_t tot;
+  const uint32_t ex = block_excl_scan_n<kTkThreads>(packed, sh.wsum, &tot);
+  uint32_t gt = ex & 0xFFFFu, eq = ex >> 16;
+  for (int i = i0; i < i1; i++) {
+    const uint32_t k = sh.u.c.ckey[i];
+    if (k > tau) {
+      const uint32_t o = gt + (eq < take_eq ? eq : take_eq);
+      if (o < (uint32_t)K) out[o] = sh.u.c.cpos[i];
+      gt++;
+    } else if (k == tau) {
+      if (eq < take_eq) {
+        const uint32_t o = gt + eq;
+        if (o < (uint32_t)K) out[o] = sh.u.c.cpos[i];
+      }
+      eq++;
+    }
+  }
+}
+
 }  // namespace mi355dsa
 
 using namespace mi355dsa;
 
+// Rows per call up to which the two-kernel path is used: it needs fewer
+// launches' worth of parallelism than one workgroup per row provides.
+constexpr int kTwoKernelMaxRows = 64;
+
+static bool two_kernel_topk(int B, int max_kv, int k) {
+  return B <= kTwoKernelMaxRows && max_kv > k && (max_kv + kScanTile - 1) / kScanTile <= 1024;
+}
+
 extern "C" size_t mi355_dsa_decode_topk_workspace_size(int B, int max_kv, int k) {
-  (void)B;
-  (void)max_kv;
-  (void)k;
-  return 0;
+  if (B <= 0 || max_kv <= 0 || !two_kernel_topk(B, max_kv, k)) return 0;
+  return topk_ws_bytes(B, (max_kv + kScanTile - 1) / kScanTile);
 }
 
 extern "C" int mi355_dsa_decode_topk(int32_t* idx, const float* score,
@@ -305,9 +585,30 @@ extern "C" int mi355_dsa_decode_topk(int32_t* idx, const float* score,
   DSA_CHECK(k <= (1 << 16) - 1, "k too large");
   if (B == 0) return MI355_DSA_OK;
   DSA_CHECK(idx && score && seq_lens && hist, "null pointer argument");
+  hipStream_t st = as_stream(stream);
+  if (two_kernel_topk(B, max_kv, k)) {
+    const int n_tiles = (max_kv + kScanTile - 1) / kScanTile;
+    const size_t need = topk_ws_bytes(B, n_tiles);
+    DSA_CHECK(workspace && workspace_bytes >= need,
+              "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    DSA_CHECK(aligned_to(workspace, 16), "workspace must be 16-byte aligned");
+    const TopkWs ws = topk_ws(workspace, B, n_tiles);
+    const uint32_t* h = reinterpret_cast<const uint32_t*>(hist);
+    topk_scan_kernel<<<dim3(n_tiles, B), kScanThreads, 0, st>>>(score, max_kv, seq_lens, h, k, ws);
+    int rc = check_launch("decode_topk scan");
+    if (rc) return rc;
+    static bool attr = false;
+    if (!attr) {
+      hipFuncSetAttribute(reinterpret_cast<const void*>(topk_select_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(SelShared));
+      attr = true;
+    }
+    topk_select_kernel<<<B, kTkThreads, sizeof(SelShared), st>>>(score, max_kv, seq_lens, h, idx,
+                                                                 k, n_tiles, ws);
+    return check_launch("decode_topk select");
+  }
   return launch_topk<true>(score, B, max_kv, seq_lens,
-                           reinterpret_cast<const uint32_t*>(hist), idx, k,
-                           as_stream(stream));
+                           reinterpret_cast<const uint32_t*>(hist), idx, k, st);
 }
 
 extern "C" size_t mi355_dsa_persistent_topk_workspace_size(int n_rows, int row_stride,

@@ -66,6 +66,25 @@ def test_decode_topk_rebuilds_bad_hist(ops, dev):
     assert torch.equal(idx.cpu(), cref.topk_rows(s, seq, 2048))
 
 
+@pytest.mark.parametrize("kind,B,W,seq,K", [
+    ("equal", 1, 40000, [40000], 2048),       # candidate set above the LDS cap: whole-row path
+    ("ties", 2, 50000, [50000, 30001], 2048),  # many keys share the threshold bin
+    ("randn", 100, 5000, None, 256),            # more rows than the two-kernel path takes
+    ("randn", 3, 3000, [2049, 2048, 3000], 2048),
+])
+def test_decode_topk_paths(ops, dev, kind, B, W, seq, K):
+    """The decode top-k's scan/select path, its whole-row fallbacks and the
+    one-workgroup-per-row path all give the exact selection."""
+    g = torch.Generator().manual_seed(B * 7 + W)
+    s = scores(kind, B, W, g)
+    if seq is None:
+        seq = [W - (i * 37) % 1000 for i in range(B)]
+    seq = torch.tensor(seq, dtype=torch.int32)
+    idx = torch.full((B, K), 123, dtype=torch.int32, device=dev)
+    ops.sm70_decode_topk(idx, s.to(dev), seq.to(dev), hist_of(s, seq).to(dev), K)
+    assert torch.equal(idx.cpu(), cref.topk_rows(s, seq, K))
+
+
 @pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-{c[1]}x{c[2]}" for c in CASES])
 def test_persistent_topk(ops, dev, case):
     kind, B, W, seq = case
