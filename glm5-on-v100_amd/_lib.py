@@ -42,6 +42,7 @@ SIGNATURES = {
                                              _c_size, _p]),
     "mi355_dsa_attn_fp8_gemv": (_c_int, [_p, _p, _p, _p, _c_int, _c_int, _c_int, _p]),
     "mi355_dsa_attn_fp8_dequant": (_c_int, [_p, _p, _p, _c_int, _c_int, _p]),
+    "mi355_dsa_attn_fp8_quantize": (_c_int, [_p, _p, _p, _c_int, _c_int, _p]),
 }
 
 _lib = None

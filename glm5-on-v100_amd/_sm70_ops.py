@@ -31,6 +31,15 @@ def sm70_attn_fp8_gemv(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor,
     _op("sm70_attn_fp8_gemv")(y, x, w, s)
 
 
+def _sm70_attn_fp8_quantize(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """[128,128]-block e4m3 quantization of an fp16 [N,K] weight, on the GPU.
+
+    Returns (uint8 e4m3 bits [N,K], fp32 scale_inv [ceil(N/128), ceil(K/128)]),
+    like the model loader's function of the same name."""
+    from . import ops as _ops
+    return _ops.attn_fp8_quantize(weight)
+
+
 def sm70_attn_fp8_dequant(out: torch.Tensor, w: torch.Tensor, s: torch.Tensor) -> None:
     """Dequantize fp8-e4m3 block-scaled weights into an fp16 scratch [N,K]."""
     _op("sm70_attn_fp8_dequant")(out, w, s)

@@ -144,6 +144,67 @@ __global__ void __launch_bounds__(WAVES * 64) fp8_gemv_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Load-time quantizer (reference _sm70_attn_fp8_quantize, glue.patch:
+// 1515-1532): per 128x128 block scale = max(amax / 448, 1e-12) and
+// q = e4m3_rne(clamp(w / scale, +-448)); partial edge blocks take the amax
+// of their valid elements (the reference pads with zeros).  One workgroup per
+// block, thread t covers 64 columns of row t / 2.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) fp8_quantize_kernel(const f16* __restrict__ w,
+                                                           uint8_t* __restrict__ q,
+                                                           float* __restrict__ s, int N, int K) {
+  const int nb = blockIdx.y, kb = blockIdx.x, KB = gridDim.x;
+  const int r = nb * 128 + (threadIdx.x >> 1);
+  const int k0 = kb * 128 + 64 * (threadIdx.x & 1);
+  const bool vec = (K % 8) == 0 && k0 + 64 <= K;
+  float v[64];
+  if (r < N && vec) {
+    const f16x8* src = reinterpret_cast<const f16x8*>(w + (int64_t)r * K + k0);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const f16x8 h = src[i];
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[8 * i + e] = (float)h[e];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 64; i++)
+      v[i] = (r < N && k0 + i < K) ? (float)w[(int64_t)r * K + k0 + i] : 0.f;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; i++) amax = fmaxf(amax, fabsf(v[i]));
+  amax = wave_max(amax);
+  __shared__ float wmax[4];
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float scale = fmaxf(amax / 448.0f, 1e-12f);  // IEEE division, as the reference
+  if (threadIdx.x == 0) s[(int64_t)nb * KB + kb] = scale;
+  if (r >= N) return;
+  uint32_t word[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    uint32_t x = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float t = fminf(fmaxf(v[4 * i + e] / scale, -448.0f), 448.0f);
+      x |= f32_to_e4m3_satfinite(t) << (8 * e);
+    }
+    word[i] = x;
+  }
+  uint8_t* dst = q + (int64_t)r * K + k0;
+  if (vec && ((uintptr_t)dst & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      reinterpret_cast<u32x4*>(dst)[i] = (u32x4){word[4 * i], word[4 * i + 1], word[4 * i + 2], word[4 * i + 3]};
+  } else {
+    for (int i = 0; i < 64; i++)
+      if (k0 + i < K) dst[i] = (uint8_t)(word[i >> 2] >> (8 * (i & 3)));
+  }
+}
+
 template <int NB>
 static void launch_gemv(const f16* x, const uint8_t* w, const float* s, f16* y,
                         int M, int N, int K, int KB, hipStream_t st) {
@@ -194,5 +255,22 @@ extern "C" int mi355_dsa_attn_fp8_dequant(void* out, const uint8_t* w,
   fp8_dequant_kernel<<<grid, 256, 0, as_stream(stream)>>>(
       w, s, reinterpret_cast<f16*>(out), K, KB);
   DSA_LAUNCH_CHECK("attn_fp8_dequant");
+  return MI355_DSA_OK;
+}
+
+extern "C" int mi355_dsa_attn_fp8_quantize(uint8_t* q, float* s, const void* w, int N, int K,
+                                           void* stream) {
+  clear_error();
+  DSA_CHECK(N >= 0 && K >= 0, "N and K must be >= 0");
+  if (N == 0 || K == 0) return MI355_DSA_OK;
+  DSA_CHECK(q && s && w, "null pointer argument");
+  DSA_CHECK(aligned_to(w, 2), "w must be 2-byte aligned");
+  const int NB = (N + 127) / 128, KB = (K + 127) / 128;
+  DSA_CHECK(NB <= 65535, "N too large");
+  const bool vec_ok = aligned_to(w, 16) && K % 8 == 0;
+  (void)vec_ok;
+  fp8_quantize_kernel<<<dim3(KB, NB), 256, 0, as_stream(stream)>>>(
+      reinterpret_cast<const f16*>(w), q, s, N, K);
+  DSA_LAUNCH_CHECK("attn_fp8_quantize");
   return MI355_DSA_OK;
 }

@@ -309,6 +309,24 @@ def attn_fp8_dequant_impl(out, w, s):
                   N, K, _stream(w))
 
 
+def attn_fp8_quantize(weight):
+    """Load-time [128,128]-block e4m3 quantization of an fp16 [N,K] weight on
+    the GPU: returns (uint8 e4m3 bits [N,K], fp32 scale [ceil(N/128),
+    ceil(K/128)]), the same values as _sm70_attn_fp8_quantize
+    (patches/glm5-v100-sm70-glue.patch:1515-1532)."""
+    _check(weight.is_cuda, "weight must be on the GPU")
+    _check(weight.dim() == 2, "weight must be 2-D [N, K]")
+    w = _contig(weight.to(torch.float16))
+    N, K = w.size(0), w.size(1)
+    q = torch.empty(N, K, dtype=torch.uint8, device=w.device)
+    s = torch.empty((N + 127) // 128, (K + 127) // 128, dtype=torch.float32, device=w.device)
+    if N and K:
+        with torch.cuda.device(w.device):
+            _lib.call("mi355_dsa_attn_fp8_quantize", q.data_ptr(), s.data_ptr(), w.data_ptr(),
+                      N, K, _stream(w))
+    return q, s
+
+
 IMPLS = {
     "sm70_sparse_mla_decode": sparse_mla_decode_impl,
     "sm70_indexer_logits": indexer_logits_impl,

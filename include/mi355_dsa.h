@@ -170,6 +170,16 @@ int mi355_dsa_attn_fp8_gemv(void* y, const void* x, const uint8_t* w,
 int mi355_dsa_attn_fp8_dequant(void* out, const uint8_t* w, const float* s,
                                int N, int K, void* stream);
 
+/*
+ * Load-time weight quantizer: w fp16 [N,K] (row-major, contiguous) ->
+ * q e4m3 bytes [N,K] and s fp32 [ceil(N/128), ceil(K/128)] with, per
+ * 128x128 block, s = max(amax/448, 1e-12) and q = e4m3_rne(clamp(w/s,
+ * +-448)).  Produces the inputs of mi355_dsa_attn_fp8_gemv / _dequant.
+ * Replaces _sm70_attn_fp8_quantize (patches/glm5-v100-sm70-glue.patch:
+ * 1515-1532), which the reference runs in PyTorch at model load.
+ */
+int mi355_dsa_attn_fp8_quantize(uint8_t* q, float* s, const void* w, int N, int K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

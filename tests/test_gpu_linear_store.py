@@ -125,3 +125,20 @@ def test_gemv_baseline_shapes(ops, dev, N, K):
         err = (y.float() - ref).abs().max().item()
         assert err <= 2e-3 * ref.abs().max().item(), (M, err)
     del w32
+
+
+@pytest.mark.parametrize("N,K", [(128, 128), (264, 400), (6144, 2112), (100, 36), (7, 1000)])
+def test_quantize_matches_oracle(ops, dev, N, K):
+    """Device quantizer == the oracle restatement of _sm70_attn_fp8_quantize,
+    bit for bit (codes and scales), including partial edge blocks, an
+    all-zero block (scale floor 1e-12) and saturating outliers."""
+    g = torch.Generator().manual_seed(N * 31 + K)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.float16)
+    w[: min(N, 128), : min(K, 128)] = 0  # a zero block
+    if N > 130 and K > 130:
+        w[130, 131] = 60000.0  # outlier: its block's scale follows it
+        w[131, 130] = -3e-7     # fp16 denormal
+    q, s = ops._sm70_attn_fp8_quantize(w.to(dev))
+    rq, rs = O.attn_fp8_quantize(w)
+    assert torch.equal(s.cpu(), rs)
+    assert torch.equal(q.cpu(), rq)
