@@ -12,10 +12,10 @@
 //    once per workgroup (nonzero bins only).
 //  * indexer_logits_packed_kernel -- mi355_dsa_indexer_logits_packed
 //    (prefill; reference sm70_indexer_logits_packed, :542-653 / :2771-2836).
-//    MFMA-bound: a 512-thread workgroup owns 64 queries x 512 keys; each wave
-//    keeps its 64 keys resident in A-operand registers for all 32 heads,
-//    streams the packed Q of one head at a time through LDS (double
-//    buffered) and keeps the relu * w head-sum in registers.
+//    MFMA-bound: a 512-thread workgroup owns 64 queries x 256 keys; each wave
+//    keeps 64 keys resident in A-operand registers for all 32 heads and
+//    scores them against 32 of the queries, whose packed Q streams through
+//    an LDS ring filled by LDS-DMA; the relu * w head-sum stays in registers.
 //
 // fp8 (132-byte) indexer rows: the decode kernel multiplies the exact
 // e4m3 dot by the row scale before the relu (reference :309-313); the packed
@@ -213,24 +213,32 @@ __global__ void __launch_bounds__(kIdxWaves * 64) indexer_logits_kernel(
 // ===========================================================================
 // packed (prefill) kernel
 //
-// Workgroup tile = 64 queries (4 x 16) x 256 keys, 8 waves of 32 keys each.
-// The tile balances two limits: it is small enough that the caller's
-// 128-row sub-chunks launch ~256 workgroups at average causal reach, and
-// wide enough in keys (256 FLOP per byte of streamed Q) that the L2 -> CU
-// stream of Q stays below what one CU can ingest.  A wave keeps its 32 keys
-// (2 blocks x 128 dims, fp16) resident as
-// MFMA A operands for all 32 heads; the packed Q of each head (16 KB for the
-// 64 queries, contiguous in the packed layout) streams through a 4-slot LDS
-// ring filled by LDS-DMA three heads ahead, so the Q fetch latency hides
-// behind three heads of MFMA work.  relu(S) * w is summed over heads in
-// registers.
+// Workgroup tile = 64 queries (4 x 16) x 256 keys, 8 waves.  The tile
+// balances two limits: it is small enough that the caller's 128-row
+// sub-chunks launch ~256 workgroups at average causal reach, and wide enough
+// in keys (256 FLOP per byte of streamed Q) that the L2 -> CU stream of Q
+// stays below what one CU can ingest.
+//
+// Wave w owns keys [64 (w & 3), +64) and query blocks 2 (w >> 2) + {0, 1}:
+// its 64 keys (4 blocks x 128 dims, fp16) stay resident as MFMA A operands
+// for all 32 heads, and per head it reads only its 32 queries' Q from LDS
+// (8 KB), so the 8 waves read 64 KB of LDS per head for 4.2 MFLOP.  The
+// packed Q of each head (16 KB for the 64 queries, contiguous in the packed
+// layout) streams through an 8-slot LDS ring filled by LDS-DMA three head
+// pairs ahead, the DMA rounds spread over the MFMA steps.  relu(S) * w is
+// summed over heads in registers, the epilogue of head h - 1 interleaved
+// with the MFMAs of head h.
 // ===========================================================================
 constexpr int kPkWaves = 8;
 constexpr int kPkQT = 64;                  // queries per workgroup (4 x 16)
-constexpr int kPkKT = 32 * kPkWaves;       // keys per workgroup (32 per wave)
+constexpr int kPkKT = 256;                 // keys per workgroup
+constexpr int kPkWaveKeys = 64;            // keys per wave (4 blocks of 16)
 constexpr int kPkRing = 8;                 // Q ring slots (heads): 4 pairs
 constexpr int kPkQHead = 4 * 2048;         // halves of one head's Q for 4 query tiles
-constexpr int kPkQRounds = kPkQHead * 2 / 16 / (kPkWaves * 64);  // 4 LDS-DMA ops per thread
+// LDS-DMA ops per thread for one head
+constexpr int kPkQRounds = kPkQHead * 2 / 16 / (kPkWaves * 64);  // 2
+
+__device__ const __align__(16) f16 kIdxZeroPiece[8] = {};  // source of unmapped key rows
 
 struct PkSmem {
   f16 q[kPkRing][kPkQHead];
@@ -263,29 +271,58 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
   const int n_qt = (B + 15) >> 4;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int half = wave >> 2;           // query-block pair
   const int c = lane & 15, g = lane >> 4;
 
   // Q ring: head h of the 4 query tiles [qt0, qt0 + 4) is 16 KB contiguous
   // in the packed layout; tiles past the last one read tile 0 (their score
-  // columns are never written).  The first pairs go out before anything
-  // else so their latency overlaps the prologue.
+  // columns are never written).  Round u of a head moves query tiles
+  // qt0 + 2u and qt0 + 2u + 1.
   const int qt0 = q_base >> 4;
+  const bool qfull = qt0 + 4 <= n_qt;
+  auto issue_q_round = [&](int h, int u) {
+    const int i = threadIdx.x + u * kPkWaves * 64;  // 16-byte piece
+    const int qt = qt0 + (i >> 8);                  // 256 pieces per tile
+    const int64_t src = ((int64_t)h * n_qt + ((qfull || qt < n_qt) ? qt : 0)) * 2048 + (i & 255) * 8;
+    dma16(Qp + src, &sh.q[h % kPkRing][(u * kPkWaves * 64 + 64 * wave) * 8]);
+  };
   auto issue_q = [&](int h) {
-    const bool full = qt0 + 4 <= n_qt;
 #pragma unroll
-    for (int u = 0; u < kPkQRounds; u++) {
-      const int i = threadIdx.x + u * kPkWaves * 64;  // 16-byte piece
-      const int qt = qt0 + (i >> 8);                  // 256 pieces per tile
-      const int64_t src = ((int64_t)h * n_qt + ((full || qt < n_qt) ? qt : 0)) * 2048 + (i & 255) * 8;
-      dma16(Qp + src, &sh.q[h % kPkRing][(u * kPkWaves * 64 + 64 * wave) * 8]);
-    }
+    for (int u = 0; u < kPkQRounds; u++) issue_q_round(h, u);
   };
   constexpr int kAhead = kPkRing / 2 - 1;  // head pairs issued ahead
-#pragma unroll
-  for (int h = 0; h < 2 * kAhead; h++) issue_q(h);
 
-  // ---- prologue: seq lens, head weights and block-table entries are
-  // independent loads; the key rows follow the block-table entries ----
+  // ---- prologue ----
+  // fp16 keys: the tile's 256 key rows (64 KB) are copied by LDS-DMA into
+  // ring slots 2..5 before any Q is requested, each 256-B row stored with
+  // its 16-byte pieces XOR-swizzled by the key's low 4 bits so that the
+  // A-operand reads below are free of bank conflicts; the first head pair
+  // follows, and pairs 1 and 2 go out once every wave has its keys in
+  // registers.  fp8 keys are converted on the way to registers instead.
+  // Keys are gathered with the block-table row of the tile's first query
+  // (all rows of a call share one table).
+  const int key0 = p_base + kPkWaveKeys * (wave & 3);  // this wave's 64 keys
+  const int qb0 = 2 * half;                            // its query blocks
+  const int32_t* bt_row = block_table + (int64_t)q_base * max_blocks;
+  const int page = 1 << page_shift;
+  constexpr int kKRounds = kPkKT * kIdxHeadDim * 2 / 16 / (kPkWaves * 64);  // 8
+  int32_t kbt[KFP8 ? 4 : kKRounds];
+  if constexpr (!KFP8) {
+#pragma unroll
+    for (int u = 0; u < kKRounds; u++) {
+      const int p = p_base + ((threadIdx.x + u * kPkWaves * 64) >> 4);
+      const int pg = p >> page_shift;
+      kbt[u] = (p < max_kv && pg < max_blocks) ? bt_row[pg] : -1;
+    }
+  } else {
+    for (int h = 0; h < 2 * kAhead; h++) issue_q(h);
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++) {
+      const int p = key0 + 16 * kb + c;
+      const int pg = p >> page_shift;
+      kbt[kb] = (p < max_kv && pg < max_blocks) ? bt_row[pg] : -1;
+    }
+  }
   int sl_v = 0;  // wave 0: query q_base + lane
   if (threadIdx.x < kPkQT) {
     const int q = q_base + threadIdx.x;
@@ -299,46 +336,49 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
     const int h = i / kPkQT, q = q_base + i % kPkQT;
     wv[u] = (q < B) ? (float)W[(int64_t)q * kIdxHeads + h] : 0.f;
   }
-  const int key0 = p_base + 32 * wave;  // this wave's 32 keys
-  // Keys are gathered with the block-table row of the tile's first query
-  // (all rows of a call share one table).
-  const int32_t* bt_row = block_table + (int64_t)q_base * max_blocks;
-  const int page = 1 << page_shift;
-  int32_t pbk[2];
-#pragma unroll
-  for (int kb = 0; kb < 2; kb++) {
-    const int p = key0 + 16 * kb + c;
-    const int pg = p >> page_shift;
-    pbk[kb] = (p < max_kv && pg < max_blocks) ? bt_row[pg] : -1;
-  }
-  // A operands: this wave's keys (2 blocks of 16), dims 32s + 8g .. +8 for
+  // A operands: this wave's keys (4 blocks of 16), dims 32s + 8g .. +8 for
   // the 4 x32 steps.
-  f16x8 ka[2][4];
+  f16x8 ka[4][4];
+  f16* const kl = sh.q[2];  // fp16 key rows, slots 2..5
+  if constexpr (!KFP8) {
 #pragma unroll
-  for (int kb = 0; kb < 2; kb++) {
-    const int p = key0 + 16 * kb + c;
-    const int64_t r = ((int64_t)pbk[kb] << page_shift) + (p & (page - 1));
-    const int64_t row = (pbk[kb] >= 0 && r < n_kv_rows) ? r : -1;
+    for (int u = 0; u < kKRounds; u++) {
+      const int i = threadIdx.x + u * kPkWaves * 64;  // LDS 16-byte unit
+      const int key = i >> 4;
+      const int p = p_base + key;
+      const int64_t r = ((int64_t)kbt[u] << page_shift) + (p & (page - 1));
+      const f16* src = (kbt[u] >= 0 && r < n_kv_rows)
+                           ? reinterpret_cast<const f16*>(Kv) + r * kIdxHeadDim +
+                                 (((i & 15) ^ (key & 15)) << 3)
+                           : kIdxZeroPiece;
+      dma16(src, &kl[(u * kPkWaves * 64 + 64 * wave) * 8]);
+    }
+    issue_q(0);
+    issue_q(1);
+  } else {
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-      if (row < 0) {
-        ka[kb][s] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-      } else if constexpr (KFP8) {
-        const uint8_t* rp = reinterpret_cast<const uint8_t*>(Kv) +
-                            row * (int64_t)kIdxkFp8RowBytes;
-        const u32x2 raw =
-            *reinterpret_cast<const u32x2*>(rp + 32 * s + 8 * g);  // 4-B aligned
-        const float sc = *reinterpret_cast<const float*>(rp + 128);
-        float v[8];
-        e4m3x4_to_f32_div256(raw[0], v);
-        e4m3x4_to_f32_div256(raw[1], v + 4);
-        f16x8 h;
+    for (int kb = 0; kb < 4; kb++) {
+      const int p = key0 + 16 * kb + c;
+      const int64_t r = ((int64_t)kbt[kb] << page_shift) + (p & (page - 1));
+      const int64_t row = (kbt[kb] >= 0 && r < n_kv_rows) ? r : -1;
 #pragma unroll
-        for (int e = 0; e < 8; e++) h[e] = (f16)(v[e] * (sc * 256.0f));
-        ka[kb][s] = h;
-      } else {
-        ka[kb][s] = *reinterpret_cast<const f16x8*>(
-            reinterpret_cast<const f16*>(Kv) + row * kIdxHeadDim + 32 * s + 8 * g);
+      for (int s = 0; s < 4; s++) {
+        if (row < 0) {
+          ka[kb][s] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+        } else {
+          const uint8_t* rp = reinterpret_cast<const uint8_t*>(Kv) +
+                              row * (int64_t)kIdxkFp8RowBytes;
+          const u32x2 raw =
+              *reinterpret_cast<const u32x2*>(rp + 32 * s + 8 * g);  // 4-B aligned
+          const float sc = *reinterpret_cast<const float*>(rp + 128);
+          float v[8];
+          e4m3x4_to_f32_div256(raw[0], v);
+          e4m3x4_to_f32_div256(raw[1], v + 4);
+          f16x8 h;
+#pragma unroll
+          for (int e = 0; e < 8; e++) h[e] = (f16)(v[e] * (sc * 256.0f));
+          ka[kb][s] = h;
+        }
       }
     }
   }
@@ -354,6 +394,7 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
     for (int o = 32; o >= 1; o >>= 1) m = max(m, __shfl_xor(m, o, 64));
     if (lane == 0) sh.maxsl = m;
   }
+  if constexpr (!KFP8) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // keys, pair 0
   __syncthreads();
 
   if (p_base >= sh.maxsl) {
@@ -367,95 +408,108 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
     return;
   }
 
-  f32x4 sacc[2][4];  // [key block][query block], relu*w summed over heads
-  f32x4 accp[2][4];  // S of the previous head, epilogue pending
+  if constexpr (!KFP8) {
 #pragma unroll
-  for (int kb = 0; kb < 2; kb++)
+    for (int kb = 0; kb < 4; kb++) {
+      const int key = kPkWaveKeys * (wave & 3) + 16 * kb + c;  // key & 15 == c
 #pragma unroll
-    for (int qb = 0; qb < 4; qb++) {
-      sacc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      accp[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      for (int s2 = 0; s2 < 4; s2++)
+        ka[kb][s2] = *reinterpret_cast<const f16x8*>(&kl[(key * 16 + ((4 * s2 + g) ^ c)) * 8]);
     }
+    lds_barrier();  // every wave holds its keys: slots 2..5 are free for Q
+#pragma unroll
+    for (int h = 2; h < 2 * kAhead; h++) issue_q(h);
+  }
 
-  for (int h0 = 0; h0 < kIdxHeads; h0 += 2) {
-    const int j = h0 >> 1;
-    pk_wait(min(kIdxHeads / 2 - 1 - j, kAhead - 1));
-    lds_barrier();  // pair j landed; every wave is done with pair j - 1
-    if (j + kAhead < kIdxHeads / 2) {
-      issue_q(h0 + 2 * kAhead);
-      issue_q(h0 + 2 * kAhead + 1);
+  // Heads alternate between two accumulator sets: while the MFMAs of head h
+  // fill one, the relu * w epilogue of head h - 1 drains the other, a
+  // quarter (one key block) per x32 step.  The B operands of step st + 1 are
+  // read from LDS during step st, so no MFMA waits on an LDS read except the
+  // first of a pair (right after the barrier).
+  f32x4 sacc[4][2];  // [key block][query block], relu*w summed over heads
+  f32x4 accA[4][2], accB[4][2];
+#pragma unroll
+  for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+      sacc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      accB[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
     }
-    // Software pipeline: the relu * w epilogue of head h - 1 is interleaved
-    // with the MFMAs of head h (independent instructions), so the VALU work
-    // overlaps the matrix cores instead of following them.
+  // B operand: query column c of tile qb0 + qb, dims 32st + 8g .. +8, i.e.
+  // packed chunk (kt = 2st + g/2, row c, half 8*(g&1))
+  const int boff = qb0 * 2048 + (g >> 1) * 256 + c * 16 + 8 * (g & 1);
+  auto load_b = [&](const f16* qs, int st, f16x8 (&b)[2]) {
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++) {
-      const int h = h0 + hh;
-      const f16* qs = sh.q[h % kPkRing];
-      f16x8 bq[4][4];
+    for (int qb = 0; qb < 2; qb++)
+      b[qb] = *reinterpret_cast<const f16x8*>(&qs[boff + qb * 2048 + st * 512]);
+  };
+  auto head = [&](int h, f32x4 (&acc)[4][2], f32x4 (&prev)[4][2], f16x8 (&bn)[2],
+                  bool next_in_pair, bool dma) {
+    const f16* qs = sh.q[h % kPkRing];
+    const f16* qs1 = sh.q[(h + 1) % kPkRing];
+    float wq[2];
 #pragma unroll
-      for (int st = 0; st < 4; st++)
+    for (int qb = 0; qb < 2; qb++) wq[qb] = (h > 0) ? sh.w[h - 1][16 * (qb0 + qb) + c] : 0.f;
 #pragma unroll
-        for (int qb = 0; qb < 4; qb++)
-          // B operand: query column c of tile qb, dims 32st + 8g .. +8, i.e.
-          // packed chunk (kt = 2st + g/2, row c, half 8*(g&1))
-          bq[st][qb] = *reinterpret_cast<const f16x8*>(
-              &qs[qb * 2048 + (2 * st + (g >> 1)) * 256 + c * 16 + 8 * (g & 1)]);
-      float wq[4];
-      const int hp = h - 1;
+    for (int st = 0; st < 4; st++) {
+      const f16x8 bc[2] = {bn[0], bn[1]};
+      if (st < 3) load_b(qs, st + 1, bn);
+      else if (next_in_pair) load_b(qs1, 0, bn);
+      if (dma && (st & 1) == 0) issue_q_round(h + 2 * kAhead, st >> 1);
 #pragma unroll
-      for (int qb = 0; qb < 4; qb++) wq[qb] = (hp >= 0) ? sh.w[hp][16 * qb + c] : 0.f;
-      f32x4 acc[2][4];
+      for (int qb = 0; qb < 2; qb++)
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++)
+        for (int kb = 0; kb < 4; kb++)
+          acc[kb][qb] = mfma16x16x32(ka[kb][st], bc[qb],
+                                     st == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : acc[kb][qb]);
 #pragma unroll
-        for (int qb = 0; qb < 4; qb++) acc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      for (int qb = 0; qb < 2; qb++)
 #pragma unroll
-      for (int st = 0; st < 4; st++)
+        for (int r = 0; r < 4; r++) sacc[st][qb][r] += relu1(prev[st][qb][r]) * wq[qb];
 #pragma unroll
-        for (int qb = 0; qb < 4; qb++)
-#pragma unroll
-          for (int kb = 0; kb < 2; kb++) acc[kb][qb] = mfma16x16x32(ka[kb][st], bq[st][qb], acc[kb][qb]);
-      // epilogue of the previous head (accp holds zeros before head 0)
-#pragma unroll
-      for (int qb = 0; qb < 4; qb++)
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) sacc[kb][qb][r] += relu1(accp[kb][qb][r]) * wq[qb];
-      // one MFMA, then two VALU, repeated
-#pragma unroll
-      for (int i = 0; i < 32; i++) {
+      for (int i = 0; i < 8; i++) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
       }
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int qb = 0; qb < 4; qb++) accp[kb][qb] = acc[kb][qb];
     }
-  }
-  {
+  };
+
+  // Pair j (heads 2j, 2j + 1): the two heads of pair j + kAhead are loaded
+  // during it, one LDS-DMA round every other x32 step.  The refilling and
+  // the draining pairs are separate loops so that neither has a branch
+  // inside its MFMA sequence.
+  auto pair = [&](int j, bool refill) {
+    const int h0 = 2 * j;
+    pk_wait(min(kIdxHeads / 2 - 1 - j, kAhead - 1));
+    lds_barrier();  // pair j landed; every wave is done with pair j - 1
+    f16x8 bn[2];
+    load_b(sh.q[h0 % kPkRing], 0, bn);
+    head(h0, accA, accB, bn, true, refill);
+    head(h0 + 1, accB, accA, bn, false, refill);
+  };
+#pragma nounroll
+  for (int j = 0; j < kIdxHeads / 2 - kAhead; j++) pair(j, true);
+#pragma nounroll
+  for (int j = kIdxHeads / 2 - kAhead; j < kIdxHeads / 2; j++) pair(j, false);
 #pragma unroll
-    for (int qb = 0; qb < 4; qb++) {
-      const float wl = sh.w[kIdxHeads - 1][16 * qb + c];
+  for (int qb = 0; qb < 2; qb++) {
+    const float wl = sh.w[kIdxHeads - 1][16 * (qb0 + qb) + c];
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++)
+    for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) sacc[kb][qb][r] += relu1(accp[kb][qb][r]) * wl;
-    }
+      for (int r = 0; r < 4; r++) sacc[kb][qb][r] += relu1(accB[kb][qb][r]) * wl;
   }
 
   // D layout: lane (query col c, key rows 4g+r) -> 4 consecutive keys.
 #pragma unroll
-  for (int qb = 0; qb < 4; qb++) {
-    const int qi = 16 * qb + c;
+  for (int qb = 0; qb < 2; qb++) {
+    const int qi = 16 * (qb0 + qb) + c;
     const int q = q_base + qi;
     if (q >= B) continue;
     const int sl = sh.sl[qi];
     float* srow = score + (int64_t)q * max_kv;
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++) {
+    for (int kb = 0; kb < 4; kb++) {
       const int p0 = key0 + 16 * kb + 4 * g;
       f32x4 v;
 #pragma unroll
