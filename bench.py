@@ -449,6 +449,19 @@ def main():
         }
         log(f"indexer prefill: {ptf:.1f} TFLOPS ({pms:.2f} ms)")
         torch.cuda.empty_cache()
+        # the same prefill in 1024-row sub-chunks: the caller's 128-row split
+        # bounds the fp32 score buffer for a 32 GB card; at 1024 rows the
+        # buffer is 256 MB and every launch fills the chip
+        pms, pflops = bench_indexer_prefill(torch, pkg, dev, sub=1024)
+        ptf = pflops / (pms * 1e-3) / 1e12
+        line["indexer_prefill_sub1024"] = {
+            "tflops": round(ptf, 2),
+            "ms": round(pms, 3),
+            "frac_fp16_peak": round(ptf / FP16_PEAK_TFLOPS, 4),
+            "workload": "as indexer_prefill, 1024-row sub-chunks (256 MB score buffer)",
+        }
+        log(f"indexer prefill, 1024-row sub-chunks: {ptf:.1f} TFLOPS ({pms:.2f} ms)")
+        torch.cuda.empty_cache()
     if "sparse_prefill" in extras:
         for fp8 in (True, False):
             key = "sparse_prefill_fp8" if fp8 else "sparse_prefill_fp16"

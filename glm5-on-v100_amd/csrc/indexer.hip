@@ -275,15 +275,21 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
   const int c = lane & 15, g = lane >> 4;
 
   // Q ring: head h of the 4 query tiles [qt0, qt0 + 4) is 16 KB contiguous
-  // in the packed layout; tiles past the last one read tile 0 (their score
-  // columns are never written).  Round u of a head moves query tiles
-  // qt0 + 2u and qt0 + 2u + 1.
+  // in the packed layout ([kt 8][row 16][dims 16] per tile); tiles past the
+  // last one read tile 0 (their score columns are never written).  In LDS
+  // the 16-byte pieces are reordered to the MFMA B-operand order: unit
+  // (tile, step st, lane c + 16g) holds row c, dims 32st + 8g .. +8, so
+  // that each B read of a wave is 1 KB contiguous (no bank conflicts).  The
+  // 64 pieces of one DMA instruction still come from 1 KB of global memory.
+  // Round u of a head moves query tiles qt0 + 2u and qt0 + 2u + 1.
   const int qt0 = q_base >> 4;
   const bool qfull = qt0 + 4 <= n_qt;
   auto issue_q_round = [&](int h, int u) {
-    const int i = threadIdx.x + u * kPkWaves * 64;  // 16-byte piece
-    const int qt = qt0 + (i >> 8);                  // 256 pieces per tile
-    const int64_t src = ((int64_t)h * n_qt + ((qfull || qt < n_qt) ? qt : 0)) * 2048 + (i & 255) * 8;
+    const int i = threadIdx.x + u * kPkWaves * 64;  // LDS 16-byte unit
+    const int qt = qt0 + (i >> 8);                  // 256 units per tile
+    const int st = (i >> 6) & 3, gg = (i >> 4) & 3, cc = i & 15;
+    const int piece = (2 * st + (gg >> 1)) * 32 + cc * 2 + (gg & 1);
+    const int64_t src = ((int64_t)h * n_qt + ((qfull || qt < n_qt) ? qt : 0)) * 2048 + piece * 8;
     dma16(Qp + src, &sh.q[h % kPkRing][(u * kPkWaves * 64 + 64 * wave) * 8]);
   };
   auto issue_q = [&](int h) {
@@ -435,26 +441,37 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
       sacc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
       accB[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
     }
-  // B operand: query column c of tile qb0 + qb, dims 32st + 8g .. +8, i.e.
-  // packed chunk (kt = 2st + g/2, row c, half 8*(g&1))
-  const int boff = qb0 * 2048 + (g >> 1) * 256 + c * 16 + 8 * (g & 1);
+  // B operand: query column c of tile qb0 + qb, dims 32st + 8g .. +8, at LDS
+  // unit (tile, st, lane)
+  const int boff = qb0 * 2048 + lane * 8;
   auto load_b = [&](const f16* qs, int st, f16x8 (&b)[2]) {
 #pragma unroll
     for (int qb = 0; qb < 2; qb++)
       b[qb] = *reinterpret_cast<const f16x8*>(&qs[boff + qb * 2048 + st * 512]);
   };
+  // load_w: the weights of head h for this lane's two query columns (one
+  // ds_read2)
+  auto load_w = [&](int h, float (&w2)[2]) {
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) w2[qb] = sh.w[h][16 * (qb0 + qb) + c];
+  };
+  // head h: MFMAs into acc, epilogue of head h - 1 (prev, weights wn); with
+  // next_in_pair, its last step also reads head h + 1's first B operands and
+  // the weights of head h into bn / wn
   auto head = [&](int h, f32x4 (&acc)[4][2], f32x4 (&prev)[4][2], f16x8 (&bn)[2],
-                  bool next_in_pair, bool dma) {
+                  float (&wn)[2], bool next_in_pair, bool dma) {
     const f16* qs = sh.q[h % kPkRing];
     const f16* qs1 = sh.q[(h + 1) % kPkRing];
-    float wq[2];
-#pragma unroll
-    for (int qb = 0; qb < 2; qb++) wq[qb] = (h > 0) ? sh.w[h - 1][16 * (qb0 + qb) + c] : 0.f;
+    const float wq[2] = {wn[0], wn[1]};
 #pragma unroll
     for (int st = 0; st < 4; st++) {
       const f16x8 bc[2] = {bn[0], bn[1]};
-      if (st < 3) load_b(qs, st + 1, bn);
-      else if (next_in_pair) load_b(qs1, 0, bn);
+      if (st < 3) {
+        load_b(qs, st + 1, bn);
+      } else if (next_in_pair) {
+        load_b(qs1, 0, bn);
+        load_w(h, wn);
+      }
       if (dma && (st & 1) == 0) issue_q_round(h + 2 * kAhead, st >> 1);
 #pragma unroll
       for (int qb = 0; qb < 2; qb++)
@@ -466,11 +483,15 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
       for (int qb = 0; qb < 2; qb++)
 #pragma unroll
         for (int r = 0; r < 4; r++) sacc[st][qb][r] += relu1(prev[st][qb][r]) * wq[qb];
+      // the next step's LDS reads first, then one MFMA and two VALU, repeated
+      if (st < 3) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      else if (next_in_pair) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);  // steps do not mix
     }
   };
 
@@ -483,9 +504,11 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
     pk_wait(min(kIdxHeads / 2 - 1 - j, kAhead - 1));
     lds_barrier();  // pair j landed; every wave is done with pair j - 1
     f16x8 bn[2];
+    float wn[2] = {0.f, 0.f};
     load_b(sh.q[h0 % kPkRing], 0, bn);
-    head(h0, accA, accB, bn, true, refill);
-    head(h0 + 1, accB, accA, bn, false, refill);
+    if (h0 > 0) load_w(h0 - 1, wn);
+    head(h0, accA, accB, bn, wn, true, refill);
+    head(h0 + 1, accB, accA, bn, wn, false, refill);
   };
 #pragma nounroll
   for (int j = 0; j < kIdxHeads / 2 - kAhead; j++) pair(j, true);
