@@ -213,37 +213,44 @@ __global__ void __launch_bounds__(kIdxWaves * 64) indexer_logits_kernel(
 // ===========================================================================
 // packed (prefill) kernel
 //
-// Workgroup tile = 64 queries (4 x 16) x 256 keys, 8 waves.  The tile
-// balances two limits: it is small enough that the caller's 128-row
-// sub-chunks launch ~256 workgroups at average causal reach, and wide enough
-// in keys (256 FLOP per byte of streamed Q) that the L2 -> CU stream of Q
-// stays below what one CU can ingest.
+// Full tile = 64 queries (4 x 16) x 256 keys, 8 waves.  The tile balances
+// two limits: it is small enough that the caller's 128-row sub-chunks launch
+// ~256 workgroups at average causal reach, and wide enough in keys (256 FLOP
+// per byte of streamed Q) that the L2 -> CU stream of Q stays below what one
+// CU can ingest.
 //
-// Wave w owns keys [64 (w & 3), +64) and query blocks 2 (w >> 2) + {0, 1}:
-// its 64 keys (4 blocks x 128 dims, fp16) stay resident as MFMA A operands
-// for all 32 heads, and per head it reads only its 32 queries' Q from LDS
-// (8 KB), so the 8 waves read 64 KB of LDS per head for 4.2 MFLOP.  The
-// packed Q of each head (16 KB for the 64 queries, contiguous in the packed
-// layout) streams through an 8-slot LDS ring filled by LDS-DMA three head
-// pairs ahead, the DMA rounds spread over the MFMA steps.  relu(S) * w is
-// summed over heads in registers, the epilogue of head h - 1 interleaved
-// with the MFMAs of head h.
+// Wave w owns keys [64 (w & 3), +64) and QB query blocks of 16 (QB = 2 in a
+// full tile): its 64 keys (4 blocks x 128 dims, fp16) stay resident as MFMA
+// A operands for all 32 heads, and per head it reads only its queries' Q
+// from LDS.  The packed Q of each head (16 KB for 64 queries, contiguous in
+// the packed layout) streams through an 8-slot LDS ring filled by LDS-DMA
+// three head pairs ahead, the DMA rounds spread over the MFMA steps.
+// relu(S) * w is summed over heads in registers, the epilogue of head h - 1
+// interleaved with the MFMAs of head h.
+//
+// A launch holds W full tiles.  A workgroup takes one full tile, or half of
+// one (QB = 1: 32 queries x 256 keys, same per-wave key set and the same
+// MFMA : LDS-read ratio, half the MFMAs): when W <= 128 every tile is split
+// in two so that the launch fills more CUs, and when W > 256 the last
+// W mod 256 tiles (if at most 128) are split so that the final partial round
+// of workgroups takes half as long.  Full tiles come first in launch order.
 // ===========================================================================
 constexpr int kPkWaves = 8;
-constexpr int kPkQT = 64;                  // queries per workgroup (4 x 16)
+constexpr int kPkThreads = kPkWaves * 64;
 constexpr int kPkKT = 256;                 // keys per workgroup
 constexpr int kPkWaveKeys = 64;            // keys per wave (4 blocks of 16)
 constexpr int kPkRing = 8;                 // Q ring slots (heads): 4 pairs
-constexpr int kPkQHead = 4 * 2048;         // halves of one head's Q for 4 query tiles
-// LDS-DMA ops per thread for one head
-constexpr int kPkQRounds = kPkQHead * 2 / 16 / (kPkWaves * 64);  // 2
+constexpr int kPkSlot = 4 * 2048;          // halves per ring slot (one head, 64 queries)
+constexpr int kPkMaxQT = 64;               // queries of a full tile
+constexpr int kPkHalfMax = 128;            // at most this many tiles are split per launch
+constexpr int kPkCUs = 256;                // workgroups of one full round (one per CU)
 
 __device__ const __align__(16) f16 kIdxZeroPiece[8] = {};  // source of unmapped key rows
 
 struct PkSmem {
-  f16 q[kPkRing][kPkQHead];
-  float w[kIdxHeads][kPkQT];
-  int32_t sl[kPkQT];
+  f16 q[kPkRing][kPkSlot];
+  float w[kIdxHeads][kPkMaxQT];
+  int32_t sl[kPkMaxQT];
   int maxsl;
 };
 
@@ -251,50 +258,65 @@ struct PkSmem {
 // first canonicalise its input under IEEE mode)
 __device__ __forceinline__ float relu1(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, FLT_MAX); }
 
-__device__ __forceinline__ void pk_wait(int k) {  // at most k head pairs in flight
+// at most k head pairs of Q (R LDS-DMA rounds per head) still in flight
+template <int R>
+__device__ __forceinline__ void pk_wait(int k) {
   switch (k) {
     case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kPkQRounds) : "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kPkQRounds) : "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * R) : "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * R) : "memory"); break;
   }
 }
 
-template <bool KFP8>
-__global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
-    const f16* __restrict__ Qp, const void* __restrict__ Kv,
-    const f16* __restrict__ W, const int32_t* __restrict__ block_table,
-    const int32_t* __restrict__ seq_lens, float* __restrict__ score, int B,
-    int64_t n_kv_rows, int max_blocks, int page_shift, int max_kv) {
-  __shared__ PkSmem sh;
-  const int q_base = blockIdx.y * kPkQT;
-  const int p_base = blockIdx.x * kPkKT;
+struct PkArgs {
+  const f16* Qp;
+  const void* Kv;
+  const f16* W;
+  const int32_t* block_table;
+  const int32_t* seq_lens;
+  float* score;
+  int B;
+  int64_t n_kv_rows;
+  int max_blocks, page_shift, max_kv;
+  int n_kt;    // key tiles per query tile
+  int n_full;  // workgroups that take a whole tile
+};
+
+// One workgroup tile: queries [q_base, q_base + 32 QB) x keys [p_base, +256).
+template <bool KFP8, int QB>
+__device__ __forceinline__ void pk_tile(const PkArgs& a, PkSmem& sh, int q_base, int p_base) {
+  constexpr int QT = 32 * QB;                          // queries of the tile
+  constexpr int QROUNDS = QT * 256 / 16 / kPkThreads;  // LDS-DMA ops per thread per head
+  const f16* __restrict__ Qp = a.Qp;
+  const int B = a.B, max_kv = a.max_kv, page_shift = a.page_shift, max_blocks = a.max_blocks;
   const int n_qt = (B + 15) >> 4;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int half = wave >> 2;           // query-block pair
+  const int half = wave >> 2;           // query-block group
   const int c = lane & 15, g = lane >> 4;
 
-  // Q ring: head h of the 4 query tiles [qt0, qt0 + 4) is 16 KB contiguous
-  // in the packed layout ([kt 8][row 16][dims 16] per tile); tiles past the
-  // last one read tile 0 (their score columns are never written).  In LDS
-  // the 16-byte pieces are reordered to the MFMA B-operand order: unit
-  // (tile, step st, lane c + 16g) holds row c, dims 32st + 8g .. +8, so
-  // that each B read of a wave is 1 KB contiguous (no bank conflicts).  The
-  // 64 pieces of one DMA instruction still come from 1 KB of global memory.
-  // Round u of a head moves query tiles qt0 + 2u and qt0 + 2u + 1.
+  // Q ring: head h of the tile's 2 QB query tiles [qt0, qt0 + 2 QB) is
+  // contiguous in the packed layout ([kt 8][row 16][dims 16] per tile);
+  // tiles past the last one read tile 0 (their score columns are never
+  // written).  In LDS the 16-byte pieces are reordered to the MFMA B-operand
+  // order: unit (tile, step st, lane c + 16g) holds row c, dims 32st + 8g ..
+  // +8, so that each B read of a wave is 1 KB contiguous (no bank
+  // conflicts).  The 64 pieces of one DMA instruction still come from 1 KB
+  // of global memory.  Round u of a head moves query tiles qt0 + 2u and
+  // qt0 + 2u + 1.
   const int qt0 = q_base >> 4;
-  const bool qfull = qt0 + 4 <= n_qt;
+  const bool qfull = qt0 + 2 * QB <= n_qt;
   auto issue_q_round = [&](int h, int u) {
-    const int i = threadIdx.x + u * kPkWaves * 64;  // LDS 16-byte unit
-    const int qt = qt0 + (i >> 8);                  // 256 units per tile
+    const int i = threadIdx.x + u * kPkThreads;  // LDS 16-byte unit
+    const int qt = qt0 + (i >> 8);               // 256 units per tile
     const int st = (i >> 6) & 3, gg = (i >> 4) & 3, cc = i & 15;
     const int piece = (2 * st + (gg >> 1)) * 32 + cc * 2 + (gg & 1);
     const int64_t src = ((int64_t)h * n_qt + ((qfull || qt < n_qt) ? qt : 0)) * 2048 + piece * 8;
-    dma16(Qp + src, &sh.q[h % kPkRing][(u * kPkWaves * 64 + 64 * wave) * 8]);
+    dma16(Qp + src, &sh.q[h % kPkRing][(u * kPkThreads + 64 * wave) * 8]);
   };
   auto issue_q = [&](int h) {
 #pragma unroll
-    for (int u = 0; u < kPkQRounds; u++) issue_q_round(h, u);
+    for (int u = 0; u < QROUNDS; u++) issue_q_round(h, u);
   };
   constexpr int kAhead = kPkRing / 2 - 1;  // head pairs issued ahead
 
@@ -308,15 +330,15 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
   // Keys are gathered with the block-table row of the tile's first query
   // (all rows of a call share one table).
   const int key0 = p_base + kPkWaveKeys * (wave & 3);  // this wave's 64 keys
-  const int qb0 = 2 * half;                            // its query blocks
-  const int32_t* bt_row = block_table + (int64_t)q_base * max_blocks;
+  const int qb0 = QB * half;                           // its first query block
+  const int32_t* bt_row = a.block_table + (int64_t)q_base * max_blocks;
   const int page = 1 << page_shift;
-  constexpr int kKRounds = kPkKT * kIdxHeadDim * 2 / 16 / (kPkWaves * 64);  // 8
+  constexpr int kKRounds = kPkKT * kIdxHeadDim * 2 / 16 / kPkThreads;  // 8
   int32_t kbt[KFP8 ? 4 : kKRounds];
   if constexpr (!KFP8) {
 #pragma unroll
     for (int u = 0; u < kKRounds; u++) {
-      const int p = p_base + ((threadIdx.x + u * kPkWaves * 64) >> 4);
+      const int p = p_base + ((threadIdx.x + u * kPkThreads) >> 4);
       const int pg = p >> page_shift;
       kbt[u] = (p < max_kv && pg < max_blocks) ? bt_row[pg] : -1;
     }
@@ -330,17 +352,17 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
     }
   }
   int sl_v = 0;  // wave 0: query q_base + lane
-  if (threadIdx.x < kPkQT) {
+  if (threadIdx.x < QT) {
     const int q = q_base + threadIdx.x;
-    sl_v = (q < B) ? seq_lens[q] : 0;
+    sl_v = (q < B) ? a.seq_lens[q] : 0;
   }
-  constexpr int WPT = kIdxHeads * kPkQT / (kPkWaves * 64);
+  constexpr int WPT = kIdxHeads * QT / kPkThreads;
   float wv[WPT];
 #pragma unroll
   for (int u = 0; u < WPT; u++) {
-    const int i = threadIdx.x + u * kPkWaves * 64;
-    const int h = i / kPkQT, q = q_base + i % kPkQT;
-    wv[u] = (q < B) ? (float)W[(int64_t)q * kIdxHeads + h] : 0.f;
+    const int i = threadIdx.x + u * kPkThreads;
+    const int h = i / QT, q = q_base + i % QT;
+    wv[u] = (q < B) ? (float)a.W[(int64_t)q * kIdxHeads + h] : 0.f;
   }
   // A operands: this wave's keys (4 blocks of 16), dims 32s + 8g .. +8 for
   // the 4 x32 steps.
@@ -349,15 +371,15 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
   if constexpr (!KFP8) {
 #pragma unroll
     for (int u = 0; u < kKRounds; u++) {
-      const int i = threadIdx.x + u * kPkWaves * 64;  // LDS 16-byte unit
+      const int i = threadIdx.x + u * kPkThreads;  // LDS 16-byte unit
       const int key = i >> 4;
       const int p = p_base + key;
       const int64_t r = ((int64_t)kbt[u] << page_shift) + (p & (page - 1));
-      const f16* src = (kbt[u] >= 0 && r < n_kv_rows)
-                           ? reinterpret_cast<const f16*>(Kv) + r * kIdxHeadDim +
+      const f16* src = (kbt[u] >= 0 && r < a.n_kv_rows)
+                           ? reinterpret_cast<const f16*>(a.Kv) + r * kIdxHeadDim +
                                  (((i & 15) ^ (key & 15)) << 3)
                            : kIdxZeroPiece;
-      dma16(src, &kl[(u * kPkWaves * 64 + 64 * wave) * 8]);
+      dma16(src, &kl[(u * kPkThreads + 64 * wave) * 8]);
     }
     issue_q(0);
     issue_q(1);
@@ -366,13 +388,13 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
     for (int kb = 0; kb < 4; kb++) {
       const int p = key0 + 16 * kb + c;
       const int64_t r = ((int64_t)kbt[kb] << page_shift) + (p & (page - 1));
-      const int64_t row = (kbt[kb] >= 0 && r < n_kv_rows) ? r : -1;
+      const int64_t row = (kbt[kb] >= 0 && r < a.n_kv_rows) ? r : -1;
 #pragma unroll
       for (int s = 0; s < 4; s++) {
         if (row < 0) {
           ka[kb][s] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
         } else {
-          const uint8_t* rp = reinterpret_cast<const uint8_t*>(Kv) +
+          const uint8_t* rp = reinterpret_cast<const uint8_t*>(a.Kv) +
                               row * (int64_t)kIdxkFp8RowBytes;
           const u32x2 raw =
               *reinterpret_cast<const u32x2*>(rp + 32 * s + 8 * g);  // 4-B aligned
@@ -390,8 +412,8 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
   }
 #pragma unroll
   for (int u = 0; u < WPT; u++) {
-    const int i = threadIdx.x + u * kPkWaves * 64;
-    sh.w[i / kPkQT][i % kPkQT] = wv[u];
+    const int i = threadIdx.x + u * kPkThreads;
+    sh.w[i / QT][i % QT] = wv[u];
   }
   if (wave == 0) {
     sh.sl[lane] = sl_v;
@@ -405,10 +427,10 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
 
   if (p_base >= sh.maxsl) {
     // no query of this tile reaches these keys: -inf padding only
-    for (int e = threadIdx.x; e < kPkQT * kPkKT; e += blockDim.x) {
+    for (int e = threadIdx.x; e < QT * kPkKT; e += blockDim.x) {
       const int qi = e / kPkKT, p = p_base + e % kPkKT;
       const int q = q_base + qi;
-      if (q < B && p < max_kv) score[(int64_t)q * max_kv + p] = -INFINITY;
+      if (q < B && p < max_kv) a.score[(int64_t)q * max_kv + p] = -INFINITY;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS-DMA may outlive the LDS
     return;
@@ -432,62 +454,65 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
   // quarter (one key block) per x32 step.  The B operands of step st + 1 are
   // read from LDS during step st, so no MFMA waits on an LDS read except the
   // first of a pair (right after the barrier).
-  f32x4 sacc[4][2];  // [key block][query block], relu*w summed over heads
-  f32x4 accA[4][2], accB[4][2];
+  f32x4 sacc[4][QB];  // [key block][query block], relu*w summed over heads
+  f32x4 accA[4][QB], accB[4][QB];
 #pragma unroll
   for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
+    for (int qb = 0; qb < QB; qb++) {
       sacc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
       accB[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
     }
   // B operand: query column c of tile qb0 + qb, dims 32st + 8g .. +8, at LDS
   // unit (tile, st, lane)
   const int boff = qb0 * 2048 + lane * 8;
-  auto load_b = [&](const f16* qs, int st, f16x8 (&b)[2]) {
+  auto load_b = [&](const f16* qs, int st, f16x8 (&b)[QB]) {
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++)
+    for (int qb = 0; qb < QB; qb++)
       b[qb] = *reinterpret_cast<const f16x8*>(&qs[boff + qb * 2048 + st * 512]);
   };
-  // load_w: the weights of head h for this lane's two query columns (one
-  // ds_read2)
-  auto load_w = [&](int h, float (&w2)[2]) {
+  // load_w: the weights of head h for this lane's query columns
+  auto load_w = [&](int h, float (&w2)[QB]) {
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++) w2[qb] = sh.w[h][16 * (qb0 + qb) + c];
+    for (int qb = 0; qb < QB; qb++) w2[qb] = sh.w[h][16 * (qb0 + qb) + c];
   };
   // head h: MFMAs into acc, epilogue of head h - 1 (prev, weights wn); with
   // next_in_pair, its last step also reads head h + 1's first B operands and
   // the weights of head h into bn / wn
-  auto head = [&](int h, f32x4 (&acc)[4][2], f32x4 (&prev)[4][2], f16x8 (&bn)[2],
-                  float (&wn)[2], bool next_in_pair, bool dma) {
+  auto head = [&](int h, f32x4 (&acc)[4][QB], f32x4 (&prev)[4][QB], f16x8 (&bn)[QB],
+                  float (&wn)[QB], bool next_in_pair, bool dma) {
     const f16* qs = sh.q[h % kPkRing];
     const f16* qs1 = sh.q[(h + 1) % kPkRing];
-    const float wq[2] = {wn[0], wn[1]};
+    float wq[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++) wq[qb] = wn[qb];
 #pragma unroll
     for (int st = 0; st < 4; st++) {
-      const f16x8 bc[2] = {bn[0], bn[1]};
+      f16x8 bc[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; qb++) bc[qb] = bn[qb];
       if (st < 3) {
         load_b(qs, st + 1, bn);
       } else if (next_in_pair) {
         load_b(qs1, 0, bn);
         load_w(h, wn);
       }
-      if (dma && (st & 1) == 0) issue_q_round(h + 2 * kAhead, st >> 1);
+      if (dma && (st & 1) == 0 && (st >> 1) < QROUNDS) issue_q_round(h + 2 * kAhead, st >> 1);
 #pragma unroll
-      for (int qb = 0; qb < 2; qb++)
+      for (int qb = 0; qb < QB; qb++)
 #pragma unroll
         for (int kb = 0; kb < 4; kb++)
           acc[kb][qb] = mfma16x16x32(ka[kb][st], bc[qb],
                                      st == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : acc[kb][qb]);
 #pragma unroll
-      for (int qb = 0; qb < 2; qb++)
+      for (int qb = 0; qb < QB; qb++)
 #pragma unroll
         for (int r = 0; r < 4; r++) sacc[st][qb][r] += relu1(prev[st][qb][r]) * wq[qb];
       // the next step's LDS reads first, then one MFMA and two VALU, repeated
-      if (st < 3) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      else if (next_in_pair) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      if (st < 3) __builtin_amdgcn_sched_group_barrier(0x100, QB, 0);
+      else if (next_in_pair) __builtin_amdgcn_sched_group_barrier(0x100, 2 * QB, 0);
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
+      for (int i = 0; i < 4 * QB; i++) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
       }
@@ -496,15 +521,16 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
   };
 
   // Pair j (heads 2j, 2j + 1): the two heads of pair j + kAhead are loaded
-  // during it, one LDS-DMA round every other x32 step.  The refilling and
-  // the draining pairs are separate loops so that neither has a branch
-  // inside its MFMA sequence.
+  // during it.  The refilling and the draining pairs are separate loops so
+  // that neither has a branch inside its MFMA sequence.
   auto pair = [&](int j, bool refill) {
     const int h0 = 2 * j;
-    pk_wait(min(kIdxHeads / 2 - 1 - j, kAhead - 1));
+    pk_wait<QROUNDS>(min(kIdxHeads / 2 - 1 - j, kAhead - 1));
     lds_barrier();  // pair j landed; every wave is done with pair j - 1
-    f16x8 bn[2];
-    float wn[2] = {0.f, 0.f};
+    f16x8 bn[QB];
+    float wn[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++) wn[qb] = 0.f;
     load_b(sh.q[h0 % kPkRing], 0, bn);
     if (h0 > 0) load_w(h0 - 1, wn);
     head(h0, accA, accB, bn, wn, true, refill);
@@ -515,7 +541,7 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
 #pragma nounroll
   for (int j = kIdxHeads / 2 - kAhead; j < kIdxHeads / 2; j++) pair(j, false);
 #pragma unroll
-  for (int qb = 0; qb < 2; qb++) {
+  for (int qb = 0; qb < QB; qb++) {
     const float wl = sh.w[kIdxHeads - 1][16 * (qb0 + qb) + c];
 #pragma unroll
     for (int kb = 0; kb < 4; kb++)
@@ -525,12 +551,12 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
 
   // D layout: lane (query col c, key rows 4g+r) -> 4 consecutive keys.
 #pragma unroll
-  for (int qb = 0; qb < 2; qb++) {
+  for (int qb = 0; qb < QB; qb++) {
     const int qi = 16 * (qb0 + qb) + c;
     const int q = q_base + qi;
     if (q >= B) continue;
     const int sl = sh.sl[qi];
-    float* srow = score + (int64_t)q * max_kv;
+    float* srow = a.score + (int64_t)q * max_kv;
 #pragma unroll
     for (int kb = 0; kb < 4; kb++) {
       const int p0 = key0 + 16 * kb + 4 * g;
@@ -546,6 +572,32 @@ __global__ void __launch_bounds__(kPkWaves * 64) indexer_logits_packed_kernel(
       }
     }
   }
+}
+
+// Workgroups [0, n_full) take full tiles t = blockIdx.x (key tile t % n_kt
+// of 64-query tile t / n_kt); the rest take halves of tiles n_full, ...
+// (two consecutive workgroups per tile, 32 queries each).
+template <bool KFP8>
+__global__ void __launch_bounds__(kPkThreads) indexer_logits_packed_kernel(PkArgs a) {
+  __shared__ PkSmem sh;
+  const int id = blockIdx.x;
+  if (id < a.n_full) {
+    pk_tile<KFP8, 2>(a, sh, (id / a.n_kt) * kPkMaxQT, (id % a.n_kt) * kPkKT);
+  } else {
+    const int j = id - a.n_full;
+    const int t = a.n_full + (j >> 1);
+    const int q_base = (t / a.n_kt) * kPkMaxQT + 32 * (j & 1);
+    if (q_base >= a.B) return;  // a half tile past the last query (no DMA issued yet)
+    pk_tile<KFP8, 1>(a, sh, q_base, (t % a.n_kt) * kPkKT);
+  }
+}
+
+// Tiles of a launch with W full tiles that run as two half tiles.
+static int pk_split_tiles(int64_t W) {
+  if (W <= kPkHalfMax) return (int)W;
+  if (W <= kPkCUs) return 0;
+  const int r = (int)(W % kPkCUs);
+  return r <= kPkHalfMax ? r : 0;
 }
 
 }  // namespace mi355dsa
@@ -612,21 +664,30 @@ extern "C" int mi355_dsa_indexer_logits_packed(
   DSA_CHECK(k_fp8 ? aligned_to(k_cache, 4) : aligned_to(k_cache, 16),
             "k_cache is misaligned");
   DSA_CHECK(aligned_to(score, 16), "score must be 16-byte aligned");
-  const int qtiles = (B + kPkQT - 1) / kPkQT;
-  DSA_CHECK(qtiles <= 65535, "B too large");
-  const dim3 grid((max_kv + kPkKT - 1) / kPkKT, qtiles);
-  const int shift = ilog2_pow2(page_size);
+  const int64_t n_kt = (max_kv + kPkKT - 1) / kPkKT;
+  const int64_t W = n_kt * ((B + kPkMaxQT - 1) / kPkMaxQT);
+  const int split = pk_split_tiles(W);
+  const int64_t grid = W + split;
+  DSA_CHECK(grid <= INT32_MAX, "B x max_kv too large");
+  PkArgs a;
+  a.Qp = reinterpret_cast<const f16*>(q_packed);
+  a.Kv = k_cache;
+  a.W = reinterpret_cast<const f16*>(weights);
+  a.block_table = block_table;
+  a.seq_lens = seq_lens;
+  a.score = score;
+  a.B = B;
+  a.n_kv_rows = n_kv_rows;
+  a.max_blocks = max_blocks;
+  a.page_shift = ilog2_pow2(page_size);
+  a.max_kv = max_kv;
+  a.n_kt = (int)n_kt;
+  a.n_full = (int)(W - split);
   hipStream_t st = as_stream(stream);
   if (k_fp8)
-    indexer_logits_packed_kernel<true><<<grid, kPkWaves * 64, 0, st>>>(
-        reinterpret_cast<const f16*>(q_packed), k_cache,
-        reinterpret_cast<const f16*>(weights), block_table, seq_lens, score, B,
-        n_kv_rows, max_blocks, shift, max_kv);
+    indexer_logits_packed_kernel<true><<<dim3((unsigned)grid), kPkThreads, 0, st>>>(a);
   else
-    indexer_logits_packed_kernel<false><<<grid, kPkWaves * 64, 0, st>>>(
-        reinterpret_cast<const f16*>(q_packed), k_cache,
-        reinterpret_cast<const f16*>(weights), block_table, seq_lens, score, B,
-        n_kv_rows, max_blocks, shift, max_kv);
+    indexer_logits_packed_kernel<false><<<dim3((unsigned)grid), kPkThreads, 0, st>>>(a);
   DSA_LAUNCH_CHECK("indexer_logits_packed");
   return MI355_DSA_OK;
 }

@@ -149,6 +149,62 @@ def test_packed_matches_decode_kernel_on_dyadic(ops, dev):
     assert torch.equal(a, b)
 
 
+# Launch shapes of the packed kernel's tile split (full tiles are 64 queries
+# x 256 keys; W = tiles per launch): all full (W = 200), full tiles plus a
+# tail run as half tiles (W = 260 -> 256 + 4 split; W = 280 with a partial
+# last query tile -> 256 + 24 split), and the fp8-key variant of the mixed
+# case.
+SPLIT = [
+    # seed, B, max_kv, fp8
+    (31, 128, 256 * 100, False),
+    (32, 128, 256 * 130, False),
+    (33, 100, 256 * 140, False),
+    (34, 128, 256 * 130, True),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT, ids=[f"B{c[1]}_kv{c[2]}_{'fp8' if c[3] else 'f16'}"
+                                             for c in SPLIT])
+def test_packed_tile_split(ops, dev, case):
+    """Dyadic inputs: the packed kernel equals the decode kernel bit for bit
+    (fp16 keys) on every row, and the oracle on sampled rows, whatever mix of
+    full and half tiles the launch uses."""
+    seed, B, max_kv, fp8 = case
+    page = 64
+    nblk = max_kv // page + 3
+    q, kc, w, bt1, _ = make_case(seed, 1, nblk, page, fp8, True, max_kv, [max_kv])
+    g = torch.Generator().manual_seed(seed + 7)
+    q = (torch.randint(-8, 9, (B, 32, 128), generator=g) / 8).to(torch.float16)
+    w = (torch.randint(-4, 5, (B, 32), generator=g) / 4).to(torch.float16)
+    bt = bt1.expand(B, bt1.shape[1]).contiguous()
+    seq = torch.arange(max_kv - B + 1, max_kv + 1, dtype=torch.int32)
+    b = torch.full((B, max_kv), 7.0, device=dev)
+    ops.sm70_indexer_logits_packed(b, O.pack_indexer_q(q).to(dev), kc.to(dev), w.to(dev),
+                                   bt.to(dev), seq.to(dev))
+    got = b.cpu()
+    rows = [0, 31, 32, 63, 64, B - 1]
+    if fp8:
+        flat = kc.view(-1, 132)
+        k16 = (O.e4m3_decode(flat[:, :128].contiguous()) *
+               flat[:, 128:].contiguous().view(torch.float32)).to(torch.float16)
+        kc_ref = k16.view(nblk, page, 128)
+    else:
+        kc_ref = kc
+        a = torch.full((B, max_kv), 7.0, device=dev)
+        ops.sm70_indexer_logits(a, q.to(dev), kc.to(dev), w.to(dev), bt.to(dev), seq.to(dev),
+                                None)
+        assert torch.equal(a.cpu(), got)
+    want, _ = O.indexer_logits(q[rows], kc_ref, w[rows], bt[rows], seq[rows], max_kv)
+    sub = got[rows]
+    assert torch.equal(torch.isinf(sub), torch.isinf(want))
+    fin = torch.isfinite(want)
+    if fp8:
+        tol = 1e-5 * want[fin].abs().max().item() + 1e-6
+        assert (sub[fin] - want[fin]).abs().max().item() <= tol
+    else:
+        assert torch.equal(sub[fin], want[fin])
+
+
 def test_decode_c2_full_size(ops, pkg, dev):
     """Config C2 (B=4, 64k keys, ~1% duplicated keys) against an fp32 torch
     computation on the GPU (gather + matmul + relu*w), then top-k bit-exact
