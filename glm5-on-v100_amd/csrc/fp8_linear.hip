@@ -49,8 +49,23 @@ __global__ void __launch_bounds__(256) fp8_dequant_kernel(
 // ---------------------------------------------------------------------------
 // GEMV.  k-slot mapping inside a 128-wide k block: step s (0..3), lane group
 // g, slot e  ->  k = 32g + 8s + e.  A lane therefore reads 32 contiguous
-// weight bytes and 64 contiguous x bytes per k block.
+// weight bytes and 64 contiguous x bytes per k block; the 4 lanes of a row
+// cover its 128-byte line.
+//
+// Wave w of a workgroup takes k blocks w, w + WAVES, ... of the workgroup's
+// 16 NB weight rows, one block at a time (load, then MFMAs).  Latency is
+// hidden by occupancy rather than by a register ring: at ~56-74 VGPRs a SIMD
+// holds 6-8 waves, and on this part that streams faster than deeper
+// per-wave prefetch at lower occupancy (measured).  Loads of k blocks past
+// the end are clamped to the last block (in bounds, scale 0).
 // ---------------------------------------------------------------------------
+template <int NB>
+struct GemvFrag {
+  f16x8 a[4];  // x, A operand
+  u32x4 b0[NB], b1[NB];
+  float sc[NB];  // block scale x 256 (0 past the end)
+};
+
 template <int NB, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64) fp8_gemv_kernel(
     const f16* __restrict__ x, const uint8_t* __restrict__ w,
@@ -67,13 +82,18 @@ __global__ void __launch_bounds__(WAVES * 64) fp8_gemv_kernel(
 
   const bool xrow = c < M;
   const f16* xr = x + (int64_t)(xrow ? c : 0) * K;
+  // weight rows of this lane (clamped into the matrix; rows >= N get scale 0)
+  const uint8_t* wr[NB];
+  const float* sr[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    wr[j] = w + (int64_t)min(n_base + 16 * j + c, N - 1) * K + 32 * g;
+    sr[j] = s + (int64_t)(min(n_base + 16 * j, N - 1) >> 7) * KB;
+  }
 
-  // One 128-wide k block: x fragment (A operand) and NB weight fragments.
-  struct Frag {
-    f16x8 a[4];
-    u32x4 b0[NB], b1[NB];
-  };
-  auto load = [&](int kb, Frag& f) {
+  auto load = [&](int kb, GemvFrag<NB>& f) {
+    const bool ok = kb < KB;
+    kb = min(kb, KB - 1);
     const int kvalid = K - kb * 128;  // multiple of 16
     const int kofs = kb * 128 + 32 * g;
 #pragma unroll
@@ -84,44 +104,37 @@ __global__ void __launch_bounds__(WAVES * 64) fp8_gemv_kernel(
     }
 #pragma unroll
     for (int j = 0; j < NB; j++) {
-      const int n = n_base + 16 * j + c;
       f.b0[j] = (u32x4){0u, 0u, 0u, 0u};
       f.b1[j] = (u32x4){0u, 0u, 0u, 0u};
-      if (n < N) {
-        const uint8_t* wr = w + (int64_t)n * K + kofs;
-        if (32 * g < kvalid) f.b0[j] = *reinterpret_cast<const u32x4*>(wr);
-        if (32 * g + 16 < kvalid) f.b1[j] = *reinterpret_cast<const u32x4*>(wr + 16);
-      }
+      const uint8_t* p = wr[j] + kb * 128;
+      if (32 * g < kvalid) f.b0[j] = *reinterpret_cast<const u32x4*>(p);
+      if (32 * g + 16 < kvalid) f.b1[j] = *reinterpret_cast<const u32x4*>(p + 16);
+      // every row of a 16-row column block shares one 128x128 scale block
+      f.sc[j] = (ok && n_base + 16 * j < N) ? sr[j][kb] * 256.0f : 0.f;
     }
   };
 
-  Frag cur, nxt;
-  if (wave < KB) load(wave, cur);
-  for (int kb = wave; kb < KB; kb += WAVES) {
-    if (kb + WAVES < KB) load(kb + WAVES, nxt);  // in flight during compute
+  const int nk = (KB + WAVES - 1) / WAVES;  // uniform trip count
+  for (int i = 0; i < nk; i++) {
+    GemvFrag<NB> f;
+    load(wave + WAVES * i, f);
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       f32x4 t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const uint32_t d0 = (q < 2) ? cur.b0[j][2 * q] : cur.b1[j][2 * (q - 2)];
-        const uint32_t d1 = (q < 2) ? cur.b0[j][2 * q + 1] : cur.b1[j][2 * (q - 2) + 1];
+        const uint32_t d0 = (q < 2) ? f.b0[j][2 * q] : f.b1[j][2 * (q - 2)];
+        const uint32_t d1 = (q < 2) ? f.b0[j][2 * q + 1] : f.b1[j][2 * (q - 2) + 1];
         u32x4 h;
         h[0] = e4m3x2_to_f16x2_div256(spread_lo(d0));
         h[1] = e4m3x2_to_f16x2_div256(spread_hi(d0));
         h[2] = e4m3x2_to_f16x2_div256(spread_lo(d1));
         h[3] = e4m3x2_to_f16x2_div256(spread_hi(d1));
-        t = mfma16x16x32(cur.a[q], __builtin_bit_cast(f16x8, h), t);
+        t = mfma16x16x32(f.a[q], __builtin_bit_cast(f16x8, h), t);
       }
-      // every row of this 16-row column block shares one 128x128 scale block
-      const int nb_row = (n_base + 16 * j) >> 7;
-      const float sc = (n_base + 16 * j < N)
-                           ? s[(int64_t)nb_row * KB + kb] * 256.0f
-                           : 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; r++) acc[j][r] += sc * t[r];
+      for (int r = 0; r < 4; r++) acc[j][r] += f.sc[j] * t[r];
     }
-    cur = nxt;
   }
 
   // reduce the WAVES partial sums through LDS
@@ -205,13 +218,11 @@ __global__ void __launch_bounds__(256) fp8_quantize_kernel(const f16* __restrict
   }
 }
 
-template <int NB>
+template <int NB, int WAVES>
 static void launch_gemv(const f16* x, const uint8_t* w, const float* s, f16* y,
                         int M, int N, int K, int KB, hipStream_t st) {
-  constexpr int WAVES = 8;
   const int blocks = (N + 16 * NB - 1) / (16 * NB);
-  fp8_gemv_kernel<NB, WAVES><<<blocks, WAVES * 64, 0, st>>>(x, w, s, y, M, N, K,
-                                                           KB);
+  fp8_gemv_kernel<NB, WAVES><<<blocks, WAVES * 64, 0, st>>>(x, w, s, y, M, N, K, KB);
 }
 
 }  // namespace mi355dsa
@@ -231,11 +242,13 @@ extern "C" int mi355_dsa_attn_fp8_gemv(void* y, const void* x, const uint8_t* w,
   hipStream_t st = as_stream(stream);
   const f16* xp = reinterpret_cast<const f16*>(x);
   f16* yp = reinterpret_cast<f16*>(y);
-  // >= ~384 workgroups of 8 waves at the BASELINE shapes
+  // Large N: 32 rows x 8 waves per workgroup (768 workgroups at N = 24576,
+  // three resident per CU).  Smaller N: 16 rows x 16 waves, so that K is
+  // spread over enough waves to keep the matrix streaming.
   if (N >= 16384)
-    launch_gemv<2>(xp, w, s, yp, M, N, K, KB, st);
+    launch_gemv<2, 8>(xp, w, s, yp, M, N, K, KB, st);
   else
-    launch_gemv<1>(xp, w, s, yp, M, N, K, KB, st);
+    launch_gemv<1, 16>(xp, w, s, yp, M, N, K, KB, st);
   DSA_LAUNCH_CHECK("attn_fp8_gemv");
   return MI355_DSA_OK;
 }
