@@ -58,6 +58,7 @@ def test_k_store_fp8_ties_and_saturation(ops, dev):
     k[0, 1:9] = torch.tensor([1.0625, 1.1875, 2.0 ** -10, 3 * 2.0 ** -10, 7.5 * 2.0 ** -9,
                               -1.0625, 240.0, 0.1])
     k[1, 1] = -448.0
+    k[1, 2] = -0.0                                     # keeps its sign: code 0x80
     k[2, 1:] = torch.linspace(-447, 447, 127)
     k[3, 0] = 65504.0                                  # fp16 max
     k = k.to(torch.float16)
