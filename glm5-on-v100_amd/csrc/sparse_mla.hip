@@ -862,23 +862,14 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
 }
 
 // ---------------------------------------------------------------------------
-// fp8_ds_mla prefill with an LDS-DMA ring.
-//
-// Workgroup = one token x 64 heads, 8 waves (two per SIMD).  The token's
-// rows are resolved once, then 32-key tiles stream through a ring of
-// kPfRing LDS slots filled by global_load_lds_dwordx4, so up to kPfRing
-// tiles of gather latency are hidden behind the MFMA work on the others.
-// Wave w = (head group w%4, half w/4):
-//   * QK: S for keys [16 half, +16) of the tile and the group's 16 heads;
-//   * the pair of waves of a head group exchange tile maxima and exp(S - m)
-//     through LDS;
-//   * PV: O^T for value dims [256 half, +256) over all 32 keys of the tile
-//     (v_mfma_f32_16x16x32_f16; k-slots 0-3 = keys 4g..4g+3, 4-7 =
-//     16+4g..16+4g+3, V^T by 8-row transpose reads).
-// The softmax is online with a lazy running max shared by the pair: O and
-// l are rescaled only when a head's tile max exceeds the running max by more
-// than kPfLazyMax, so p = exp(s - m) <= e^8 (well inside fp16) and rescales
-// are rare; o = O / l and lse = m + ln l are unchanged by the choice of m.
+// fp8_ds_mla prefill: shared constants and the LDS-DMA tile gather.
+// 32-key tiles of raw 656-byte rows land in LDS slots by
+// global_load_lds_dwordx4 (piece q of a tile = key q / 41, 16-byte chunk
+// q % 41; padding pieces read a static zero row).  The running softmax max
+// is lazy: O and l are rescaled only when a head's tile max exceeds the
+// running max by more than kPfLazyMax, so p = exp(s - m) <= e^8 (well inside
+// fp16) and rescales are rare; o = O / l and lse = m + ln l are unchanged by
+// the choice of m.
 // ---------------------------------------------------------------------------
 constexpr int kPfWaves = 8;
 constexpr int kPfThreads = 64 * kPfWaves;
@@ -886,17 +877,7 @@ constexpr int kPfTileKeys = 32;
 constexpr int kPfPieces = kPfTileKeys * (kDsmlaRowBytes / 16);          // 1312
 constexpr int kPfRounds = (kPfPieces + kPfThreads - 1) / kPfThreads;    // 3 LDS-DMA ops per thread
 constexpr int kPfSlotBytes = kPfRounds * kPfThreads * 16;
-constexpr int kPfRing = 5;
-constexpr int kPfPPitch = kPfTileKeys + 4;  // fp32 P row pitch (floats)
 constexpr float kPfLazyMax = 8.0f;
-
-struct PfSmem {
-  uint8_t ring[kPfRing][kPfSlotBytes];
-  int32_t rows[kSegKeys];
-  float pt[4][16 * kPfPPitch];  // per head group: P[head][tile key]
-  float tmax[kPfWaves * 16];
-  float lsum[kPfWaves * 16];
-};
 
 // LDS-DMA gather of one 32-key tile (rows[0..32), -1 = masked) into a slot.
 __device__ __forceinline__ void pf_dma_tile(const uint8_t* __restrict__ kv, const int32_t* rows,
@@ -920,24 +901,75 @@ __device__ __forceinline__ void pf_dma_tile(const uint8_t* __restrict__ kv, cons
   }
 }
 
-__device__ __forceinline__ void pf_wait(int k) {  // at most k tiles still in flight
-  switch (k) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(1 * kPfRounds) : "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kPfRounds) : "memory"); break;
-    case 3: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * kPfRounds) : "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kPfRounds) : "memory"); break;
-  }
-}
-static_assert(kPfRing <= 5, "pf_wait covers up to 4 tiles in flight");
+// ---------------------------------------------------------------------------
+// fp8_ds_mla prefill, software-pipelined over 32-key tiles.
+//
+// Workgroup = one token x 64 heads, 8 waves; tiles stream through a 3-slot
+// LDS ring by LDS-DMA.  Every e4m3 byte of a tile is converted to fp16 once
+// per workgroup:
+//   * QK: wave w = (key block kb = w & 1, scale tile qd = w >> 1) computes
+//     S^T for keys [16 kb, +16) x all 64 heads over NoPE dims [128 qd, +128)
+//     (one fp8 scale tile) and RoPE dims [512 + 16 qd, +16); each converted
+//     key fragment feeds 4 head-group MFMAs with Q of all 64 heads for those
+//     dims resident in registers.  The four dim partials meet in LDS and are
+//     summed in a fixed order.
+//   * softmax: thread t owns head t / 8 and keys 4 (t % 8) .. +3; online
+//     softmax with a lazy running max (rescale only when a tile max exceeds
+//     it by more than kPfLazyMax); reductions over the 8 threads of a head
+//     are DPP butterflies; P is stored in fp16 already multiplied by each
+//     key's four tile scales.
+//   * PV: wave w owns value dims [64 w, +64) for all 64 heads; each V^T
+//     fragment (8-key transpose read of raw e4m3) is converted once and
+//     feeds 4 head-group MFMAs.
+// Two barrier-separated phases per tile: X = {PV of tile i, QK of tile i+1}
+// (independent MFMA streams that hide each other's LDS latency), then
+// Y = {softmax of tile i+1, LDS-DMA of tile i+3, wait for tile i+2}.
+// ---------------------------------------------------------------------------
+constexpr int kP3Ring = 3;
+constexpr int kP3SPitch = 36;  // floats per (dim quarter, head) row of S partials
+constexpr int kP3PPitch = 40;  // halves per (scale tile, head) row of P
 
-__global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_dma_kernel(MlaParams p) {
+struct P3Smem {
+  uint8_t ring[kP3Ring][kPfSlotBytes];
+  int32_t rows[kSegKeys];
+  float sp[4][64 * kP3SPitch];  // [dim quarter][head][key]
+  f16 pt[4][64 * kP3PPitch];    // [scale tile][head][key]: fp16(p * scale)
+  f32x4 alpha[16];              // [head % 16][head / 16]: rescale factor for PV
+  f32x4 lsum[16];               // [head % 16][head / 16]: final l
+  int rescale[2];               // tile parity: some head's running max moved
+};
+
+// DPP lane exchange inside rows of 16 (CTRL: quad_perm / row_half_mirror)
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// reductions over aligned groups of 8 lanes (the result is bitwise equal in
+// all 8 lanes: every step combines a value with its partner symmetrically)
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, dppf<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dppf<0x4E>(v));   // quad_perm [2,3,0,1]
+  return fmaxf(v, dppf<0x141>(v));  // row_half_mirror: quad 0 <-> quad 1
+}
+__device__ __forceinline__ float sum8(float v) {
+  v += dppf<0xB1>(v);
+  v += dppf<0x4E>(v);
+  return v + dppf<0x141>(v);
+}
+
+__device__ __forceinline__ void p3_wait(int k) {  // at most k tiles still in flight
+  if (k <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kPfRounds) : "memory");
+}
+static_assert(kP3Ring == 3, "p3_wait covers one tile in flight");
+
+__global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  PfSmem& sh = *reinterpret_cast<PfSmem*>(smem_raw);
+  P3Smem& sh = *reinterpret_cast<P3Smem*>(smem_raw);
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
-  const int hg = w & 3, half = w >> 2;
   const int c = lane & 15, g = lane >> 4;
+  const int kb = w & 1, qd = w >> 1;  // QK role
   // XCD-aware token order: consecutive tokens (overlapping top-k sets) share an XCD
   int b;
   {
@@ -946,34 +978,151 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_dma_kernel(MlaP
     const int per = nx >> 3, rem = nx & 7;
     b = xcd * per + (xcd < rem ? xcd : rem) + j;
   }
-  const int h0 = blockIdx.y * 64 + 16 * hg;
+  const int hbase = blockIdx.y * 64;
   const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
   const int seq_len = p.seq_lens[b];
 
-  // ---- Q fragments of the head group, k-slot order of dma_qk ----
-  f16x8 qf[18];
+  // ---- Q of all 64 heads for this wave's QK dims, scaled in fp16 ----
+  // NoPE step s: lane (head c of group hg, g) holds dims 128 qd + 32 g + 8 s .. +8
+  // RoPE: dims 512 + 16 qd + 4 g .. +4
+  f16x8 qn[4][4];
+  f16x4 qr[4];
   {
-    const int hq = h0 + c < p.n_head ? h0 + c : 0;
-    const f16* qr = p.q + ((int64_t)b * p.n_head + hq) * kLatentDim;
     const f16 sc = (f16)p.scale_h;
     const f16x8 sc8 = {sc, sc, sc, sc, sc, sc, sc, sc};
+    const f16x4 sc4 = {sc, sc, sc, sc};
 #pragma unroll
-    for (int s2 = 0; s2 < 8; s2++) {
-      qf[2 * s2] = *reinterpret_cast<const f16x8*>(qr + 64 * s2 + 16 * g) * sc8;
-      qf[2 * s2 + 1] = *reinterpret_cast<const f16x8*>(qr + 64 * s2 + 16 * g + 8) * sc8;
+    for (int hg = 0; hg < 4; hg++) {
+      const int h = hbase + 16 * hg + c;
+      const f16* qrow = p.q + ((int64_t)b * p.n_head + (h < p.n_head ? h : 0)) * kLatentDim;
+#pragma unroll
+      for (int s = 0; s < 4; s++)
+        qn[hg][s] = *reinterpret_cast<const f16x8*>(qrow + 128 * qd + 32 * g + 8 * s) * sc8;
+      qr[hg] = *reinterpret_cast<const f16x4*>(qrow + 512 + 16 * qd + 4 * g) * sc4;
     }
-#pragma unroll
-    for (int s3 = 0; s3 < 2; s3++)
-      qf[16 + s3] = *reinterpret_cast<const f16x8*>(qr + 512 + 32 * s3 + 8 * g) * sc8;
   }
 
-  constexpr int NT = kOTiles / 2;  // 16 O^T tiles: dims 256 half + 16t
-  f32x4 oacc[NT];
+  // softmax role: head sm_h, keys 4 sm_k .. +3 of a tile
+  const int sm_h = threadIdx.x >> 3, sm_k = threadIdx.x & 7;
+  float m_run = -1e30f, l_run = 0.f;  // identical in the 8 threads of a head
+
+  f32x4 oacc[4][4];  // [dim tile][head group]: O^T of dims 64 w + 16 t + ..
 #pragma unroll
-  for (int t = 0; t < NT; t++) oacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float m_run = -1e30f, l_run = 0.f;  // l_run: this wave's keys only
-  bool first = true;
-  float* ptab = sh.pt[hg];
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int hg = 0; hg < 4; hg++) oacc[t][hg] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const int st_pv = w >> 1;  // fp8 scale tile of this wave's value dims
+
+  // QK partial of the tile in slot cb -> sh.sp
+  auto qk = [&](const uint8_t* cb) {
+    const uint8_t* krow = cb + (16 * kb + c) * kDsmlaRowBytes;
+    const u32x4 k0 = *reinterpret_cast<const u32x4*>(krow + 128 * qd + 32 * g);
+    const u32x4 k1 = *reinterpret_cast<const u32x4*>(krow + 128 * qd + 32 * g + 16);
+    const f16x4 kr = *reinterpret_cast<const f16x4*>(krow + 528 + 2 * (16 * qd + 4 * g));
+    float ksc[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      ksc[r] = *reinterpret_cast<const float*>(cb + (16 * kb + 4 * g + r) * kDsmlaRowBytes + 512 +
+                                               4 * qd);
+    f32x4 accn[4], accr[4];
+#pragma unroll
+    for (int hg = 0; hg < 4; hg++) {
+      accn[hg] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      accr[hg] = mfma16x16x16(kr, qr[hg], (f32x4){0.f, 0.f, 0.f, 0.f});
+    }
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const uint32_t d0 = s < 2 ? k0[2 * s] : k1[2 * (s - 2)];
+      const uint32_t d1 = s < 2 ? k0[2 * s + 1] : k1[2 * (s - 2) + 1];
+      const f16x4 a0 = e4m3x4_to_f16x4(d0), a1 = e4m3x4_to_f16x4(d1);
+      const f16x8 kf = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+#pragma unroll
+      for (int hg = 0; hg < 4; hg++) accn[hg] = mfma16x16x32(kf, qn[hg][s], accn[hg]);
+    }
+#pragma unroll
+    for (int hg = 0; hg < 4; hg++) {
+      f32x4 v;
+#pragma unroll
+      for (int r = 0; r < 4; r++) v[r] = accr[hg][r] + ksc[r] * accn[hg][r];
+      *reinterpret_cast<f32x4*>(&sh.sp[qd][(16 * hg + c) * kP3SPitch + 16 * kb + 4 * g]) = v;
+    }
+  };
+
+  // softmax of the tile in slot cb (rows trows) from sh.sp -> sh.pt, alpha
+  auto softmax = [&](const uint8_t* cb, const int32_t* trows, int* flag) {
+    f32x4 s4 = *reinterpret_cast<const f32x4*>(&sh.sp[0][sm_h * kP3SPitch + 4 * sm_k]);
+#pragma unroll
+    for (int q = 1; q < 4; q++)
+      s4 += *reinterpret_cast<const f32x4*>(&sh.sp[q][sm_h * kP3SPitch + 4 * sm_k]);
+    const int4 vr = *reinterpret_cast<const int4*>(trows + 4 * sm_k);
+    f32x4 ks[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      ks[r] = *reinterpret_cast<const f32x4*>(cb + (4 * sm_k + r) * kDsmlaRowBytes + 512);
+    const int vv[4] = {vr.x, vr.y, vr.z, vr.w};
+    float mt = -1e30f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      s4[r] = vv[r] >= 0 ? s4[r] : -INFINITY;
+      mt = fmaxf(mt, s4[r]);
+    }
+    mt = max8(mt);
+    float alpha = 1.f;
+    if (mt > m_run + kPfLazyMax) {
+      const float m_new = fmaxf(m_run, mt);
+      alpha = __expf(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+      *flag = 1;
+    }
+    if (sm_k == 0) reinterpret_cast<float*>(&sh.alpha[sm_h & 15])[sm_h >> 4] = alpha;
+    f32x4 pr;
+    float ls = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      pr[r] = (s4[r] > -INFINITY) ? __expf(s4[r] - m_run) : 0.f;
+      ls += pr[r];
+    }
+    l_run += sum8(ls);
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+      f16x4 ph;
+#pragma unroll
+      for (int r = 0; r < 4; r++) ph[r] = (f16)(pr[r] * ks[r][st]);
+      *reinterpret_cast<f16x4*>(&sh.pt[st][sm_h * kP3PPitch + 4 * sm_k]) = ph;
+    }
+  };
+
+  // PV of the tile in slot cb with sh.pt (after applying sh.alpha)
+  auto pv = [&](const uint8_t* cb, bool rescale) {
+    if (rescale) {
+      const f32x4 al = sh.alpha[c];
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int hg = 0; hg < 4; hg++) oacc[t][hg] *= al[hg];
+    }
+    f16x8 pb[4];
+#pragma unroll
+    for (int hg = 0; hg < 4; hg++)
+      pb[hg] = *reinterpret_cast<const f16x8*>(&sh.pt[st_pv][(16 * hg + c) * kP3PPitch + 8 * g]);
+    // transpose source: lane i of a 16-lane group points at key 8g + i/2,
+    // bytes 64 w + 16 t + 8 (i % 2); lane j receives keys 8g .. 8g+7 at
+    // dim 64 w + 16 t + j
+    const uint8_t* vsrc = cb + (8 * g + (c >> 1)) * kDsmlaRowBytes + 64 * w + 8 * (c & 1);
+    s32x2 vt[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+      vt[t] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_s32x2*)(vsrc + 16 * t));
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const f16x4 lo = e4m3x4_to_f16x4((uint32_t)vt[t][0]);
+      const f16x4 hi = e4m3x4_to_f16x4((uint32_t)vt[t][1]);
+      const f16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+      for (int hg = 0; hg < 4; hg++) oacc[t][hg] = mfma16x16x32(av, pb[hg], oacc[t][hg]);
+    }
+  };
 
   for (int seg_lo = 0; seg_lo < p.topk; seg_lo += kSegKeys) {
     const int nkeys = min(p.topk - seg_lo, kSegKeys);
@@ -998,111 +1147,57 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_dma_kernel(MlaP
       }
     }
     lds_barrier();
-    // kPfRing - 1 tiles ahead; the last slot is refilled at the top of each
-    // iteration with the slot the previous tile used
-    const int ahead = min(kPfRing - 1, ntiles);
-    for (int i = 0; i < ahead; i++) pf_dma_tile(kv, sh.rows + i * kPfTileKeys, sh.ring[i]);
+    // prologue: tiles 0 and 1 in flight, QK + softmax of tile 0
+    pf_dma_tile(kv, sh.rows, sh.ring[0]);
+    if (ntiles > 1) pf_dma_tile(kv, sh.rows + kPfTileKeys, sh.ring[1]);
+    p3_wait(ntiles > 1 ? 1 : 0);
+    if (threadIdx.x == 0) sh.rescale[0] = 0;
+    lds_barrier();  // tile 0 landed
+    qk(sh.ring[0]);
+    lds_barrier();
+    softmax(sh.ring[0], sh.rows, &sh.rescale[0]);
+    if (ntiles > 2) pf_dma_tile(kv, sh.rows + 2 * kPfTileKeys, sh.ring[2]);
+    p3_wait(ntiles > 2 ? 1 : 0);  // tile 1 landed (this wave's part)
+    lds_barrier();
 
     for (int i = 0; i < ntiles; i++) {
-      pf_wait(min(ntiles, kPfRing - 1 + i) - 1 - i);
-      lds_barrier();  // tile i landed; every wave is done with tile i - 1
-      if (i + kPfRing - 1 < ntiles)
-        pf_dma_tile(kv, sh.rows + (i + kPfRing - 1) * kPfTileKeys,
-                    sh.ring[(i + kPfRing - 1) % kPfRing]);
-      const uint8_t* cb = sh.ring[i % kPfRing];
-      const int32_t* trows = sh.rows + i * kPfTileKeys;
-
-      // ---- S^T for keys [16 half, +16) ----
-      f32x4 ksc[4];
-      const f32x4 sv = dma_qk<false>(cb, 16 * half, trows, qf, ksc);
-      // ---- tile max of the head group (both halves) ----
-      float mt = -1e30f;
-#pragma unroll
-      for (int r = 0; r < 4; r++) mt = fmaxf(mt, sv[r]);
-      mt = fmaxf(mt, shfl_xor_f(mt, 16));
-      mt = fmaxf(mt, shfl_xor_f(mt, 32));
-      if (g == 0) sh.tmax[w * 16 + c] = mt;
-      lds_barrier();
-      mt = fmaxf(sh.tmax[hg * 16 + c], sh.tmax[(hg + 4) * 16 + c]);
-      // lazy running max (the pair sees the same values, so both decide alike)
-      if (__any(mt > m_run + kPfLazyMax)) {
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = __expf(m_run - m_new);
-        l_run *= alpha;
-        m_run = m_new;
-        if (!first) {
-#pragma unroll
-          for (int t = 0; t < NT; t++) oacc[t] *= alpha;
-        }
-      }
-      first = false;
-      f32x4 pr;
-      float ls = 0.f;
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        pr[r] = (sv[r] > -INFINITY) ? __expf(sv[r] - m_run) : 0.f;
-        ls += pr[r];
-      }
-      ls += shfl_xor_f(ls, 16);
-      ls += shfl_xor_f(ls, 32);
-      l_run += ls;
-      *reinterpret_cast<f32x4*>(&ptab[c * kPfPPitch + 16 * half + 4 * g]) = pr;
-      lds_barrier();
-
-      // ---- O^T[dims 256 half + .. ] += V^T (P x tile scale)^T ----
-      const f32x4 p0 = *reinterpret_cast<const f32x4*>(&ptab[c * kPfPPitch + 4 * g]);
-      const f32x4 p1 = *reinterpret_cast<const f32x4*>(&ptab[c * kPfPPitch + 16 + 4 * g]);
-      // scales of this half's two tiles (2 half, 2 half + 1) for keys 4g+r, 16+4g+r
-      f32x2 s0[4], s1[4];
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        s0[r] = *reinterpret_cast<const f32x2*>(cb + (4 * g + r) * kDsmlaRowBytes + 512 + 8 * half);
-        s1[r] = *reinterpret_cast<const f32x2*>(cb + (16 + 4 * g + r) * kDsmlaRowBytes + 512 + 8 * half);
-      }
-      f16x8 pb[2];
-#pragma unroll
-      for (int sl = 0; sl < 2; sl++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          pb[sl][r] = (f16)(p0[r] * s0[r][sl]);
-          pb[sl][4 + r] = (f16)(p1[r] * s1[r][sl]);
-        }
-      // transpose source: lane i of a 16-lane group points at row i/2 of
-      // {4g..4g+3, 16+4g..16+4g+3}, bytes 256 half + 16t + 8(i%2)
-      const int vkey = ((c >> 1) < 4) ? 4 * g + (c >> 1) : 16 + 4 * g + ((c >> 1) - 4);
-      const uint8_t* vsrc = cb + vkey * kDsmlaRowBytes + 256 * half + 8 * (c & 1);
-#pragma unroll
-      for (int t0 = 0; t0 < NT; t0 += 8) {
-        s32x2 vt[8];
-#pragma unroll
-        for (int t = 0; t < 8; t++)
-          vt[t] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_s32x2*)(vsrc + 16 * (t0 + t)));
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-          const f16x4 lo = e4m3x4_to_f16x4((uint32_t)vt[t][0]);
-          const f16x4 hi = e4m3x4_to_f16x4((uint32_t)vt[t][1]);
-          const f16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          oacc[t0 + t] = mfma16x16x32(av, pb[(t0 + t) >> 3], oacc[t0 + t]);
-        }
+      // ---- X: PV of tile i, QK of tile i + 1 ----
+      const bool rescale = sh.rescale[i & 1] != 0;
+      if (threadIdx.x == 0) sh.rescale[(i + 1) & 1] = 0;  // read by PV(i - 1), set by softmax(i + 1)
+      pv(sh.ring[i % kP3Ring], rescale);
+      if (i + 1 < ntiles) qk(sh.ring[(i + 1) % kP3Ring]);
+      lds_barrier();  // PV(i) read pt / alpha; sp of tile i+1 is complete
+      if (i + 1 < ntiles) {
+        // ---- Y: softmax of tile i + 1, DMA of tile i + 3 into tile i's slot ----
+        softmax(sh.ring[(i + 1) % kP3Ring], sh.rows + (i + 1) * kPfTileKeys,
+                &sh.rescale[(i + 1) & 1]);
+        if (i + 3 < ntiles) pf_dma_tile(kv, sh.rows + (i + 3) * kPfTileKeys, sh.ring[i % kP3Ring]);
+        p3_wait(i + 3 < ntiles ? 1 : 0);  // tile i + 2 landed (this wave's part)
+        lds_barrier();
       }
     }
   }
 
-  // ---- l over both halves, then o = O / l for dims 256 half + 16t + 4g + r ----
-  if (g == 0) sh.lsum[w * 16 + c] = l_run;
+  // ---- l and lse per head, then o = O / l ----
+  if (sm_k == 0) {
+    reinterpret_cast<float*>(&sh.lsum[sm_h & 15])[sm_h >> 4] = l_run;
+    const int h = hbase + sm_h;
+    if (h < p.n_head)
+      p.lse[(int64_t)b * p.n_head + h] = (l_run > 0.f) ? (m_run + logf(l_run)) : p.empty_lse;
+  }
   lds_barrier();
-  const float L = sh.lsum[hg * 16 + c] + sh.lsum[(hg + 4) * 16 + c];
-  const int h = h0 + c;
-  if (h < p.n_head) {
-    const int64_t bh = (int64_t)b * p.n_head + h;
-    if (half == 0 && g == 0) p.lse[bh] = (L > 0.f) ? (m_run + logf(L)) : p.empty_lse;
-    const float inv = (L > 0.f) ? 1.f / L : 0.f;
-    f16* orow = p.o + bh * kValueDim + 256 * half;
+  const f32x4 L = sh.lsum[c];
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
+  for (int hg = 0; hg < 4; hg++) {
+    const int h = hbase + 16 * hg + c;
+    if (h >= p.n_head) continue;
+    const float inv = (L[hg] > 0.f) ? 1.f / L[hg] : 0.f;
+    f16* orow = p.o + ((int64_t)b * p.n_head + h) * kValueDim + 64 * w;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
       f16x4 v;
 #pragma unroll
-      for (int r = 0; r < 4; r++) v[r] = (f16)(oacc[t][r] * inv);
+      for (int r = 0; r < 4; r++) v[r] = (f16)(oacc[t][hg][r] * inv);
       *reinterpret_cast<f16x4*>(orow + 16 * t + 4 * g) = v;
     }
   }
@@ -1280,11 +1375,11 @@ extern "C" int mi355_dsa_sparse_mla_decode(
     if (kv_fp8) {
       static bool pattr = false;
       if (!pattr) {
-        hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_mla_prefill_dma_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(PfSmem));
+        hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_mla_prefill_fp8_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(P3Smem));
         pattr = true;
       }
-      sparse_mla_prefill_dma_kernel<<<grid, kPfThreads, sizeof(PfSmem), st>>>(prm);
+      sparse_mla_prefill_fp8_kernel<<<grid, kPfThreads, sizeof(P3Smem), st>>>(prm);
       return check_launch("sparse_mla_decode");
     }
     return launch_mla<false, 4, 1, 2>(prm, grid, st);

@@ -116,6 +116,18 @@ def test_prefill_config(ops, dev):
     check(o, lse, ro, rl)
 
 
+def test_prefill_config_segments_partial_heads(ops, dev):
+    """Prefill configuration with a partial second 64-head group (H = 80),
+    top-k past one 2048-key segment, and invalid / out-of-range entries."""
+    B = 128
+    seqs = [2600 + 5 * i for i in range(B)]
+    q, kv, idx, bt, seq = make(22, B, 80, 60, 64, True, 2304, seqs, invalid_frac=0.05,
+                               shared_bt=True)
+    o, lse = run(ops, dev, q, kv, idx, bt, seq)
+    ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
+    check(o, lse, ro, rl)
+
+
 def test_prefill_equals_decode_config(ops, dev):
     """Split-count / configuration invariance: the first rows of a 256-token
     batch (prefill configuration) equal the same rows run alone (decode
