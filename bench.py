@@ -306,7 +306,8 @@ def bench_gemv(torch, pkg, dev):
 
 
 def bench_k_store(torch, pkg, dev, n_tok=65536, copies=8):
-    """Config C5b: indexer-K scatter of 64k tokens into random unique slots."""
+    """Config C5b: indexer-K scatter of 64k tokens into random unique slots, and
+    the fp8_ds_mla latent-cache writer on 64k tokens."""
     ops = pkg._sm70_ops
     g = torch.Generator(device=dev)
     g.manual_seed(7)
@@ -328,6 +329,26 @@ def bench_k_store(torch, pkg, dev, n_tok=65536, copies=8):
         out["fp8" if fp8 else "fp16"] = {"us": round(us, 2), "gbps": round(gbps, 1),
                                          "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
         del ks, slots, caches
+    # latent-cache writer (concat_and_cache_mla, fp8_ds_mla): the same 64k
+    # tokens as kv_c [T, 512] + k_pe [T, 64] fp16 into 656-byte rows
+    cops = pkg._cache_ops
+    kvs = [torch.randn(n_tok, 576, generator=g, device=dev).to(torch.float16)
+           for _ in range(copies)]
+    slots = [torch.randperm(n_tok, generator=g, device=dev) for _ in range(copies)]
+    caches = [torch.zeros(n_tok // 64, 64, 656, dtype=torch.uint8, device=dev)
+              for _ in range(copies)]
+    one = torch.ones((), device=dev)
+
+    def fn2():
+        for kv, sl, c in zip(kvs, slots, caches):
+            cops.concat_and_cache_mla(kv[:, :512], kv[:, 512:], c, sl, "fp8_ds_mla", one)
+
+    us = graph_time_per_call(torch, fn2, copies)
+    nbytes = n_tok * (1152 + 8 + 656)
+    gbps = nbytes / (us * 1e-6) / 1e9
+    out["latent_fp8_ds_mla"] = {"us": round(us, 2), "gbps": round(gbps, 1),
+                                "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
+    del kvs, slots, caches
     return out
 
 

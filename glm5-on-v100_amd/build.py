@@ -53,6 +53,24 @@ def _compile(src: str) -> str:
     return obj
 
 
+TESTKIT_SRC = os.path.join(PKG_DIR, "..", "tests", "hip", "quant_exhaustive.hip")
+TESTKIT_LIB = os.path.join(PKG_DIR, "..", "tests", "hip", "libdsa_testkit.so")
+
+
+def build_testkit(verbose: bool = True) -> str:
+    """Builds the test-only kernels (tests/hip/*.hip) into
+    tests/hip/libdsa_testkit.so; the product library does not contain them."""
+    tmp = TESTKIT_LIB + ".tmp"
+    cmd = [hipcc(), *compile_flags(), "-shared", TESTKIT_SRC, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {TESTKIT_SRC}:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, TESTKIT_LIB)
+    if verbose:
+        print(f"built {os.path.normpath(TESTKIT_LIB)}", flush=True)
+    return TESTKIT_LIB
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
@@ -74,4 +92,5 @@ def build(verbose: bool = True) -> str:
 
 if __name__ == "__main__":
     build()
+    build_testkit()
     sys.exit(0)

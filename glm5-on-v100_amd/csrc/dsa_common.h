@@ -22,6 +22,7 @@
 // on the device.
 #pragma once
 
+#include <float.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -115,6 +116,71 @@ __device__ __forceinline__ uint32_t f32_to_e4m3_satfinite(float x) {
     if (code > 0x7eu) code = 0x7eu;
   }
   return sign | code;
+}
+
+// 8 values -> 8 e4m3 bytes of v / scale, RNE with SATFINITE, given
+// scale = max(amax / 448, FLT_MIN) of a group whose |values| <= amax.
+// For 2^-80 <= amax <= FLT_MAX (every finite fp16 amax but 0; bf16 amax
+// away from the bottom of the fp32 range, where the reciprocal and the
+// correction would leave normal numbers): v / scale via the reciprocal with
+// one Markstein correction
+// (r = RN(1/scale), y = RN(v r), rho = v - y scale exactly, q = RN(y + rho r),
+// the sign of v restored for v = -0), then the hardware RNE conversion
+// v_cvt_pk_fp8_f32.  Both steps were checked exhaustively on gfx950 against
+// IEEE division and f32_to_e4m3_satfinite: identical codes for every fp16
+// and every bf16 amax and every v of the same type with |v| <= amax, both
+// signs (all such quotients lie within +-448).  NaN inputs keep the
+// encoder's code (sign | 0x7f); any other amax (0, tiny, infinite) takes
+// IEEE division and the integer encoder.
+__device__ __forceinline__ u32x2 e4m3_quant8(const float v[8], float amax, float scale) {
+  uint32_t q0 = 0, q1 = 0;
+  if (amax <= FLT_MAX && amax >= 0x1p-80f) {
+    const float r = 1.0f / scale;
+    float q[8];
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float y = v[i] * r;
+      q[i] = __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-y, scale, v[i]), r, y), v[i]);
+      nan |= v[i] != v[i];
+    }
+    q0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+    q0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], (int)q0, true);
+    q1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
+    q1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], (int)q1, true);
+    if (nan) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        if (v[i] != v[i]) {
+          const uint32_t code = f32_to_e4m3_satfinite(v[i] / scale);
+          const int sh = 8 * (i & 3);
+          if (i < 4) q0 = (q0 & ~(0xffu << sh)) | (code << sh);
+          else q1 = (q1 & ~(0xffu << sh)) | (code << sh);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      q0 |= f32_to_e4m3_satfinite(v[i] / scale) << (8 * i);
+      q1 |= f32_to_e4m3_satfinite(v[4 + i] / scale) << (8 * i);
+    }
+  }
+  return (u32x2){q0, q1};
+}
+
+// DPP lane exchange inside rows of 16 lanes (CTRL: a quad_perm, row_mirror
+// or row_half_mirror code); the result depends only on the row's values.
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// max over aligned groups of 16 lanes, bitwise equal in all 16
+__device__ __forceinline__ float max16(float v) {
+  v = fmaxf(v, dppf<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dppf<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dppf<0x141>(v));  // row_half_mirror: quad 0 <-> quad 1
+  return fmaxf(v, dppf<0x140>(v));  // row_mirror: half-row 0 <-> half-row 1
 }
 
 // ---------------------------------------------------------------------------

@@ -939,11 +939,6 @@ struct P3Smem {
   int rescale[2];               // tile parity: some head's running max moved
 };
 
-// DPP lane exchange inside rows of 16 (CTRL: quad_perm / row_half_mirror)
-template <int CTRL>
-__device__ __forceinline__ float dppf(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
-}
 // reductions over aligned groups of 8 lanes (the result is bitwise equal in
 // all 8 lanes: every step combines a value with its partner symmetrically)
 __device__ __forceinline__ float max8(float v) {

@@ -47,6 +47,11 @@ SCHEMAS = {
     "persistent_topk": (
         "persistent_topk(Tensor logits, Tensor lengths, Tensor! output, "
         "Tensor workspace, int k, int max_seq_len) -> ()"),
+    # vLLM cache op (vllm/_custom_ops.py concat_and_cache_mla), the writer of
+    # the latent cache the sparse MLA kernels read
+    "concat_and_cache_mla": (
+        "concat_and_cache_mla(Tensor kv_c, Tensor k_pe, Tensor! kv_cache, "
+        "Tensor slot_mapping, str kv_cache_dtype, Tensor scale) -> ()"),
 }
 
 DSMLA_ROW_BYTES = 656
@@ -271,6 +276,49 @@ def indexer_k_store_impl(kv_cache, k, slot_mapping):
                   k.data_ptr(), n_tok, head_dim, slot_mapping.data_ptr(), _stream(k))
 
 
+def concat_and_cache_mla_impl(kv_c, k_pe, kv_cache, slot_mapping, kv_cache_dtype, scale):
+    """vLLM concat_and_cache_mla for kv_cache_dtype "auto" (fp16 rows of
+    kv_lora_rank + pe_dim) and "fp8_ds_mla" (656-byte rows); the token count
+    is slot_mapping's length (kv_c / k_pe may carry padding rows)."""
+    _check(kv_cache_dtype in ("auto", "fp8_ds_mla"),
+           f"concat_and_cache_mla: unsupported kv_cache_dtype {kv_cache_dtype!r}")
+    _check(kv_c.is_cuda and k_pe.is_cuda and kv_cache.is_cuda and slot_mapping.is_cuda,
+           "all tensors must be on the GPU")
+    _check(kv_c.dim() == 2 and k_pe.dim() == 2, "kv_c and k_pe must be 2-D")
+    _check(kv_c.size(1) == 512 and k_pe.size(1) == 64,
+           "kv_lora_rank must be 512 and the rope dim 64")
+    _check(slot_mapping.dtype in (torch.int64, torch.int32), "slot_mapping must be int64 or int32")
+    n_tok = slot_mapping.size(0)
+    _check(kv_c.size(0) >= n_tok and k_pe.size(0) >= n_tok, "fewer kv_c / k_pe rows than slots")
+    _check(kv_cache.is_contiguous(), "kv_cache must be contiguous")
+    fp8 = kv_cache_dtype == "fp8_ds_mla"
+    if fp8:
+        _check(kv_cache.dtype == torch.uint8 and kv_cache.size(-1) == DSMLA_ROW_BYTES,
+               "fp8_ds_mla kv_cache must be uint8 with last dim 656")
+        _check(kv_c.dtype in (torch.float16, torch.bfloat16) and k_pe.dtype == kv_c.dtype,
+               "kv_c and k_pe must be fp16 or bf16 of one dtype")
+        n_rows = kv_cache.numel() // DSMLA_ROW_BYTES
+    else:
+        _check(kv_cache.dtype == torch.float16 and kv_cache.size(-1) == 576,
+               "auto kv_cache must be fp16 with last dim 576")
+        _check(kv_c.dtype == torch.float16 and k_pe.dtype == torch.float16,
+               "kv_c and k_pe must be fp16")
+        n_rows = kv_cache.numel() // 576
+    if n_tok == 0:
+        return
+
+    def rows16(x):
+        ok = (x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0)
+        return x if ok else x.contiguous()
+
+    kv_c, k_pe, slot_mapping = rows16(kv_c), rows16(k_pe), _contig(slot_mapping)
+    with torch.cuda.device(kv_c.device):
+        _lib.call("mi355_dsa_concat_and_cache_mla", kv_cache.data_ptr(), int(fp8), n_rows,
+                  kv_c.data_ptr(), kv_c.stride(0), k_pe.data_ptr(), k_pe.stride(0),
+                  int(kv_c.dtype == torch.bfloat16), n_tok, slot_mapping.data_ptr(),
+                  int(slot_mapping.dtype == torch.int64), _stream(kv_c))
+
+
 def attn_fp8_gemv_impl(y, x, w, s):
     """sm70_attn_fp8.cu:148-191 checks."""
     _check(x.is_cuda and w.is_cuda and s.is_cuda and y.is_cuda, "all tensors must be on the GPU")
@@ -336,6 +384,7 @@ IMPLS = {
     "sm70_attn_fp8_gemv": attn_fp8_gemv_impl,
     "sm70_attn_fp8_dequant": attn_fp8_dequant_impl,
     "persistent_topk": persistent_topk_impl,
+    "concat_and_cache_mla": concat_and_cache_mla_impl,
 }
 
 _registered = {}

@@ -67,6 +67,30 @@ int mi355_dsa_indexer_k_store(void* kv_cache, int kv_fp8, int64_t n_rows,
                               const int32_t* slot_mapping, void* stream);
 
 /*
+ * MLA latent cache writer: kv_cache row slot_mapping[t] <- token t for every
+ * t < n_tok with 0 <= slot < n_rows (other slots are skipped on device).
+ *   kv_c: [n_tok, >= 512] 16-bit rows (row stride kv_c_stride elements),
+ *   k_pe: [n_tok, >= 64] 16-bit rows (row stride k_pe_stride elements),
+ *         in_bf16 = 1: bf16 inputs, else fp16; rows 16-byte aligned.
+ *   kv_fp8 == 0 ("auto"): kv_cache rows of 576 fp16 = [kv_c | k_pe]
+ *                (fp16 inputs only).
+ *   kv_fp8 == 1 ("fp8_ds_mla"): kv_cache rows of 656 bytes = 512 e4m3 with
+ *                one scale per 128-dim tile, scale = max(amax/448, FLT_MIN),
+ *                e4m3 = RNE-satfinite(kv_c/scale); then the 4 fp32 scales;
+ *                then k_pe's 64 16-bit values unchanged.
+ *   slot_mapping: int64 (slot_i64 = 1) or int32 [n_tok].
+ * Replaces vLLM's concat_and_cache_mla for kv_cache_dtype "auto" and
+ * "fp8_ds_mla" (concat_and_cache_ds_mla_kernel; the reference carries only
+ * its amax fix, patches/glm5-v100-sm70-glue.patch:517-531).
+ */
+int mi355_dsa_concat_and_cache_mla(void* kv_cache, int kv_fp8, int64_t n_rows,
+                                   const void* kv_c, int64_t kv_c_stride,
+                                   const void* k_pe, int64_t k_pe_stride,
+                                   int in_bf16, int64_t n_tok,
+                                   const void* slot_mapping, int slot_i64,
+                                   void* stream);
+
+/*
  * Indexer logits (decode and generic path):
  *   score[b,p] = sum_h relu(q[b,h,:] . K[row(b,p),:]) * w[b,h]   (p < seq_len[b])
  *   score[b,p] = -inf                                          (seq_len[b] <= p < max_kv)

@@ -320,6 +320,38 @@ def dsmla_rows(latent: torch.Tensor, per_tile: bool = False) -> torch.Tensor:
     return torch.cat([qb, sb, rb], dim=1).contiguous()
 
 
+def concat_and_cache_mla(kv_cache: torch.Tensor, kv_c: torch.Tensor, k_pe: torch.Tensor,
+                         slot: torch.Tensor, kv_cache_dtype: str) -> torch.Tensor:
+    """Returns a copy of the latent cache with token t written to row
+    slot[t] (slots < 0 or >= n_rows skipped), following vLLM's
+    concat_and_cache_mla:
+      * "auto": row = [kv_c | k_pe] in fp16 (576 halves);
+      * "fp8_ds_mla": row = 512 e4m3 bytes with one scale per 128-dim tile,
+        scale = max(amax/448, FLT_MIN) (amax of |kv_c| over the tile as the
+        reference's fixed hunk computes it, patches/glm5-v100-sm70-glue.patch:
+        517-531), e4m3 = RNE-satfinite(v/scale); then the 4 fp32 scales; then
+        k_pe's 16-bit values unchanged (fp16 or bf16 bits)."""
+    out = kv_cache.clone()
+    T = slot.shape[0]
+    s = slot.to(torch.int64)
+    if kv_cache_dtype == "auto":
+        flat = out.view(-1, 576)
+        rows = torch.cat([kv_c[:T].to(torch.float16), k_pe[:T].to(torch.float16)], dim=1)
+    else:
+        flat = out.view(-1, DSMLA_ROW_BYTES)
+        x = kv_c[:T].to(torch.float32).reshape(T, 4, 128)
+        amax = torch.nan_to_num(x.abs(), nan=0.0).amax(dim=2, keepdim=True)
+        scale = torch.clamp(amax / 448.0, min=FLT_MIN)
+        qb = e4m3_encode(x / scale).reshape(T, 512)
+        sb = scale.reshape(T, 4).contiguous().view(torch.uint8).reshape(T, 16)
+        rb = k_pe[:T].contiguous().view(torch.uint8).reshape(T, 128)
+        rows = torch.cat([qb, sb, rb], dim=1)
+    n_rows = flat.shape[0]
+    ok = (s >= 0) & (s < n_rows)
+    flat[s[ok]] = rows[ok]
+    return out
+
+
 # ---------------------------------------------------------------------------
 # fp8 weight-only projections (glue.patch:1515-1532; sm70_attn_fp8.cu)
 # ---------------------------------------------------------------------------

@@ -22,7 +22,7 @@ def test_header_declares_the_op_surface():
     names = declared_functions()
     for op in ["indexer_k_store", "indexer_logits", "indexer_logits_packed", "decode_topk",
                "persistent_topk", "sparse_mla_decode", "attn_fp8_gemv", "attn_fp8_dequant",
-               "selfcheck", "last_error"]:
+               "selfcheck", "last_error", "concat_and_cache_mla"]:
         assert f"mi355_dsa_{op}" in names
 
 
@@ -93,3 +93,10 @@ def test_sparse_rejects_small_workspace(pkg, lib):
     rc = lib.mi355_dsa_sparse_mla_decode(16, 16, 16, 4, 64, 16, 0, 100, 64, 16, 2048,
                                          16, 4, 16, 0.1, 16, 10, None)
     assert rc == 1 and "workspace too small" in _err(pkg)
+
+
+def test_cache_writer_rejects_misaligned_rows(pkg, lib):
+    rc = lib.mi355_dsa_concat_and_cache_mla(16, 1, 64, 16, 500, 16, 64, 0, 1, 16, 1, None)
+    assert rc == 1 and "row strides" in _err(pkg)
+    rc = lib.mi355_dsa_concat_and_cache_mla(16, 0, 64, 16, 512, 16, 64, 1, 1, 16, 1, None)
+    assert rc == 1 and "fp16 inputs" in _err(pkg)
