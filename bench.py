@@ -14,7 +14,9 @@ GB/s); indexer prefill TFLOPS @64k"):
 * extra records: indexer prefill logits TFLOPS over a 64k-token causal
   prefill (the caller's 128-row sub-chunks, causal-triangle FLOPs only), a
   context-flatness sweep of the decode, the roofline of the decode kernel
-  and the CPU baseline (the oracle's PyTorch restatement on the host cores).
+  and the CPU baseline (the oracle's PyTorch restatement on the host cores),
+  and one whole DSA decode layer step (cache writes, indexer, top-k, the two
+  head projections and the attention) at the same shape.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L]
 Only one GPU is supported: --gpus N with N > 1 exits with a message.
@@ -172,7 +174,8 @@ def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
 
 
 SPARSE_PREFILL_T = 65536
-EXTRAS = ("sweep", "indexer_prefill", "sparse_prefill", "indexer_decode", "gemv", "k_store")
+EXTRAS = ("sweep", "indexer_prefill", "sparse_prefill", "indexer_decode", "gemv", "k_store",
+          "dsa_layer")
 
 
 def sparse_prefill_flops(T=SPARSE_PREFILL_T, topk=2048, heads=64):
@@ -352,6 +355,76 @@ def bench_k_store(torch, pkg, dev, n_tok=65536, copies=8):
     return out
 
 
+def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128):
+    """One whole DSA decode layer step at the C3 shape (B=4 tokens at ctx,
+    64 heads, top-2048): the step's cache writes (latent + indexer-K), the
+    indexer logits with the fused histogram over the full context, decode
+    top-k, the q_nope -> latent bmm, sparse MLA decode + merge and the W_UV
+    bmm.  `copies` layers with their own caches and weights (> 256 MB MALL)
+    are captured in one graph.  Also reports the indexer + top-k and the
+    attention parts alone, from graphs of their own."""
+    m = pkg.dsa_layer
+    B, H, page = 4, 64, 64
+    layers, steps = [], []
+    for i in range(copies):
+        d = pkg.synthetic.decode_inputs(B=B, H=H, ctx=ctx, device=dev, seed=60 + i)
+        ix = pkg.synthetic.indexer_decode_inputs(B=B, ctx=ctx, dup_frac=0.0, device=dev,
+                                                 seed=70 + i)
+        g = torch.Generator(device=dev)
+        g.manual_seed(80 + i)
+        w = m.DsaLayerWeights(
+            (torch.randn(H, P, 512, generator=g, device=dev) / P ** 0.5).to(torch.float16),
+            (torch.randn(H, 512, V, generator=g, device=dev) / 512 ** 0.5).to(torch.float16),
+            (P + 64) ** -0.5)
+        # both caches share the latent cache's block table
+        layer = m.DsaLayer(w, d["kv"], ix["kc"])
+        bt, seq = d["bt"], d["seq"]
+        pos = (seq.long() - 1)
+        slot = bt.long().gather(1, (pos // page).view(B, 1)).view(B) * page + pos % page
+        steps.append(dict(
+            layer=layer, bt=bt, seq=seq, slot=slot,
+            q=(torch.randn(B, H, P + 64, generator=g, device=dev) / 8).to(torch.float16),
+            idx_q=ix["q"], idx_w=ix["w"],
+            kv_c=(torch.randn(B, 512, generator=g, device=dev) / 24).to(torch.float16),
+            k_pe=(torch.randn(B, 64, generator=g, device=dev) / 24).to(torch.float16),
+            idx_k=torch.randn(B, 128, generator=g, device=dev).to(torch.float16)))
+        del d, ix
+
+    def full():
+        for s in steps:
+            s["layer"].decode(s["q"], s["idx_q"], s["idx_w"], s["bt"], s["seq"],
+                              s["kv_c"], s["k_pe"], s["idx_k"], s["slot"])
+
+    def topk_only():
+        for s in steps:
+            s["layer"].decode_topk(s["idx_q"], s["idx_w"], s["bt"], s["seq"])
+
+    def attn_only():
+        ops = pkg._sm70_ops
+        for s in steps:
+            L = s["layer"]
+            ql = m.q_latent(s["q"], L.w)
+            o = torch.empty(B, H, 512, dtype=torch.float16, device=dev)
+            lse = torch.empty(B, H, device=dev)
+            ops.sm70_sparse_mla_decode(o, lse, ql, L.latent_cache, L.last_idx, s["bt"],
+                                       s["seq"], L.w.scale)
+            m.v_up(o, L.w)
+
+    us = graph_time_per_call(torch, full, copies)
+    us_topk = graph_time_per_call(torch, topk_only, copies)
+    us_attn = graph_time_per_call(torch, attn_only, copies)
+    del steps
+    return {
+        "us_per_layer": round(us, 2),
+        "indexer_topk_us": round(us_topk, 2),
+        "attention_us": round(us_attn, 2),
+        "workload": (f"one DSA decode layer: B=4 tokens at {ctx} ctx, 64 heads (q_nope {P}, "
+                     f"v {V}), cache writes + indexer 32x128 fp16 K over the full context + "
+                     "top-2048 + q_latent bmm + sparse MLA (fp8_ds_mla) + W_UV bmm; "
+                     f"{copies} layers per graph"),
+    }
+
+
 def cpu_baseline(torch, d, idxs, qs, budget_s):
     """The oracle's PyTorch restatement (fp32) of the same decode layers on
     the host cores: gather -> dequant -> QK -> softmax -> PV."""
@@ -499,6 +572,10 @@ def main():
     if "k_store" in extras:
         line["k_store"] = bench_k_store(torch, pkg, dev)
         log(f"k store: {line['k_store']}")
+        torch.cuda.empty_cache()
+    if "dsa_layer" in extras:
+        line["dsa_layer_decode"] = bench_dsa_layer(torch, pkg, dev)
+        log(f"dsa layer decode: {line['dsa_layer_decode']}")
         torch.cuda.empty_cache()
 
     if not args.no_cpu:

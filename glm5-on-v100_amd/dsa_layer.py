@@ -1,0 +1,203 @@
+"""One DSA attention layer step on top of the hot-path ops: the caller side
+of the kernels, as the reference's model runner drives them.
+
+Decode (reference/sparse_attn_indexer.py:528-639 with the fused decode top-k,
+then reference/triton_mla.py:212-301 _forward_mqa_sparse and the layer's
+v_up projection):
+  1. write the step's tokens into the latent cache (concat_and_cache_mla)
+     and the indexer-K cache (sm70_indexer_k_store);
+  2. indexer logits with the level-1 histogram, then sm70_decode_topk;
+  3. q_nope -> latent through W_UK_T (bmm over heads), concatenated with q_pe;
+  4. sparse MLA attention over the top-k rows;
+  5. o -> values through W_UV (bmm over heads).
+Speculative decode rows (B tokens over B / next_n requests) are expanded per
+token as the reference does (triton_mla.py:267-279).
+
+Prefill (sparse_attn_indexer.py:641-881 without tensor-parallel key
+sharding, then triton_mla.py:380-492 _forward_mha_sparse): per request and
+per `sub_rows`-row sub-chunk, the packed indexer logits over the causal reach
+of the sub-chunk (rounded up to the 64-key tile) and persistent_topk with the
+per-token causal lengths; then the attention with per-token causal lengths and
+per-token block-table rows, and the W_UV projection.  `sub_rows` defaults to
+the reference's 128; the score buffer is sub_rows x reach fp32, so 1024-row
+sub-chunks (256 MB at 64k reach) are affordable on a 288 GB part.
+
+All buffers come from torch's caching allocator; nothing here synchronises
+the host except the per-sub-chunk causal reach, which the reference also reads
+on the host (memoized per chunk, :774-789) and which callers can pass in.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _cache_ops, _sm70_ops
+
+KT = 64  # key tile the prefill logits launch is rounded to (sparse_attn_indexer.py:753)
+
+
+@dataclass
+class DsaLayerWeights:
+    """W_UK_T [H, P, 512] and W_UV [H, 512, V] fp16 (built from kv_b_proj as
+    triton_mla.py:388-412 does), softmax scale of the 576-dim latent q."""
+    W_UK_T: torch.Tensor
+    W_UV: torch.Tensor
+    scale: float
+
+    @property
+    def n_heads(self) -> int:
+        return self.W_UK_T.shape[0]
+
+    @property
+    def nope_dim(self) -> int:
+        return self.W_UK_T.shape[1]
+
+    @property
+    def v_dim(self) -> int:
+        return self.W_UV.shape[2]
+
+
+def q_latent(q: torch.Tensor, w: DsaLayerWeights) -> torch.Tensor:
+    """q [T, H, P + 64] -> [T, H, 576] fp16: bmm(q_nope, W_UK_T) | q_pe
+    (triton_mla.py:413-418)."""
+    P = w.nope_dim
+    q_nope = q[..., :P].transpose(0, 1).contiguous()        # [H, T, P]
+    ql = torch.bmm(q_nope, w.W_UK_T).transpose(0, 1)         # [T, H, 512]
+    return torch.cat([ql, q[..., P:]], dim=-1).to(torch.float16).contiguous()
+
+
+def v_up(o: torch.Tensor, w: DsaLayerWeights) -> torch.Tensor:
+    """o [T, H, 512] -> [T, H * V]: bmm over heads with W_UV
+    (triton_mla.py:486-492)."""
+    T, H, _ = o.shape
+    ov = torch.bmm(o.transpose(0, 1).contiguous(), w.W_UV)   # [H, T, V]
+    return ov.transpose(0, 1).reshape(T, H * w.v_dim)
+
+
+class DsaLayer:
+    """One layer's caches and weights; decode() / prefill() run a step."""
+
+    def __init__(self, weights: DsaLayerWeights, latent_cache: torch.Tensor,
+                 idx_k_cache: torch.Tensor, topk: int = 2048):
+        self.w = weights
+        self.latent_cache = latent_cache   # [n_blocks, page, 656] u8 or [.., 576] fp16
+        self.idx_k_cache = idx_k_cache     # [n_blocks, page, 128] fp16 or [.., 132] u8
+        self.topk = topk
+        self.kv_dtype = "fp8_ds_mla" if latent_cache.dtype == torch.uint8 else "auto"
+
+    # -- cache writes -------------------------------------------------------
+    def store(self, kv_c: torch.Tensor, k_pe: torch.Tensor, idx_k: torch.Tensor,
+              slot_mapping: torch.Tensor) -> None:
+        """Writes the step's tokens into both paged caches (slot < 0 skipped)."""
+        _cache_ops.concat_and_cache_mla(kv_c, k_pe, self.latent_cache, slot_mapping,
+                                        self.kv_dtype, torch.ones((), device=kv_c.device))
+        _sm70_ops.sm70_indexer_k_store(self.idx_k_cache, idx_k.to(torch.float16).contiguous(),
+                                       slot_mapping.to(torch.int32))
+
+    # -- decode -------------------------------------------------------------
+    def decode_topk(self, idx_q: torch.Tensor, idx_w: torch.Tensor,
+                    block_table: torch.Tensor, seq_lens: torch.Tensor) -> torch.Tensor:
+        """Indexer logits + fused histogram + decode top-k: idx [B, topk]."""
+        B = idx_q.shape[0]
+        page = self.idx_k_cache.shape[1]
+        max_kv = block_table.shape[1] * page
+        score = torch.empty(B, max_kv, dtype=torch.float32, device=idx_q.device)
+        hist = torch.zeros(B, 4096, dtype=torch.int32, device=idx_q.device)
+        idx = torch.empty(B, self.topk, dtype=torch.int32, device=idx_q.device)
+        _sm70_ops.sm70_indexer_logits(score, idx_q.contiguous(), self.idx_k_cache,
+                                      idx_w.contiguous(), block_table, seq_lens, hist)
+        _sm70_ops.sm70_decode_topk(idx, score, seq_lens, hist, self.topk)
+        return idx
+
+    def decode(self, q: torch.Tensor, idx_q: torch.Tensor, idx_w: torch.Tensor,
+               block_table: torch.Tensor, seq_lens: torch.Tensor,
+               kv_c: torch.Tensor | None = None, k_pe: torch.Tensor | None = None,
+               idx_k: torch.Tensor | None = None,
+               slot_mapping: torch.Tensor | None = None) -> torch.Tensor:
+        """q [B, H, P + 64], idx_q [B, 32, 128], idx_w [B, 32]; block_table
+        [R, max_blocks] and seq_lens [R] per request (R = B / next_n, seq_lens
+        counting the step's tokens).  With kv_c / k_pe / idx_k / slot_mapping
+        the step's tokens are first written to the caches.  Returns
+        out [B, H * V]."""
+        if kv_c is not None:
+            self.store(kv_c, k_pe, idx_k, slot_mapping)
+        B, R = q.shape[0], seq_lens.shape[0]
+        bt = block_table.to(torch.int32)
+        sl = seq_lens.to(torch.int32)
+        if B != R:  # spec-as-decode: per-token rows (triton_mla.py:267-279)
+            assert B % R == 0, f"non-uniform decode batch: {B} tokens, {R} requests"
+            n = B // R
+            offs = torch.arange(n, device=q.device, dtype=torch.int32)
+            sl = (sl.unsqueeze(1) - (n - 1) + offs).reshape(-1).contiguous()
+            bt = bt.repeat_interleave(n, dim=0).contiguous()
+        idx = self.decode_topk(idx_q, idx_w, bt, sl)
+        ql = q_latent(q, self.w)
+        o = torch.empty(B, self.w.n_heads, 512, dtype=torch.float16, device=q.device)
+        lse = torch.empty(B, self.w.n_heads, dtype=torch.float32, device=q.device)
+        _sm70_ops.sm70_sparse_mla_decode(o, lse, ql, self.latent_cache, idx, bt, sl,
+                                         self.w.scale)
+        self.last_idx, self.last_o, self.last_lse = idx, o, lse
+        return v_up(o, self.w)
+
+    # -- prefill ------------------------------------------------------------
+    def prefill_topk(self, idx_q: torch.Tensor, idx_w: torch.Tensor, bounds: list[int],
+                     block_table: torch.Tensor, causal_len: torch.Tensor,
+                     sub_rows: int = 128, reach: list[int] | None = None) -> torch.Tensor:
+        """Top-k rows of the prefill tokens: request r owns token rows
+        [bounds[r], bounds[r+1]) and block-table row r; causal_len[t] is
+        token t's context length (its position + 1).  `reach` optionally gives
+        each sub-chunk's max causal length (else read from causal_len)."""
+        T = idx_q.shape[0]
+        page = self.idx_k_cache.shape[1]
+        full_kv = block_table.shape[1] * page
+        out = torch.full((T, self.topk), -1, dtype=torch.int32, device=idx_q.device)
+        ws = torch.empty(1 << 20, dtype=torch.uint8, device=idx_q.device)
+        max_len = int(causal_len.max()) if reach is None else max(reach)
+        k = 0
+        for r in range(len(bounds) - 1):
+            lo, hi = bounds[r], bounds[r + 1]
+            for lo2 in range(lo, hi, sub_rows):
+                hi2 = min(lo2 + sub_rows, hi)
+                n = hi2 - lo2
+                cl = causal_len[lo2:hi2].to(torch.int32).contiguous()
+                cmax = int(cl.max()) if reach is None else reach[k]
+                k += 1
+                max_kv = max(min(full_kv, (cmax + KT - 1) // KT * KT), page)
+                cols = min(block_table.shape[1], (max_kv + page - 1) // page)
+                seg_bt = block_table[r:r + 1, :cols].to(torch.int32).expand(n, cols).contiguous()
+                score = torch.empty(n, max_kv, dtype=torch.float32, device=idx_q.device)
+                qs = idx_q[lo2:hi2]
+                n16 = (n + 15) // 16 * 16
+                if n16 != n:
+                    qs = torch.nn.functional.pad(qs, (0, 0, 0, 0, 0, n16 - n))
+                qp = qs.reshape(n16 // 16, 16, 32, 8, 16).permute(2, 0, 3, 1, 4).contiguous()
+                _sm70_ops.sm70_indexer_logits_packed(score, qp, self.idx_k_cache,
+                                                     idx_w[lo2:hi2].contiguous(), seg_bt, cl)
+                _sm70_ops.persistent_topk(score, cl.view(n, 1), out[lo2:hi2], ws, self.topk,
+                                          max_len)
+        return out
+
+    def prefill(self, q: torch.Tensor, idx_q: torch.Tensor, idx_w: torch.Tensor,
+                bounds: list[int], block_table: torch.Tensor, causal_len: torch.Tensor,
+                kv_c: torch.Tensor | None = None, k_pe: torch.Tensor | None = None,
+                idx_k: torch.Tensor | None = None, slot_mapping: torch.Tensor | None = None,
+                sub_rows: int = 128, reach: list[int] | None = None) -> torch.Tensor:
+        """Prefill tokens q [T, H, P + 64] (see prefill_topk for the
+        metadata).  Returns out [T, H * V]."""
+        if kv_c is not None:
+            self.store(kv_c, k_pe, idx_k, slot_mapping)
+        T = q.shape[0]
+        idx = self.prefill_topk(idx_q, idx_w, bounds, block_table, causal_len, sub_rows, reach)
+        req = torch.repeat_interleave(
+            torch.arange(len(bounds) - 1, device=q.device),
+            torch.tensor([bounds[r + 1] - bounds[r] for r in range(len(bounds) - 1)],
+                         device=q.device))
+        per_tok_bt = block_table.to(torch.int32).index_select(0, req).contiguous()
+        ql = q_latent(q, self.w)
+        o = torch.empty(T, self.w.n_heads, 512, dtype=torch.float16, device=q.device)
+        lse = torch.empty(T, self.w.n_heads, dtype=torch.float32, device=q.device)
+        _sm70_ops.sm70_sparse_mla_decode(o, lse, ql, self.latent_cache, idx, per_tok_bt,
+                                         causal_len.to(torch.int32).contiguous(), self.w.scale)
+        self.last_idx, self.last_o, self.last_lse = idx, o, lse
+        return v_up(o, self.w)

@@ -390,13 +390,19 @@ IMPLS = {
 _registered = {}
 
 
-def register(namespace: str | None = None) -> str:
-    """Registers every op (idempotent per namespace); returns the namespace."""
+CACHE_OPS = ("concat_and_cache_mla",)
+
+
+def register(namespace: str | None = None, names=None) -> str:
+    """Registers the ops `names` (default: every op) in `namespace`
+    (idempotent per namespace); returns the namespace."""
     ns = namespace or NAMESPACE
     if ns in _registered:
         return ns
     lib = torch.library.Library(ns, "FRAGMENT")
     for name, schema in SCHEMAS.items():
+        if names is not None and name not in names:
+            continue
         if hasattr(getattr(torch.ops, ns), name):
             continue  # defined elsewhere (e.g. a real vLLM _C build)
         lib.define(schema)
@@ -408,6 +414,12 @@ def register(namespace: str | None = None) -> str:
         torch.library.register_fake(f"{ns}::{name}", _fake, lib=lib)
     _registered[ns] = lib
     return ns
+
+
+def register_cache_ops(namespace: str = "_C_cache_ops") -> str:
+    """Registers the latent-cache writer alone in the namespace vLLM's
+    _custom_ops.concat_and_cache_mla resolves (torch.ops._C_cache_ops)."""
+    return register(namespace, CACHE_OPS)
 
 
 def op(name: str):

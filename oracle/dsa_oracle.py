@@ -387,3 +387,73 @@ def attn_fp8_gemv(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor) -> torch.Te
     n, k = w.shape
     deq = e4m3_decode(w).double() * expand_block_scale(s, n, k).double()
     return x.double() @ deq.T
+
+
+# ---------------------------------------------------------------------------
+# one DSA layer step: the reference's callers of the ops
+# (sparse_attn_indexer.py:528-881, triton_mla.py:212-301 and :365-492)
+# ---------------------------------------------------------------------------
+def q_latent(q: torch.Tensor, W_UK_T: torch.Tensor) -> torch.Tensor:
+    """[T, H, P + 64] -> [T, H, 576] fp16: q_nope @ W_UK_T per head in fp64,
+    rounded to fp16, then q_pe (triton_mla.py:413-418)."""
+    P = W_UK_T.shape[1]
+    ql = torch.einsum("thp,hpl->thl", q[..., :P].double(), W_UK_T.double())
+    return torch.cat([ql, q[..., P:].double()], dim=-1).to(torch.float16)
+
+
+def v_up(o: torch.Tensor, W_UV: torch.Tensor) -> torch.Tensor:
+    """o [T, H, 512] (the kernel's fp16 output) @ W_UV per head, fp64
+    (triton_mla.py:486-492): [T, H * V]."""
+    T, H, _ = o.shape
+    return torch.einsum("thl,hlv->thv", o.to(torch.float16).double(),
+                        W_UV.double()).reshape(T, -1)
+
+
+def dsa_layer_decode(q, idx_q, idx_w, block_table, seq_lens, latent_cache, idx_k_cache,
+                     W_UK_T, W_UV, scale, topk=2048):
+    """Decode step with per-token rows already expanded (block_table and
+    seq_lens [B]): indexer logits -> top-k -> sparse attention -> v_up.
+    Returns (out, idx, o, lse)."""
+    page = idx_k_cache.shape[1]
+    max_kv = block_table.shape[1] * page
+    score, _ = indexer_logits(idx_q, idx_k_cache, idx_w, block_table, seq_lens, max_kv)
+    idx = topk_rows(score, seq_lens, topk)
+    o, lse = sparse_mla(q_latent(q, W_UK_T), latent_cache, idx, block_table, seq_lens, scale)
+    return v_up(o, W_UV), idx, o, lse
+
+
+def dsa_layer_prefill_topk(idx_q, idx_w, bounds, block_table, causal_len, idx_k_cache,
+                           topk=2048, kt=64):
+    """Prefill top-k rows: per request r (token rows [bounds[r], bounds[r+1])),
+    scores over the request's block-table row up to each token's causal
+    length; the reference's sub-chunking and the 64-key launch rounding do
+    not change the selected sets (sparse_attn_indexer.py:760-881)."""
+    T = idx_q.shape[0]
+    page = idx_k_cache.shape[1]
+    out = torch.full((T, topk), -1, dtype=torch.int32)
+    for r in range(len(bounds) - 1):
+        lo, hi = bounds[r], bounds[r + 1]
+        if hi <= lo:
+            continue
+        cl = causal_len[lo:hi].to(torch.int32)
+        max_kv = max(min(block_table.shape[1] * page,
+                         (int(cl.max()) + kt - 1) // kt * kt), page)
+        bt = block_table[r:r + 1].expand(hi - lo, -1)
+        score, _ = indexer_logits(idx_q[lo:hi], idx_k_cache, idx_w[lo:hi], bt, cl, max_kv)
+        out[lo:hi] = topk_rows(score, cl, topk)
+    return out
+
+
+def dsa_layer_prefill(q, idx_q, idx_w, bounds, block_table, causal_len, latent_cache,
+                      idx_k_cache, W_UK_T, W_UV, scale, topk=2048):
+    """Prefill step: top-k per token, attention with per-token causal lengths
+    and per-token block-table rows, v_up.  Returns (out, idx, o, lse)."""
+    idx = dsa_layer_prefill_topk(idx_q, idx_w, bounds, block_table, causal_len, idx_k_cache,
+                                 topk)
+    req = torch.repeat_interleave(torch.arange(len(bounds) - 1),
+                                  torch.tensor([bounds[r + 1] - bounds[r]
+                                                for r in range(len(bounds) - 1)]))
+    bt = block_table.index_select(0, req)
+    o, lse = sparse_mla(q_latent(q, W_UK_T), latent_cache, idx, bt,
+                        causal_len.to(torch.int32), scale)
+    return v_up(o, W_UV), idx, o, lse

@@ -44,3 +44,20 @@ def test_cpu_tensors_are_refused(pkg, lib):
 def test_missing_op_raises_like_reference(pkg):
     with pytest.raises(RuntimeError, match="not available"):
         pkg._sm70_ops._op("sm70_no_such_op")
+
+
+def test_cache_writer_in_vllm_namespace(pkg, lib):
+    """register_cache_ops puts only the latent-cache writer in the namespace
+    vLLM's _custom_ops.concat_and_cache_mla resolves."""
+    ns = pkg.ops.register_cache_ops("_mi355_test_cache_ops")
+    space = getattr(torch.ops, ns)
+    got = str(space.concat_and_cache_mla.default._schema)
+    want = str(torch._C.parse_schema(f"{ns}::{pkg.ops.SCHEMAS['concat_and_cache_mla']}"))
+    assert got == want
+    assert not hasattr(space, "sm70_sparse_mla_decode")
+    kv = torch.empty(4, 512, dtype=torch.float16)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        space.concat_and_cache_mla(kv, torch.empty(4, 64, dtype=torch.float16),
+                                   torch.empty(1, 64, 656, dtype=torch.uint8),
+                                   torch.zeros(4, dtype=torch.int64), "fp8_ds_mla",
+                                   torch.ones(()))
