@@ -361,8 +361,9 @@ def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128):
     indexer logits with the fused histogram over the full context, decode
     top-k, the q_nope -> latent bmm, sparse MLA decode + merge and the W_UV
     bmm.  `copies` layers with their own caches and weights (> 256 MB MALL)
-    are captured in one graph.  Also reports the indexer + top-k and the
-    attention parts alone, from graphs of their own."""
+    are captured in one graph.  Also reports the indexer + top-k, the
+    attention (with both projections) and the two projections alone, from
+    graphs of their own."""
     m = pkg.dsa_layer
     B, H, page = 4, 64, 64
     layers, steps = [], []
@@ -410,14 +411,25 @@ def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128):
                                        s["seq"], L.w.scale)
             m.v_up(o, L.w)
 
+    def proj_only():
+        for s in steps:
+            L = s["layer"]
+            m.q_latent(s["q"], L.w)
+            m.v_up(L.last_o, L.w)
+
     us = graph_time_per_call(torch, full, copies)
     us_topk = graph_time_per_call(torch, topk_only, copies)
     us_attn = graph_time_per_call(torch, attn_only, copies)
+    us_proj = graph_time_per_call(torch, proj_only, copies)
+    # weight bytes of the two projections (each read once per call)
+    proj_bytes = 2 * H * 512 * (P + V)
     del steps
     return {
         "us_per_layer": round(us, 2),
         "indexer_topk_us": round(us_topk, 2),
         "attention_us": round(us_attn, 2),
+        "projections_us": round(us_proj, 2),
+        "projections_gbps": round(proj_bytes / (us_proj * 1e-6) / 1e9, 1),
         "workload": (f"one DSA decode layer: B=4 tokens at {ctx} ctx, 64 heads (q_nope {P}, "
                      f"v {V}), cache writes + indexer 32x128 fp16 K over the full context + "
                      "top-2048 + q_latent bmm + sparse MLA (fp8_ds_mla) + W_UV bmm; "

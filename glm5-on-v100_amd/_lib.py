@@ -27,6 +27,8 @@ SIGNATURES = {
     "mi355_dsa_abi_version": (_c_int, []),
     "mi355_dsa_selfcheck": (_c_int, [_p]),
     "mi355_dsa_indexer_k_store": (_c_int, [_p, _c_int, _c_i64, _p, _c_i64, _c_int, _p, _p]),
+    "mi355_dsa_head_proj": (_c_int, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _c_int, _c_int,
+                                     _c_int, _c_int, _c_int, _p]),
     "mi355_dsa_concat_and_cache_mla": (_c_int, [_p, _c_int, _c_i64, _p, _c_i64, _p, _c_i64,
                                                 _c_int, _c_i64, _p, _c_int, _p]),
     "mi355_dsa_indexer_logits": (_c_int, [_p, _c_int, _c_int, _p, _c_int, _c_int, _p, _c_int,

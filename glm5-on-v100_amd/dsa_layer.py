@@ -10,6 +10,8 @@ v_up projection):
   3. q_nope -> latent through W_UK_T (bmm over heads), concatenated with q_pe;
   4. sparse MLA attention over the top-k rows;
   5. o -> values through W_UV (bmm over heads).
+Steps 3 and 5 run the per-head projection kernel (mi355_dsa_head_proj): one
+launch each instead of the reference's transposes, bmm and concatenation.
 Speculative decode rows (B tokens over B / next_n requests) are expanded per
 token as the reference does (triton_mla.py:267-279).
 
@@ -32,7 +34,8 @@ from dataclasses import dataclass
 
 import torch
 
-from . import _cache_ops, _sm70_ops
+from . import _cache_ops, _lib, _sm70_ops
+from .ops import _check, _stream
 
 KT = 64  # key tile the prefill logits launch is rounded to (sparse_attn_indexer.py:753)
 
@@ -40,10 +43,23 @@ KT = 64  # key tile the prefill logits launch is rounded to (sparse_attn_indexer
 @dataclass
 class DsaLayerWeights:
     """W_UK_T [H, P, 512] and W_UV [H, 512, V] fp16 (built from kv_b_proj as
-    triton_mla.py:388-412 does), softmax scale of the 576-dim latent q."""
+    triton_mla.py:388-412 does), softmax scale of the 576-dim latent q.
+    The projection kernel reads each head's weight transposed (k
+    contiguous); those copies are made once here, as the reference makes
+    W_UK_T once after loading."""
     W_UK_T: torch.Tensor
     W_UV: torch.Tensor
     scale: float
+
+    def __post_init__(self):
+        _check(self.W_UK_T.dtype == torch.float16 and self.W_UV.dtype == torch.float16,
+               "W_UK_T and W_UV must be fp16")
+        _check(self.W_UK_T.dim() == 3 and self.W_UK_T.shape[2] == 512
+               and self.W_UV.dim() == 3 and self.W_UV.shape[1] == 512
+               and self.W_UV.shape[0] == self.W_UK_T.shape[0],
+               "W_UK_T must be [H, P, 512] and W_UV [H, 512, V]")
+        self.uk_t = self.W_UK_T.transpose(1, 2).contiguous()   # [H, 512, P]
+        self.uv_t = self.W_UV.transpose(1, 2).contiguous()     # [H, V, 512]
 
     @property
     def n_heads(self) -> int:
@@ -58,21 +74,47 @@ class DsaLayerWeights:
         return self.W_UV.shape[2]
 
 
+def _rows8(x: torch.Tensor) -> torch.Tensor:
+    """x with unit last stride, 16-byte aligned, token / head strides that
+    are multiples of 8 elements (what the kernel loads 16 B at a time)."""
+    ok = (x.stride(2) == 1 and x.stride(1) % 8 == 0 and x.stride(0) % 8 == 0
+          and x.data_ptr() % 16 == 0)
+    return x if ok else x.contiguous()
+
+
+def head_proj(out: torch.Tensor, x: torch.Tensor, wt: torch.Tensor, tail: int) -> None:
+    """out[t, h, :N] = x[t, h, :K] @ wt[h].T, out[t, h, N:N+tail] = x[t, h, K:K+tail];
+    x [T, H, >= K + tail], wt [H, N, K], out [T, H, >= N + tail] (fp16)."""
+    _check(x.is_cuda and wt.is_cuda and out.is_cuda, "all tensors must be on the GPU")
+    _check(x.dtype == torch.float16 and wt.dtype == torch.float16 and out.dtype == torch.float16,
+           "head_proj: fp16 tensors expected")
+    _check(wt.is_contiguous() and out.stride(2) == 1, "head_proj: wt contiguous, out rows dense")
+    H, N, K = wt.shape
+    T = x.shape[0]
+    _check(x.shape[1] == H and out.shape[:2] == (T, H), "head_proj: token / head shapes differ")
+    with torch.cuda.device(x.device):
+        _lib.call("mi355_dsa_head_proj", out.data_ptr(), out.stride(0), out.stride(1),
+                  x.data_ptr(), x.stride(0), x.stride(1), wt.data_ptr(), T, H, N, K, tail,
+                  _stream(x))
+
+
 def q_latent(q: torch.Tensor, w: DsaLayerWeights) -> torch.Tensor:
     """q [T, H, P + 64] -> [T, H, 576] fp16: bmm(q_nope, W_UK_T) | q_pe
-    (triton_mla.py:413-418)."""
-    P = w.nope_dim
-    q_nope = q[..., :P].transpose(0, 1).contiguous()        # [H, T, P]
-    ql = torch.bmm(q_nope, w.W_UK_T).transpose(0, 1)         # [T, H, 512]
-    return torch.cat([ql, q[..., P:]], dim=-1).to(torch.float16).contiguous()
+    (triton_mla.py:413-418), one launch."""
+    _check(q.dim() == 3 and q.shape[2] == w.nope_dim + 64, "q must be [T, H, P + 64]")
+    q = _rows8(q)
+    out = torch.empty(q.shape[0], q.shape[1], 576, dtype=torch.float16, device=q.device)
+    head_proj(out, q, w.uk_t, 64)
+    return out
 
 
 def v_up(o: torch.Tensor, w: DsaLayerWeights) -> torch.Tensor:
     """o [T, H, 512] -> [T, H * V]: bmm over heads with W_UV
-    (triton_mla.py:486-492)."""
+    (triton_mla.py:486-492), one launch."""
     T, H, _ = o.shape
-    ov = torch.bmm(o.transpose(0, 1).contiguous(), w.W_UV)   # [H, T, V]
-    return ov.transpose(0, 1).reshape(T, H * w.v_dim)
+    out = torch.empty(T, H * w.v_dim, dtype=torch.float16, device=o.device)
+    head_proj(out.view(T, H, w.v_dim), _rows8(o), w.uv_t, 0)
+    return out
 
 
 class DsaLayer:

@@ -91,6 +91,27 @@ int mi355_dsa_concat_and_cache_mla(void* kv_cache, int kv_fp8, int64_t n_rows,
                                    void* stream);
 
 /*
+ * Per-head projection of an MLA layer (fp16 in and out, fp32 accumulation):
+ *   out[t,h,n]   = sum_k x[t,h,k] * wt[h,n,k]    (t < T, h < H, n < N, k < K)
+ *   out[t,h,N+i] = x[t,h,K+i]                    (i < tail)
+ * x and out are addressed with element strides (token, head); wt is the
+ * per-head weight transposed, [H, N, K] contiguous.  K must be a multiple of
+ * 32 (of 64 when 256 <= K < 512, of 128 when K >= 512) and at most 1024; N a
+ * multiple of 64 (K < 256), 32 (256 <= K < 512) or 16 (K >= 512); tail a
+ * multiple of 8.  x and wt 16-byte aligned with strides that are multiples of
+ * 8 elements (out too when tail > 0).
+ * Replaces the torch.bmm calls around the attention op with their transposes
+ * and concatenation: q_nope @ W_UK_T concatenated with q_pe
+ * (reference/triton_mla.py:388-418: x = q, K = qk_nope_head_dim, N = 512,
+ * tail = 64, wt = W_UK_T transposed) and o @ W_UV (:486-492: x = o, K = 512,
+ * N = v_head_dim, tail = 0, wt = W_UV transposed).
+ */
+int mi355_dsa_head_proj(void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                        const void* x, int64_t x_tok_stride, int64_t x_head_stride,
+                        const void* wt, int T, int H, int N, int K, int tail,
+                        void* stream);
+
+/*
  * Indexer logits (decode and generic path):
  *   score[b,p] = sum_h relu(q[b,h,:] . K[row(b,p),:]) * w[b,h]   (p < seq_len[b])
  *   score[b,p] = -inf                                          (seq_len[b] <= p < max_kv)

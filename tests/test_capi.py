@@ -22,7 +22,7 @@ def test_header_declares_the_op_surface():
     names = declared_functions()
     for op in ["indexer_k_store", "indexer_logits", "indexer_logits_packed", "decode_topk",
                "persistent_topk", "sparse_mla_decode", "attn_fp8_gemv", "attn_fp8_dequant",
-               "selfcheck", "last_error", "concat_and_cache_mla"]:
+               "selfcheck", "last_error", "concat_and_cache_mla", "head_proj"]:
         assert f"mi355_dsa_{op}" in names
 
 
@@ -100,3 +100,17 @@ def test_cache_writer_rejects_misaligned_rows(pkg, lib):
     assert rc == 1 and "row strides" in _err(pkg)
     rc = lib.mi355_dsa_concat_and_cache_mla(16, 0, 64, 16, 512, 16, 64, 1, 1, 16, 1, None)
     assert rc == 1 and "fp16 inputs" in _err(pkg)
+
+
+def test_head_proj_rejects_bad_shapes(pkg, lib):
+    # K not a multiple of 32
+    rc = lib.mi355_dsa_head_proj(16, 576 * 4, 576, 16, 4 * 192, 192, 16, 4, 4, 512, 100, 64, None)
+    assert rc == 1 and "multiple of 32" in _err(pkg)
+    # N not a multiple of 64 at K = 128
+    rc = lib.mi355_dsa_head_proj(16, 576 * 4, 576, 16, 4 * 192, 192, 16, 4, 4, 480, 128, 64, None)
+    assert rc == 1 and "multiple of 64" in _err(pkg)
+    # x head stride too small for K + tail
+    rc = lib.mi355_dsa_head_proj(16, 576 * 4, 576, 16, 4 * 128, 128, 16, 4, 4, 512, 128, 64, None)
+    assert rc == 1 and "strides too small" in _err(pkg)
+    # T = 0 is a no-op
+    assert lib.mi355_dsa_head_proj(None, 0, 0, None, 0, 0, None, 0, 4, 512, 128, 64, None) == 0
