@@ -491,15 +491,37 @@ __global__ void __launch_bounds__(kTkThreads) topk_select_kernel(
     topk_row_select(sh.u.full, row, L, K, out, hrow);
     return;
   }
+  if (threadIdx.x == 0) sh.u.c.toff[used_tiles] = total_c;
   __syncthreads();
   // ---- gather the candidates into LDS (tile lists are position ordered) ----
-  for (int t = threadIdx.x >> 6; t < used_tiles; t += kTkWaves) {
-    const int n = ws.counts[(int64_t)b * n_tiles + t];
-    const int o = sh.u.c.toff[t];
-    const int64_t s0 = ((int64_t)b * n_tiles + t) * kScanTile;
-    for (int i = threadIdx.x & 63; i < n; i += 64) {
-      sh.u.c.ckey[o + i] = ws.ckey[s0 + i];
-      sh.u.c.cpos[o + i] = ws.cpos[s0 + i];
+  // Flat over the candidate index: candidate i lives in the tile t with
+  // toff[t] <= i < toff[t+1] (binary search in LDS), so every thread's loads
+  // are independent and kGatherU of them are in flight at once.
+  constexpr int kGatherU = 4;
+  for (int i0 = threadIdx.x; i0 < total_c; i0 += kGatherU * kTkThreads) {
+    uint32_t kk[kGatherU];
+    int32_t pp[kGatherU];
+#pragma unroll
+    for (int u = 0; u < kGatherU; u++) {
+      const int i = i0 + u * kTkThreads;
+      if (i < total_c) {
+        int lo = 0, hi = used_tiles;  // invariant: toff[lo] <= i < toff[hi]
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (sh.u.c.toff[mid] <= i) lo = mid; else hi = mid;
+        }
+        const int64_t src = ((int64_t)b * n_tiles + lo) * kScanTile + (i - sh.u.c.toff[lo]);
+        kk[u] = ws.ckey[src];
+        pp[u] = ws.cpos[src];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kGatherU; u++) {
+      const int i = i0 + u * kTkThreads;
+      if (i < total_c) {
+        sh.u.c.ckey[i] = kk[u];
+        sh.u.c.cpos[i] = pp[u];
+      }
     }
   }
   for (int i = threadIdx.x; i < kSelBins; i += kTkThreads) sh.u.c.hist[i] = 0u;

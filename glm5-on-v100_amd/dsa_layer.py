@@ -12,6 +12,10 @@ v_up projection):
   5. o -> values through W_UV (bmm over heads).
 Steps 3 and 5 run the per-head projection kernel (mi355_dsa_head_proj): one
 launch each instead of the reference's transposes, bmm and concatenation.
+Everything runs in order on the caller's stream: a second stream for the
+latent write and step 3 (which do not feed the indexer) made a captured
+decode layer slower (106.7 vs 96.0 us at 180k context), the cross-stream
+join costing more than the overlap hides.
 Speculative decode rows (B tokens over B / next_n requests) are expanded per
 token as the reference does (triton_mla.py:267-279).
 
@@ -127,13 +131,22 @@ class DsaLayer:
         self.idx_k_cache = idx_k_cache     # [n_blocks, page, 128] fp16 or [.., 132] u8
         self.topk = topk
         self.kv_dtype = "fp8_ds_mla" if latent_cache.dtype == torch.uint8 else "auto"
+        # the writer's (unused) scale argument, made once: a fill per step costs a launch
+        self._one = torch.ones((), device=latent_cache.device)
 
     # -- cache writes -------------------------------------------------------
     def store(self, kv_c: torch.Tensor, k_pe: torch.Tensor, idx_k: torch.Tensor,
               slot_mapping: torch.Tensor) -> None:
         """Writes the step's tokens into both paged caches (slot < 0 skipped)."""
+        self.store_latent(kv_c, k_pe, slot_mapping)
+        self.store_index_key(idx_k, slot_mapping)
+
+    def store_latent(self, kv_c: torch.Tensor, k_pe: torch.Tensor,
+                     slot_mapping: torch.Tensor) -> None:
         _cache_ops.concat_and_cache_mla(kv_c, k_pe, self.latent_cache, slot_mapping,
-                                        self.kv_dtype, torch.ones((), device=kv_c.device))
+                                        self.kv_dtype, self._one)
+
+    def store_index_key(self, idx_k: torch.Tensor, slot_mapping: torch.Tensor) -> None:
         _sm70_ops.sm70_indexer_k_store(self.idx_k_cache, idx_k.to(torch.float16).contiguous(),
                                        slot_mapping.to(torch.int32))
 
@@ -162,8 +175,6 @@ class DsaLayer:
         counting the step's tokens).  With kv_c / k_pe / idx_k / slot_mapping
         the step's tokens are first written to the caches.  Returns
         out [B, H * V]."""
-        if kv_c is not None:
-            self.store(kv_c, k_pe, idx_k, slot_mapping)
         B, R = q.shape[0], seq_lens.shape[0]
         bt = block_table.to(torch.int32)
         sl = seq_lens.to(torch.int32)
@@ -173,6 +184,8 @@ class DsaLayer:
             offs = torch.arange(n, device=q.device, dtype=torch.int32)
             sl = (sl.unsqueeze(1) - (n - 1) + offs).reshape(-1).contiguous()
             bt = bt.repeat_interleave(n, dim=0).contiguous()
+        if kv_c is not None:
+            self.store(kv_c, k_pe, idx_k, slot_mapping)
         idx = self.decode_topk(idx_q, idx_w, bt, sl)
         ql = q_latent(q, self.w)
         o = torch.empty(B, self.w.n_heads, 512, dtype=torch.float16, device=q.device)
