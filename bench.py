@@ -381,7 +381,10 @@ def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128):
         layer = m.DsaLayer(w, d["kv"], ix["kc"])
         bt, seq = d["bt"], d["seq"]
         pos = (seq.long() - 1)
-        slot = bt.long().gather(1, (pos // page).view(B, 1)).view(B) * page + pos % page
+        # int32 slots: the indexer-K store takes int32 (sm70_mla_decode.cu:2919),
+        # and the latent writer accepts them too
+        slot = (bt.long().gather(1, (pos // page).view(B, 1)).view(B) * page
+                + pos % page).to(torch.int32)
         steps.append(dict(
             layer=layer, bt=bt, seq=seq, slot=slot,
             q=(torch.randn(B, H, P + 64, generator=g, device=dev) / 8).to(torch.float16),

@@ -36,8 +36,11 @@ constexpr int kIdxPPB = 1024;             // positions per workgroup
 constexpr int kIdxBlocksPerWave = kIdxPPB / 16 / kIdxWaves;  // 16
 constexpr int kIdxGroup = 2;              // 16-key blocks per pipeline stage
 
-// Key-row fragment of one 16-key block for one lane (key c, group g): dims
-// [32g, 32g+32) -- 64 bytes of an fp16 row or 32 bytes of an fp8 row.
+// Key-row fragment of one 16-key block for one lane (key c, group g).
+// fp16 rows: dims 32s + 8g .. +8 for steps s = 0..3, four 16-byte loads of
+// which load s of the four lanes of a key covers 64 contiguous bytes of its
+// row (one half cache line per key and instruction).  fp8 rows: dims
+// [32g, 32g+32), 32 bytes.
 struct KeyFrag {
   u32x4 v[4];
   float scale;  // fp8: row scale * 256; fp16: 1
@@ -62,14 +65,15 @@ __device__ __forceinline__ void load_key_frag(KeyFrag& f, const void* kv,
     f.scale = *reinterpret_cast<const float*>(rp + 128) * 256.0f;
   } else {
     const u32x4* p = reinterpret_cast<const u32x4*>(
-        reinterpret_cast<const f16*>(kv) + row * kIdxHeadDim + 32 * g);
+        reinterpret_cast<const f16*>(kv) + row * kIdxHeadDim + 8 * g);
 #pragma unroll
-    for (int i = 0; i < 4; i++) f.v[i] = p[i];
+    for (int i = 0; i < 4; i++) f.v[i] = p[4 * i];
     f.scale = 1.f;
   }
 }
 
-// B operand for step s (dims 32g + 8s .. +8) from a key fragment.
+// B operand for step s from a key fragment (dims 32s + 8g .. +8 for fp16
+// rows, 32g + 8s .. +8 for fp8 rows).
 template <bool KFP8>
 __device__ __forceinline__ f16x8 key_operand(const KeyFrag& f, int s) {
   if constexpr (KFP8) {
@@ -121,9 +125,9 @@ __global__ void __launch_bounds__(kIdxWaves * 64) indexer_logits_kernel(
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
 
-  // A operands: q rows (heads c and 16 + c).  k-slot mapping: step s,
-  // group g, slot e -> dim 32g + 8s + e, so a lane's key data is one
-  // contiguous 64-byte (fp16) / 32-byte (fp8) span of the row.
+  // A operands: q rows (heads c and 16 + c), with the keys' k-slot mapping:
+  // step s, group g, slot e -> dim 32s + 8g + e (fp16 keys) or 32g + 8s + e
+  // (fp8 keys, whose 32 bytes per lane are one contiguous span).
   f16x8 qa[2][4];
   const f16* qb = Q + (int64_t)b * kIdxHeads * kIdxHeadDim;
 #pragma unroll
@@ -131,7 +135,7 @@ __global__ void __launch_bounds__(kIdxWaves * 64) indexer_logits_kernel(
 #pragma unroll
     for (int s = 0; s < 4; s++)
       qa[t][s] = *reinterpret_cast<const f16x8*>(
-          qb + (16 * t + c) * kIdxHeadDim + 32 * g + 8 * s);
+          qb + (16 * t + c) * kIdxHeadDim + (KFP8 ? 32 * g + 8 * s : 32 * s + 8 * g));
   // head weights of this lane's D rows: heads 4g + r and 16 + 4g + r
   float wv[2][4];
 #pragma unroll
