@@ -15,8 +15,9 @@ GB/s); indexer prefill TFLOPS @64k"):
   prefill (the caller's 128-row sub-chunks, causal-triangle FLOPs only), a
   context-flatness sweep of the decode, the roofline of the decode kernel
   and the CPU baseline (the oracle's PyTorch restatement on the host cores),
-  and one whole DSA decode layer step (cache writes, indexer, top-k, the two
-  head projections and the attention) at the same shape.
+  one whole DSA decode layer step (cache writes, indexer, top-k, the two
+  head projections and the attention) at the same shape, and the dense MLA
+  decode (sm70_mla_decode) at 4k / 32k / 131k context.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L]
 Only one GPU is supported: --gpus N with N > 1 exits with a message.
@@ -175,7 +176,7 @@ def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
 
 SPARSE_PREFILL_T = 65536
 EXTRAS = ("sweep", "indexer_prefill", "sparse_prefill", "indexer_decode", "gemv", "k_store",
-          "dsa_layer")
+          "dsa_layer", "dense_decode")
 
 
 def sparse_prefill_flops(T=SPARSE_PREFILL_T, topk=2048, heads=64):
@@ -440,6 +441,34 @@ def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128):
     }
 
 
+def bench_dense_decode(torch, pkg, dev):
+    """Dense MLA decode (sm70_mla_decode) over an fp16 latent cache, B=4
+    tokens x 64 heads, at three context lengths; enough distinct caches per
+    graph that the rows stream from HBM.  Algorithmic bytes: the B x ctx
+    rows of 1152 B, each read once."""
+    ops = pkg._sm70_ops
+    out = {}
+    for ctx in (4096, 32768, 131072):
+        copies = max(2, min(8, (1200 << 20) // (4 * ctx * 1152)))
+        ins = [pkg.synthetic.decode_inputs(B=4, H=64, ctx=ctx, fp8=False, device=dev,
+                                           seed=90 + i) for i in range(copies)]
+        o = torch.empty(4, 64, 512, dtype=torch.float16, device=dev)
+        lse = torch.empty(4, 64, device=dev)
+
+        def fn():
+            for d in ins:
+                ops.sm70_mla_decode(o, lse, d["q"], d["kv"], d["bt"], d["seq"], d["scale"])
+
+        us = graph_time_per_call(torch, fn, copies)
+        nbytes = 4 * ctx * 1152
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out[str(ctx)] = {"us": round(us, 2), "gbps": round(gbps, 1),
+                         "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
+        del ins
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(torch, d, idxs, qs, budget_s):
     """The oracle's PyTorch restatement (fp32) of the same decode layers on
     the host cores: gather -> dequant -> QK -> softmax -> PV."""
@@ -588,6 +617,9 @@ def main():
         line["k_store"] = bench_k_store(torch, pkg, dev)
         log(f"k store: {line['k_store']}")
         torch.cuda.empty_cache()
+    if "dense_decode" in extras:
+        line["dense_mla_decode"] = bench_dense_decode(torch, pkg, dev)
+        log(f"dense mla decode: {line['dense_mla_decode']}")
     if "dsa_layer" in extras:
         line["dsa_layer_decode"] = bench_dsa_layer(torch, pkg, dev)
         log(f"dsa layer decode: {line['dsa_layer_decode']}")

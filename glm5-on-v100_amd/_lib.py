@@ -27,6 +27,9 @@ SIGNATURES = {
     "mi355_dsa_abi_version": (_c_int, []),
     "mi355_dsa_selfcheck": (_c_int, [_p]),
     "mi355_dsa_indexer_k_store": (_c_int, [_p, _c_int, _c_i64, _p, _c_i64, _c_int, _p, _p]),
+    "mi355_dsa_mla_decode_workspace_size": (_c_size, [_c_int, _c_int, _c_int]),
+    "mi355_dsa_mla_decode": (_c_int, [_p, _p, _p, _c_int, _c_int, _p, _c_i64, _c_int, _p, _c_int,
+                                      _p, _c_f32, _p, _c_size, _p]),
     "mi355_dsa_head_proj": (_c_int, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _c_int, _c_int,
                                      _c_int, _c_int, _c_int, _p]),
     "mi355_dsa_concat_and_cache_mla": (_c_int, [_p, _c_int, _c_i64, _p, _c_i64, _p, _c_i64,

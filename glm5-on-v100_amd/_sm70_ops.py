@@ -45,6 +45,14 @@ def sm70_attn_fp8_dequant(out: torch.Tensor, w: torch.Tensor, s: torch.Tensor) -
     _op("sm70_attn_fp8_dequant")(out, w, s)
 
 
+def sm70_mla_decode(o: torch.Tensor, lse: torch.Tensor, q: torch.Tensor,
+                    kv_cache: torch.Tensor, block_table: torch.Tensor,
+                    seq_lens: torch.Tensor, scale: float) -> None:
+    """Dense MLA decode over positions [0, seq_len): writes o [B,H,512] fp16,
+    lse [B,H] fp32 (reference/_sm70_ops.py:1774-1784)."""
+    _op("sm70_mla_decode")(o, lse, q, kv_cache, block_table, seq_lens, scale)
+
+
 def sm70_sparse_mla_decode(o: torch.Tensor, lse: torch.Tensor, q: torch.Tensor,
                            kv_cache: torch.Tensor, idx: torch.Tensor,
                            block_table: torch.Tensor, seq_lens: torch.Tensor,

@@ -163,6 +163,14 @@ constexpr int kResU = 8;
 template <int NT>
 __device__ __forceinline__ void resolve_idx(const MlaParams& p, int b, int j0, int n, int base,
                                             int pos[kResU]) {
+  if (p.idx == nullptr) {  // dense: key j is position j
+#pragma unroll
+    for (int u = 0; u < kResU; u++) {
+      const int j = base + u * NT + (int)threadIdx.x;
+      pos[u] = (j < n) ? j0 + j : -1;
+    }
+    return;
+  }
   const int32_t* idx_row = p.idx + (int64_t)b * p.topk + j0;
 #pragma unroll
   for (int u = 0; u < kResU; u++) {
@@ -183,16 +191,23 @@ __device__ __forceinline__ void resolve_bt(const MlaParams& p, int b, int seq_le
   }
 }
 
+// Row codes: >= 0 a cache row; -1 a masked key; -2 (dense mode only) a
+// position below seq_len whose row does not resolve -- it reads as a zero
+// row and stays in the softmax with score 0, as the reference's dense kernel
+// does (sm70_mla_decode.cu:762-771).
 template <int NT>
-__device__ __forceinline__ void resolve_store(const MlaParams& p, int n, int base,
+__device__ __forceinline__ void resolve_store(const MlaParams& p, int n, int base, int seq_len,
                                               const int pos[kResU], const int pg[kResU],
                                               const int blk[kResU], int32_t* rows) {
+  const bool dense = p.idx == nullptr;
 #pragma unroll
   for (int u = 0; u < kResU; u++) {
     const int j = base + u * NT + (int)threadIdx.x;
     if (j < n) {
       const int64_t row = (int64_t)blk[u] * p.page_size + (pos[u] - pg[u] * p.page_size);
-      rows[j] = (blk[u] < 0 || row >= p.n_kv_rows) ? -1 : (int32_t)row;
+      const bool bad = blk[u] < 0 || row >= p.n_kv_rows;
+      const bool in_range = pos[u] >= 0 && pos[u] < seq_len;
+      rows[j] = bad ? ((dense && in_range) ? -2 : -1) : (int32_t)row;
     }
   }
 }
@@ -230,7 +245,10 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
   const int seq_len = p.seq_lens[b];
 
   // ---- this workgroup's key range (tiles of TN) ----
-  const int n_tiles_all = (p.topk + TN - 1) / TN;
+  // Dense mode (idx == nullptr) attends to positions [0, seq_len): the
+  // token's own length is split, not the table's width.
+  const int n_keys = p.idx ? p.topk : max(0, min(p.topk, seq_len));
+  const int n_tiles_all = (n_keys + TN - 1) / TN;
   const int tps = (n_tiles_all + p.n_splits - 1) / p.n_splits;  // tiles per split
   const int tile_lo = split * tps;
   const int tile_hi = min(tile_lo + tps, n_tiles_all);
@@ -238,7 +256,7 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
 
   // first index batch in flight while Q is staged
   int pos0[kResU];
-  const int nkeys0 = tile_lo < tile_hi ? min(min(tile_lo + SEG_TILES, tile_hi) * TN, p.topk) - tile_lo * TN : 0;
+  const int nkeys0 = tile_lo < tile_hi ? min(min(tile_lo + SEG_TILES, tile_hi) * TN, n_keys) - tile_lo * TN : 0;
   resolve_idx<NT>(p, b, tile_lo * TN, nkeys0, 0, pos0);
 
   // ---- scaled Q of this workgroup's heads into LDS; the block-table loads
@@ -285,16 +303,16 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
   for (int seg_lo = tile_lo; seg_lo < tile_hi; seg_lo += SEG_TILES) {
     const int seg_hi = min(seg_lo + SEG_TILES, tile_hi);
     const int j0 = seg_lo * TN;
-    const int nkeys = min(seg_hi * TN, p.topk) - j0;
+    const int nkeys = min(seg_hi * TN, n_keys) - j0;
     __syncthreads();  // previous segment done with sh.rows
     for (int base = 0; base < nkeys; base += NT * kResU) {
       if (seg_lo == tile_lo && base == 0) {
-        resolve_store<NT>(p, nkeys, base, pos0, pg0, blk0, sh.rows);
+        resolve_store<NT>(p, nkeys, base, seq_len, pos0, pg0, blk0, sh.rows);
       } else {
         int pos[kResU], pg[kResU], blk[kResU];
         resolve_idx<NT>(p, b, j0, nkeys, base, pos);
         resolve_bt<NT>(p, b, seq_len, pos, pg, blk);
-        resolve_store<NT>(p, nkeys, base, pos, pg, blk, sh.rows);
+        resolve_store<NT>(p, nkeys, base, seq_len, pos, pg, blk, sh.rows);
       }
     }
     __syncthreads();
@@ -346,7 +364,7 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
 #pragma unroll
       for (int nb = 0; nb < NB; nb++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) valid[nb][r] = row_of(rd, 16 * nb + 4 * g + r) >= 0;
+        for (int r = 0; r < 4; r++) valid[nb][r] = row_of(rd, 16 * nb + 4 * g + r) != -1;
       if (rd + 1 < rounds) issue(rd + 1);
       __syncthreads();
 
@@ -1198,6 +1216,279 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp16-row attention over 64 heads, software-pipelined over 32-key tiles:
+// the fp16 (576-half) latent cache in the prefill configuration, and dense
+// decode (idx == nullptr) split over the context.
+//
+// Workgroup = (token, 64 heads, split), 8 waves; tiles of raw 1152-byte rows
+// stream through a 3-slot LDS ring by LDS-DMA, each row at a 1168-byte pitch
+// (72 pieces + one zero pad, so the 16 rows of an MFMA operand spread over
+// the banks as the fp8 rows do).
+//   * QK: wave w = (key block kb = w & 1, dim half dh = (w >> 1) & 1, head
+//     half hh = w >> 2) computes S^T for keys [16 kb, +16) x heads
+//     [32 hh, +32) over dims [288 dh, +288), Q of its 32 heads for those dims
+//     resident in registers.  The two dim halves meet in LDS and are summed
+//     in a fixed order.
+//   * softmax: as the fp8 kernel (thread t owns head t / 8 and keys
+//     4 (t % 8) .. +3, lazy running max, DPP reductions); P in fp16.
+//   * PV: wave w owns value dims [64 w, +64) for all 64 heads; V^T operands
+//     come from ds_read_b64_tr_b16 transpose reads (4 keys each).
+// Phases per tile as in the fp8 kernel: X = {PV(i), QK(i+1)}, then
+// Y = {softmax(i+1), LDS-DMA of tile i+3, wait for tile i+2}.
+// Split s of a token covers keys [s kps, (s+1) kps) of its key list (the
+// top-k list, or positions [0, seq_len) in dense mode) and, with more than
+// one split, writes its normalised partial for the merge kernel.
+// ---------------------------------------------------------------------------
+constexpr int kHfPitchPieces = kLatentDim / 8 + 1;                       // 73
+constexpr int kHfRowPitch = kHfPitchPieces * 16;                         // 1168 B
+constexpr int kHfPieces = kPfTileKeys * kHfPitchPieces;                  // 2336
+constexpr int kHfRounds = (kHfPieces + kPfThreads - 1) / kPfThreads;     // 5
+constexpr int kHfSlotBytes = kHfRounds * kPfThreads * 16;                // 40960
+constexpr int kHfSegKeys = 1024;
+constexpr int kHfHalfDims = kLatentDim / 2;                              // 288
+constexpr int kHfSteps = kHfHalfDims / 32;                               // 9
+
+struct HfSmem {
+  uint8_t ring[kP3Ring][kHfSlotBytes];
+  int32_t rows[kHfSegKeys];
+  float sp[2][64 * kP3SPitch];  // [dim half][head][key]
+  f16 pt[64 * kP3PPitch];       // [head][key]
+  f32x4 alpha[16];
+  f32x4 lsum[16];
+  int rescale[2];
+};
+
+__device__ __forceinline__ void hf_dma_tile(const uint8_t* __restrict__ kv, const int32_t* rows,
+                                            uint8_t* slot) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int row[kHfRounds];
+#pragma unroll
+  for (int u = 0; u < kHfRounds; u++) {
+    const int q = kPfThreads * u + 64 * wave + lane;
+    const int r = q / kHfPitchPieces;
+    row[u] = rows[r < kPfTileKeys ? r : 0];
+  }
+#pragma unroll
+  for (int u = 0; u < kHfRounds; u++) {
+    const int q = kPfThreads * u + 64 * wave + lane;
+    const int r = q / kHfPitchPieces, ch = q - r * kHfPitchPieces;
+    const bool ok = q < kHfPieces && ch < kLatentDim / 8 && row[u] >= 0;
+    const uint8_t* src = ok ? kv + (int64_t)row[u] * (kLatentDim * 2) + 16 * ch : kZeroRow;
+    dma16(src, slot + 16 * (kPfThreads * u + 64 * wave));
+  }
+}
+
+__device__ __forceinline__ void hf_wait(int k) {  // at most k tiles still in flight
+  if (k <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kHfRounds) : "memory");
+}
+
+__global__ void __launch_bounds__(kPfThreads) mla_attn_f16_kernel(MlaParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  HfSmem& sh = *reinterpret_cast<HfSmem*>(smem_raw);
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int kb = w & 1, dh = (w >> 1) & 1, hh = w >> 2;  // QK role
+  int b;
+  {
+    // XCD-aware token order: consecutive tokens share an XCD
+    const int nx = gridDim.x, bid = blockIdx.x;
+    const int xcd = bid & 7, j = bid >> 3;
+    const int per = nx >> 3, rem = nx & 7;
+    b = xcd * per + (xcd < rem ? xcd : rem) + j;
+  }
+  const int hbase = blockIdx.y * 64;
+  const int split = blockIdx.z;
+  const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
+  const int seq_len = p.seq_lens[b];
+
+  // ---- this workgroup's keys ----
+  const int n_keys = p.idx ? p.topk : max(0, min(p.topk, seq_len));
+  const int kps = ((n_keys + p.n_splits - 1) / p.n_splits + kPfTileKeys - 1) / kPfTileKeys *
+                  kPfTileKeys;
+  const int k_lo = min(split * kps, n_keys);
+  const int k_hi = min(k_lo + kps, n_keys);
+
+  // ---- Q of this wave's 32 heads over its 288 dims, scaled in fp16 ----
+  // step s: lane (head c of group hg, g) holds dims 288 dh + 32 s + 8 g .. +8
+  f16x8 qf[2][kHfSteps];
+  {
+    const f16 sc = (f16)p.scale_h;
+    const f16x8 sc8 = {sc, sc, sc, sc, sc, sc, sc, sc};
+#pragma unroll
+    for (int hg = 0; hg < 2; hg++) {
+      const int h = hbase + 32 * hh + 16 * hg + c;
+      const f16* qrow = p.q + ((int64_t)b * p.n_head + (h < p.n_head ? h : 0)) * kLatentDim +
+                        kHfHalfDims * dh + 8 * g;
+#pragma unroll
+      for (int st = 0; st < kHfSteps; st++)
+        qf[hg][st] = *reinterpret_cast<const f16x8*>(qrow + 32 * st) * sc8;
+    }
+  }
+
+  const int sm_h = threadIdx.x >> 3, sm_k = threadIdx.x & 7;  // softmax role
+  float m_run = -1e30f, l_run = 0.f;
+  f32x4 oacc[4][4];  // [dim tile][head group]: O^T of dims 64 w + 16 t + ..
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int hg = 0; hg < 4; hg++) oacc[t][hg] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  auto qk = [&](const uint8_t* cb) {
+    const uint8_t* krow = cb + (16 * kb + c) * kHfRowPitch + 2 * (kHfHalfDims * dh + 8 * g);
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int st = 0; st < kHfSteps; st++) {
+      const f16x8 kf = *reinterpret_cast<const f16x8*>(krow + 64 * st);
+#pragma unroll
+      for (int hg = 0; hg < 2; hg++) acc[hg] = mfma16x16x32(kf, qf[hg][st], acc[hg]);
+    }
+#pragma unroll
+    for (int hg = 0; hg < 2; hg++)
+      *reinterpret_cast<f32x4*>(&sh.sp[dh][(32 * hh + 16 * hg + c) * kP3SPitch + 16 * kb + 4 * g]) =
+          acc[hg];
+  };
+
+  auto softmax = [&](const int32_t* trows, int* flag) {
+    f32x4 s4 = *reinterpret_cast<const f32x4*>(&sh.sp[0][sm_h * kP3SPitch + 4 * sm_k]);
+    s4 += *reinterpret_cast<const f32x4*>(&sh.sp[1][sm_h * kP3SPitch + 4 * sm_k]);
+    const int4 vr = *reinterpret_cast<const int4*>(trows + 4 * sm_k);
+    const int vv[4] = {vr.x, vr.y, vr.z, vr.w};
+    float mt = -1e30f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      s4[r] = vv[r] != -1 ? s4[r] : -INFINITY;  // -2: dense zero row, a valid key
+      mt = fmaxf(mt, s4[r]);
+    }
+    mt = max8(mt);
+    float alpha = 1.f;
+    if (mt > m_run + kPfLazyMax) {
+      const float m_new = fmaxf(m_run, mt);
+      alpha = __expf(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+      *flag = 1;
+    }
+    if (sm_k == 0) reinterpret_cast<float*>(&sh.alpha[sm_h & 15])[sm_h >> 4] = alpha;
+    f16x4 ph;
+    float ls = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float pr = (s4[r] > -INFINITY) ? __expf(s4[r] - m_run) : 0.f;
+      ls += pr;
+      ph[r] = (f16)pr;
+    }
+    l_run += sum8(ls);
+    *reinterpret_cast<f16x4*>(&sh.pt[sm_h * kP3PPitch + 4 * sm_k]) = ph;
+  };
+
+  auto pv = [&](const uint8_t* cb, bool rescale) {
+    if (rescale) {
+      const f32x4 al = sh.alpha[c];
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int hg = 0; hg < 4; hg++) oacc[t][hg] *= al[hg];
+    }
+    f16x8 pb[4];
+#pragma unroll
+    for (int hg = 0; hg < 4; hg++)
+      pb[hg] = *reinterpret_cast<const f16x8*>(&sh.pt[(16 * hg + c) * kP3PPitch + 8 * g]);
+    // transpose reads: lane i of group g supplies key 8 g + i / 4 (+4 for the
+    // second read), dims 64 w + 16 t + 4 (i % 4) .. +3; lane j receives keys
+    // 8 g .. 8 g + 3 (then + 4 .. + 7) at dim 64 w + 16 t + j
+    const uint8_t* vsrc = cb + (8 * g + (c >> 2)) * kHfRowPitch + 2 * (64 * w + 4 * (c & 3));
+    s16x4 v0[4], v1[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      v0[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vsrc + 32 * t));
+      v1[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vsrc + 4 * kHfRowPitch + 32 * t));
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const f16x4 x0 = __builtin_bit_cast(f16x4, v0[t]), x1 = __builtin_bit_cast(f16x4, v1[t]);
+      const f16x8 av = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+      for (int hg = 0; hg < 4; hg++) oacc[t][hg] = mfma16x16x32(av, pb[hg], oacc[t][hg]);
+    }
+  };
+
+  for (int seg_lo = k_lo; seg_lo < k_hi; seg_lo += kHfSegKeys) {
+    const int nkeys = min(k_hi - seg_lo, kHfSegKeys);
+    const int ntiles = (nkeys + kPfTileKeys - 1) / kPfTileKeys;
+    lds_barrier();  // previous segment done with rows and the ring
+    for (int base = 0; base < ntiles * kPfTileKeys; base += kPfThreads * kResU) {
+      int pos[kResU], pg[kResU], blk[kResU];
+      resolve_idx<kPfThreads>(p, b, seg_lo, nkeys, base, pos);
+      resolve_bt<kPfThreads>(p, b, seq_len, pos, pg, blk);
+      resolve_store<kPfThreads>(p, ntiles * kPfTileKeys, base, seq_len, pos, pg, blk, sh.rows);
+    }
+    lds_barrier();
+    hf_dma_tile(kv, sh.rows, sh.ring[0]);
+    if (ntiles > 1) hf_dma_tile(kv, sh.rows + kPfTileKeys, sh.ring[1]);
+    hf_wait(ntiles > 1 ? 1 : 0);
+    if (threadIdx.x == 0) sh.rescale[0] = 0;
+    lds_barrier();  // tile 0 landed
+    qk(sh.ring[0]);
+    lds_barrier();
+    softmax(sh.rows, &sh.rescale[0]);
+    if (ntiles > 2) hf_dma_tile(kv, sh.rows + 2 * kPfTileKeys, sh.ring[2]);
+    hf_wait(ntiles > 2 ? 1 : 0);  // tile 1 landed (this wave's part)
+    lds_barrier();
+
+    for (int i = 0; i < ntiles; i++) {
+      const bool rescale = sh.rescale[i & 1] != 0;
+      if (threadIdx.x == 0) sh.rescale[(i + 1) & 1] = 0;
+      pv(sh.ring[i % kP3Ring], rescale);
+      if (i + 1 < ntiles) qk(sh.ring[(i + 1) % kP3Ring]);
+      lds_barrier();
+      if (i + 1 < ntiles) {
+        softmax(sh.rows + (i + 1) * kPfTileKeys, &sh.rescale[(i + 1) & 1]);
+        if (i + 3 < ntiles) hf_dma_tile(kv, sh.rows + (i + 3) * kPfTileKeys, sh.ring[i % kP3Ring]);
+        hf_wait(i + 3 < ntiles ? 1 : 0);
+        lds_barrier();
+      }
+    }
+  }
+
+  // ---- outputs: o = O / l and lse, or the split's partial ----
+  const bool final_out = (p.n_splits == 1);
+  if (sm_k == 0) {
+    reinterpret_cast<float*>(&sh.lsum[sm_h & 15])[sm_h >> 4] = l_run;
+    const int h = hbase + sm_h;
+    if (h < p.n_head) {
+      const int64_t bh = (int64_t)b * p.n_head + h;
+      if (final_out) {
+        p.lse[bh] = (l_run > 0.f) ? (m_run + logf(l_run)) : p.empty_lse;
+      } else {
+        const int64_t ps = bh * p.n_splits + split;
+        p.part_ml[ps * 2 + 0] = m_run;
+        p.part_ml[ps * 2 + 1] = l_run;
+      }
+    }
+  }
+  lds_barrier();
+  const f32x4 L = sh.lsum[c];
+#pragma unroll
+  for (int hg = 0; hg < 4; hg++) {
+    const int h = hbase + 16 * hg + c;
+    if (h >= p.n_head) continue;
+    const int64_t bh = (int64_t)b * p.n_head + h;
+    const float inv = (L[hg] > 0.f) ? 1.f / L[hg] : 0.f;
+    f16* orow = (final_out ? p.o + bh * kValueDim
+                           : p.part_o + (bh * p.n_splits + split) * kValueDim) + 64 * w;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      f16x4 v;
+#pragma unroll
+      for (int r = 0; r < 4; r++) v[r] = (f16)(oacc[t][hg][r] * inv);
+      *reinterpret_cast<f16x4*>(orow + 16 * t + 4 * g) = v;
+    }
+  }
+}
+
 // Flash-decode merge of S partial states (reference :1138-1184):
 // m = max_s m_s, w_s = l_s > 0 ? exp(m_s - m) l_s : 0, o = sum w_s o_s / sum w_s
 // (o_s is the split's own normalised output, stored in fp16).
@@ -1291,6 +1582,29 @@ static int decode_splits(int B, int n_head, int topk) {
   return s;
 }
 
+// dense decode: splits of the context so that ~256 workgroups run, at least
+// one 32-key tile each
+static int dense_splits(int B, int n_head, int max_kv) {
+  const int hg = (n_head + 63) / 64;
+  int s = kTargetWGs / (B * hg > 0 ? B * hg : 1);
+  const int max_s = (max_kv + kPfTileKeys - 1) / kPfTileKeys;
+  if (s > max_s) s = max_s;
+  if (s > kMergeMaxSplits) s = kMergeMaxSplits;
+  if (s < 1) s = 1;
+  return s;
+}
+
+static int launch_attn_f16(const MlaParams& prm, dim3 grid, hipStream_t st) {
+  static bool attr = false;
+  if (!attr) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(mla_attn_f16_kernel),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(HfSmem));
+    attr = true;
+  }
+  mla_attn_f16_kernel<<<grid, kPfThreads, sizeof(HfSmem), st>>>(prm);
+  return check_launch("mla_attn_f16");
+}
+
 template <bool KVFP8, int HW, int KW, int NB>
 static int launch_mla(const MlaParams& prm, dim3 grid, hipStream_t st) {
   using Smem = MlaSmem<HW, KW, NB>;
@@ -1324,19 +1638,21 @@ extern "C" size_t mi355_dsa_sparse_mla_workspace_size(int B, int n_head, int top
   return (size_t)B * n_head * S * (kValueDim * sizeof(f16) + 2 * sizeof(float));
 }
 
-extern "C" int mi355_dsa_sparse_mla_decode(
+// Sparse (idx given, topk keys per token) and dense (idx == nullptr: the
+// positions [0, seq_len) of each token, topk = the block table's width in
+// keys) attention share the kernels below.
+static int mla_decode_impl(
     void* o, float* lse, const void* q, int B, int n_head, const void* kv_cache,
     int kv_fp8, int64_t n_kv_rows, int page_size, const int32_t* idx, int topk,
     const int32_t* block_table, int max_blocks, const int32_t* seq_lens,
-    float scale, void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
+    float scale, void* workspace, size_t workspace_bytes, void* stream, bool dense) {
   DSA_CHECK(B >= 0 && n_head > 0, "n_head must be > 0");
   DSA_CHECK(topk >= 0 && max_blocks >= 0 && n_kv_rows >= 0, "bad sizes");
   DSA_CHECK(page_size > 0, "page size must be > 0");
   DSA_CHECK(n_kv_rows < ((int64_t)1 << 31), "cache has too many rows");
   if (B == 0) return MI355_DSA_OK;
   DSA_CHECK(o && lse && q && kv_cache && seq_lens, "null pointer argument");
-  DSA_CHECK(topk == 0 || idx, "null idx");
+  DSA_CHECK(dense || topk == 0 || idx, "null idx");
   DSA_CHECK(max_blocks == 0 || block_table, "null block_table");
   DSA_CHECK(aligned_to(q, 16) && aligned_to(kv_cache, 16) && aligned_to(o, 8),
             "q / kv_cache / o misaligned");
@@ -1344,7 +1660,7 @@ extern "C" int mi355_dsa_sparse_mla_decode(
   MlaParams prm;
   prm.q = reinterpret_cast<const f16*>(q);
   prm.kv = kv_cache;
-  prm.idx = idx;
+  prm.idx = dense ? nullptr : idx;
   prm.bt = block_table;
   prm.seq_lens = seq_lens;
   prm.o = reinterpret_cast<f16*>(o);
@@ -1359,10 +1675,29 @@ extern "C" int mi355_dsa_sparse_mla_decode(
   prm.page_shift = (page_size & (page_size - 1)) == 0 ? ilog2_pow2(page_size) : -1;
   prm.n_kv_rows = n_kv_rows;
   prm.scale_h = (float)(f16)scale;
-  // the reference's prefill kernel (taken for B >= 32 && n_head <= 16,
-  // sm70_mla_decode.cu:2511) leaves lse = -1e30 + ln 1 for an empty token
-  prm.empty_lse = (B >= 32 && n_head <= 16) ? -1e30f : -INFINITY;
+  // the reference's sparse prefill kernel (taken for B >= 32 && n_head <= 16,
+  // sm70_mla_decode.cu:2511) leaves lse = -1e30 + ln 1 for an empty token;
+  // its dense decode writes -inf (:891-894)
+  prm.empty_lse = (!dense && B >= 32 && n_head <= 16) ? -1e30f : -INFINITY;
   hipStream_t st = as_stream(stream);
+
+  if (dense) {
+    const int S = dense_splits(B, n_head, topk);
+    prm.n_splits = S;
+    if (S > 1) {
+      const size_t need = mi355_dsa_mla_decode_workspace_size(B, n_head, topk);
+      DSA_CHECK(workspace && workspace_bytes >= need,
+                "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+      DSA_CHECK(aligned_to(workspace, 16), "workspace must be 16-byte aligned");
+      prm.part_o = reinterpret_cast<f16*>(workspace);
+      prm.part_ml = reinterpret_cast<float*>(prm.part_o + (size_t)B * n_head * S * kValueDim);
+    }
+    int rc = launch_attn_f16(prm, dim3(B, (n_head + 63) / 64, S), st);
+    if (rc != MI355_DSA_OK || S == 1) return rc;
+    sparse_mla_merge_kernel<<<dim3((unsigned)((int64_t)B * n_head)), 128, 0, st>>>(
+        prm.part_o, prm.part_ml, prm.o, prm.lse, S, prm.empty_lse);
+    return check_launch("sparse_mla_merge");
+  }
 
   if (use_prefill_config(B, n_head)) {
     prm.n_splits = 1;
@@ -1377,9 +1712,9 @@ extern "C" int mi355_dsa_sparse_mla_decode(
       sparse_mla_prefill_fp8_kernel<<<grid, kPfThreads, sizeof(P3Smem), st>>>(prm);
       return check_launch("sparse_mla_decode");
     }
-    return launch_mla<false, 4, 1, 2>(prm, grid, st);
+    return launch_attn_f16(prm, dim3(B, (n_head + 63) / 64, 1), st);
   }
-  const bool dma = kv_fp8 && use_dma_decode(topk);
+  const bool dma = kv_fp8 && !dense && use_dma_decode(topk);
   const int S = splits_for(B, n_head, topk, kv_fp8);
   prm.n_splits = S;
   if (S > 1) {
@@ -1409,4 +1744,36 @@ extern "C" int mi355_dsa_sparse_mla_decode(
   sparse_mla_merge_kernel<<<dim3((unsigned)((int64_t)B * n_head)), 128, 0, st>>>(
       prm.part_o, prm.part_ml, prm.o, prm.lse, S, prm.empty_lse);
   return check_launch("sparse_mla_merge");
+}
+
+extern "C" int mi355_dsa_sparse_mla_decode(
+    void* o, float* lse, const void* q, int B, int n_head, const void* kv_cache,
+    int kv_fp8, int64_t n_kv_rows, int page_size, const int32_t* idx, int topk,
+    const int32_t* block_table, int max_blocks, const int32_t* seq_lens,
+    float scale, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return mla_decode_impl(o, lse, q, B, n_head, kv_cache, kv_fp8, n_kv_rows, page_size, idx,
+                         topk, block_table, max_blocks, seq_lens, scale, workspace,
+                         workspace_bytes, stream, false);
+}
+
+extern "C" size_t mi355_dsa_mla_decode_workspace_size(int B, int n_head, int max_kv) {
+  if (B <= 0 || n_head <= 0 || max_kv <= 0) return 0;
+  const int S = dense_splits(B, n_head, max_kv);
+  if (S <= 1) return 0;
+  return (size_t)B * n_head * S * (kValueDim * sizeof(f16) + 2 * sizeof(float));
+}
+
+extern "C" int mi355_dsa_mla_decode(void* o, float* lse, const void* q, int B, int n_head,
+                                    const void* kv_cache, int64_t n_kv_rows, int page_size,
+                                    const int32_t* block_table, int max_blocks,
+                                    const int32_t* seq_lens, float scale, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  clear_error();
+  DSA_CHECK(max_blocks >= 0 && page_size > 0 && (int64_t)max_blocks * page_size < (1 << 30),
+            "mla_decode: block table too wide");
+  const int max_kv = max_blocks * page_size;
+  return mla_decode_impl(o, lse, q, B, n_head, kv_cache, 0, n_kv_rows, page_size, nullptr,
+                         max_kv, block_table, max_blocks, seq_lens, scale, workspace,
+                         workspace_bytes, stream, true);
 }

@@ -24,6 +24,9 @@ from . import _lib
 NAMESPACE = os.environ.get("MI355_DSA_NAMESPACE", "mi355_dsa")
 
 SCHEMAS = {
+    "sm70_mla_decode": (
+        "sm70_mla_decode(Tensor! o, Tensor! lse, Tensor q, Tensor kv_cache, "
+        "Tensor block_table, Tensor seq_lens, float scale) -> ()"),
     "sm70_sparse_mla_decode": (
         "sm70_sparse_mla_decode(Tensor! o, Tensor! lse, Tensor q, "
         "Tensor kv_cache, Tensor idx, Tensor block_table, Tensor seq_lens, "
@@ -82,6 +85,43 @@ def _out_ok(t: torch.Tensor, name: str) -> None:
 # ---------------------------------------------------------------------------
 # implementations (CUDA dispatch key)
 # ---------------------------------------------------------------------------
+def mla_decode_impl(o, lse, q, kv_cache, block_table, seq_lens, scale):
+    """Dense decode, sm70_mla_decode.cu:1474-1501 checks (fp16 cache only,
+    n_head a multiple of 32)."""
+    _check(q.is_cuda and kv_cache.is_cuda, "q and kv_cache must be on the GPU")
+    _check(q.dtype == torch.float16, "q must be fp16")
+    _check(kv_cache.dtype == torch.float16, "kv_cache must be fp16")
+    _check(o.dtype == torch.float16, "o must be fp16")
+    _check(lse.dtype == torch.float32, "lse must be fp32")
+    _check(block_table.dtype == torch.int32, "block_table must be int32")
+    _check(seq_lens.dtype == torch.int32, "seq_lens must be int32")
+    _check(q.dim() == 3 and q.size(2) == 576, "q last dim must be 576")
+    B, H = q.size(0), q.size(1)
+    _check(H % 32 == 0 and H > 0, "n_head must be a multiple of 32")
+    _check(o.dim() == 3 and o.size(0) == B and o.size(1) == H and o.size(2) == 512,
+           "o last dim must be 512")
+    _check(lse.dim() == 2 and lse.size(0) == B and lse.size(1) == H, "lse must be [B, H]")
+    _check(block_table.dim() == 2 and block_table.size(0) == B, "block_table must be [B, max_blocks]")
+    _check(seq_lens.numel() == B, "seq_lens must be [B]")
+    _check(kv_cache.size(-1) == 576, "kv_cache last dim must be 576")
+    _check(kv_cache.is_contiguous(), "kv_cache must be contiguous")
+    _out_ok(o, "o")
+    _out_ok(lse, "lse")
+    if B == 0:
+        return
+    q, block_table, seq_lens = _contig(q), _contig(block_table), _contig(seq_lens)
+    page = kv_cache.size(-2)
+    n_rows = kv_cache.numel() // 576
+    max_blocks = block_table.size(1)
+    L = _lib.lib()
+    ws_bytes = L.mi355_dsa_mla_decode_workspace_size(B, H, max_blocks * page)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.call("mi355_dsa_mla_decode", o.data_ptr(), lse.data_ptr(), q.data_ptr(), B, H,
+                  kv_cache.data_ptr(), n_rows, page, block_table.data_ptr(), max_blocks,
+                  seq_lens.data_ptr(), float(scale), ws.data_ptr(), ws_bytes, _stream(q))
+
+
 def sparse_mla_decode_impl(o, lse, q, kv_cache, idx, block_table, seq_lens, scale):
     """sm70_mla_decode.cu:2457-2616 checks."""
     _check(q.is_cuda and kv_cache.is_cuda, "q and kv_cache must be on the GPU")
@@ -376,6 +416,7 @@ def attn_fp8_quantize(weight):
 
 
 IMPLS = {
+    "sm70_mla_decode": mla_decode_impl,
     "sm70_sparse_mla_decode": sparse_mla_decode_impl,
     "sm70_indexer_logits": indexer_logits_impl,
     "sm70_indexer_logits_packed": indexer_logits_packed_impl,

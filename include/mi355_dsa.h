@@ -91,6 +91,28 @@ int mi355_dsa_concat_and_cache_mla(void* kv_cache, int kv_fp8, int64_t n_rows,
                                    void* stream);
 
 /*
+ * Dense MLA decode over a paged fp16 latent cache: for each token b and head
+ * h, attention of q[b,h,:576] * scale over the cache rows of positions
+ * [0, seq_lens[b]) (row(p) = bt[b, p/page]*page + p%page; a position whose
+ * page index is >= max_blocks or whose row is outside [0, n_kv_rows) is
+ * skipped).  V = the first 512 dims of a row.  q * scale is rounded to fp16
+ * (scale itself rounded to fp16 first) and P to fp16 before PV; O is
+ * accumulated in fp32.  o fp16 [B,H,512], lse fp32 [B,H] (natural log; a
+ * token with no valid position gets o = 0, lse = -inf).  kv_cache rows are
+ * 576 fp16; n_kv_rows counts them.  Needs workspace of
+ * mi355_dsa_mla_decode_workspace_size(B, n_head, max_blocks * page_size)
+ * bytes (16-byte aligned; 0 means none).
+ * Replaces sm70_mla_decode (csrc/attention/sm70_mla_decode.cu:717-898, host
+ * :1474-1534), whose kernel keeps the running O in fp16 between 32-key tiles.
+ */
+size_t mi355_dsa_mla_decode_workspace_size(int B, int n_head, int max_kv);
+int mi355_dsa_mla_decode(void* o, float* lse, const void* q, int B, int n_head,
+                         const void* kv_cache, int64_t n_kv_rows, int page_size,
+                         const int32_t* block_table, int max_blocks,
+                         const int32_t* seq_lens, float scale, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/*
  * Per-head projection of an MLA layer (fp16 in and out, fp32 accumulation):
  *   out[t,h,n]   = sum_k x[t,h,k] * wt[h,n,k]    (t < T, h < H, n < N, k < K)
  *   out[t,h,N+i] = x[t,h,K+i]                    (i < tail)

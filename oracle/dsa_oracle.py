@@ -297,6 +297,76 @@ def dense_mla(q: torch.Tensor, kv_cache: torch.Tensor, bt: torch.Tensor,
     return sparse_mla(q, kv_cache, idx, bt, seq_lens, scale, dtype)
 
 
+def mla_decode(q: torch.Tensor, kv_cache: torch.Tensor, bt: torch.Tensor,
+               seq_lens: torch.Tensor, scale: float, fp16_acc: bool = False, tile: int = 32):
+    """Dense MLA decode, the reference's sm70_mla_decode
+    (sm70_mla_decode.cu:717-898, host :1474-1534): positions [0, seq_len) of
+    an fp16 latent cache, q * fp16(scale) rounded to fp16 (:793-794), V = the
+    first 512 dims, lse = m + ln l, and o = 0 / lse = -inf for a token with no
+    valid position (:887-895).
+
+    A position below seq_len whose row does not resolve (page index past the
+    table, negative block, row outside the cache) reads a zero row and stays
+    in the softmax with score 0 (:762-771, :826-832).  Positions at or past
+    the table's width (max_blocks * page) are not attended: the reference
+    reads its block table out of bounds there (:766), which defines nothing.
+
+    fp16_acc=False: exact (fp64) attention.
+    fp16_acc=True: the kernel's own arithmetic tile by tile (`tile` keys,
+    :759): running max from -1e30 (:746), p = exp(s - m) rounded to fp16 for
+    PV while l sums the unrounded p (:839-841), and the running O kept in
+    fp16 -- rescaled by alpha and rounded (:850-851), then the tile's P V
+    (fp32 sum) added and rounded again (:873-875); o = fp16(O / l)."""
+    B, H, _ = q.shape
+    page = kv_cache.shape[-2]
+    n_rows = kv_cache.numel() // 576
+    flat = kv_cache.reshape(n_rows, 576)
+    o = torch.zeros(B, H, 512, dtype=torch.float32)
+    lse = torch.full((B, H), float("-inf"), dtype=torch.float32)
+    qs = scaled_q(q, scale).to(torch.float64)
+    for b in range(B):
+        L = min(int(seq_lens[b]), bt.shape[1] * page)
+        if not fp16_acc:
+            if L <= 0:
+                continue
+            rows = resolve_rows(torch.arange(L), bt[b], page, n_rows)
+            kv = torch.zeros(L, 576, dtype=torch.float64)
+            ok = rows >= 0
+            kv[ok] = flat[rows[ok]].to(torch.float64)
+            sc = qs[b] @ kv.T                                  # [H, L]
+            mx = sc.max(dim=1, keepdim=True).values
+            p = torch.exp(sc - mx)
+            l = p.sum(dim=1, keepdim=True)
+            o[b] = ((p @ kv[:, :512]) / l).to(torch.float32)
+            lse[b] = (mx + torch.log(l)).squeeze(1).to(torch.float32)
+            continue
+        m = torch.full((H,), -1e30, dtype=torch.float64)
+        l = torch.zeros(H, dtype=torch.float64)
+        acc = torch.zeros(H, 512, dtype=torch.float16)
+        for base in range(0, L, tile):
+            pos = torch.arange(base, min(base + tile, L))
+            rows = resolve_rows(pos, bt[b], page, n_rows)
+            kv = torch.zeros(tile, 576, dtype=torch.float64)
+            ok = rows >= 0
+            kv[:len(pos)][ok] = flat[rows[ok]].to(torch.float64)
+            s = qs[b] @ kv.T                                  # [H, tile]
+            s[:, len(pos):] = float("-inf")
+            m_cur = torch.maximum(m, s.max(dim=1).values)
+            alpha = torch.exp(m - m_cur)
+            p = torch.where(torch.isinf(s), torch.zeros_like(s), torch.exp(s - m_cur[:, None]))
+            l = l * alpha + p.sum(dim=1)
+            m = m_cur
+            acc = (acc.to(torch.float64) * alpha[:, None]).to(torch.float16)
+            pv = p.to(torch.float16).to(torch.float64) @ kv[:, :512]
+            acc = (acc.to(torch.float64) + pv).to(torch.float16)
+        pos_l = l > 0
+        inv = torch.where(pos_l, 1.0 / torch.where(pos_l, l, torch.ones_like(l)), torch.zeros_like(l))
+        o[b] = (acc.to(torch.float64) * inv[:, None]).to(torch.float16).to(torch.float32)
+        lse[b] = torch.where(pos_l, m + torch.log(torch.where(pos_l, l, torch.ones_like(l))),
+                             torch.full_like(m, float("-inf"))).to(torch.float32)
+    return o, lse
+
+
 # ---------------------------------------------------------------------------
 # fp8_ds_mla latent-cache writer (generator side; the reference's writer
 # concat_and_cache_ds_mla is not vendored, only its 656-B layout is:

@@ -106,22 +106,24 @@ def test_empty_token_lse_convention(ops, dev, B, H, expect):
     assert torch.all(lse[3] == expect) and torch.all(rl[3] == expect)
 
 
-def test_prefill_config(ops, dev):
+@pytest.mark.parametrize("fp8", [True, False], ids=["fp8", "fp16"])
+def test_prefill_config(ops, dev, fp8):
     """B >= 256 tokens takes the 64-head prefill configuration."""
     B = 300
     seqs = [1800 + 3 * i for i in range(B)]
-    q, kv, idx, bt, seq = make(20, B, 64, 60, 64, True, 2048, seqs, shared_bt=True)
+    q, kv, idx, bt, seq = make(20, B, 64, 60, 64, fp8, 2048, seqs, shared_bt=True)
     o, lse = run(ops, dev, q, kv, idx, bt, seq)
     ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
     check(o, lse, ro, rl)
 
 
-def test_prefill_config_segments_partial_heads(ops, dev):
+@pytest.mark.parametrize("fp8", [True, False], ids=["fp8", "fp16"])
+def test_prefill_config_segments_partial_heads(ops, dev, fp8):
     """Prefill configuration with a partial second 64-head group (H = 80),
     top-k past one 2048-key segment, and invalid / out-of-range entries."""
     B = 128
     seqs = [2600 + 5 * i for i in range(B)]
-    q, kv, idx, bt, seq = make(22, B, 80, 60, 64, True, 2304, seqs, invalid_frac=0.05,
+    q, kv, idx, bt, seq = make(22, B, 80, 60, 64, fp8, 2304, seqs, invalid_frac=0.05,
                                shared_bt=True)
     o, lse = run(ops, dev, q, kv, idx, bt, seq)
     ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)

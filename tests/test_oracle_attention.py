@@ -138,3 +138,67 @@ def test_empty_token_lse_follows_reference_dispatch(B, H, expect):
     o, lse = O.sparse_mla(q, kv, idx, bt, torch.full((B,), 40, dtype=torch.int32), SCALE)
     assert torch.all(o[0] == 0) and torch.all(lse[0] == expect)
     assert torch.isfinite(lse[1:]).all() and (lse[1:] > -1e29).all()
+
+
+# ---- dense MLA decode (sm70_mla_decode) ----
+
+@pytest.mark.parametrize("fp16_acc", [False, True])
+def test_dense_single_position_closed_form(fp16_acc):
+    """seq_len = 1: o = V of position 0 (fp16 rounding of V / 1), lse = s."""
+    g = torch.Generator().manual_seed(10)
+    kv, _ = make_cache(g)
+    bt = torch.randperm(6, generator=g).to(torch.int32)[None]
+    q = torch.randn(1, 32, 576, generator=g).to(torch.float16)
+    o, lse = O.mla_decode(q, kv, bt, torch.tensor([1], dtype=torch.int32), SCALE, fp16_acc)
+    K = kv.view(-1, 576)[int(bt[0, 0]) * 16].double()
+    assert torch.allclose(o[0].double(), K[:512].expand(32, 512), atol=1e-6)
+    qs = O.scaled_q(q, SCALE)[0].double()
+    assert torch.allclose(lse[0].double(), qs @ K, atol=1e-5)
+
+
+@pytest.mark.parametrize("fp16_acc", [False, True])
+def test_dense_unresolvable_rows_are_zero_keys(fp16_acc):
+    """Every position below seq_len on a -1 block: each is a zero key with
+    score 0, so o = 0 and lse = ln seq_len (the reference's zero-row read,
+    sm70_mla_decode.cu:762-771); seq_len 0 gives o = 0, lse = -inf."""
+    g = torch.Generator().manual_seed(11)
+    kv, _ = make_cache(g)
+    bt = torch.full((2, 6), -1, dtype=torch.int32)
+    q = torch.randn(2, 32, 576, generator=g).to(torch.float16)
+    o, lse = O.mla_decode(q, kv, bt, torch.tensor([70, 0], dtype=torch.int32), SCALE, fp16_acc)
+    assert torch.all(o == 0)
+    assert torch.allclose(lse[0].double(), torch.full((32,), math.log(70.0), dtype=torch.float64),
+                          atol=1e-6)
+    assert torch.all(torch.isinf(lse[1])) and torch.all(lse[1] < 0)
+
+
+def test_dense_equals_sparse_over_all_positions():
+    """With every row resolvable, dense decode is the sparse op with idx =
+    0..seq_len-1 (the pinned sparse_mla), empty token included."""
+    g = torch.Generator().manual_seed(12)
+    kv, _ = make_cache(g, nblk=8)
+    bt = torch.stack([torch.randperm(8, generator=g)[:6] for _ in range(3)]).to(torch.int32)
+    q = torch.randn(3, 32, 576, generator=g).to(torch.float16)
+    seq = torch.tensor([96, 33, 0], dtype=torch.int32)
+    o, lse = O.mla_decode(q, kv, bt, seq, SCALE)
+    idx = torch.arange(96, dtype=torch.int32).expand(3, 96).contiguous()
+    ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE, empty_lse=float("-inf"))
+    assert torch.allclose(o, ro, atol=1e-6) and torch.equal(torch.isinf(lse), torch.isinf(rl))
+    fin = torch.isfinite(rl)
+    assert torch.allclose(lse[fin], rl[fin], atol=1e-6)
+
+
+def test_dense_fp16_accumulation_stays_near_exact():
+    """The reference's fp16 running O (restated tile by tile) differs from
+    the exact result by fp16 rounding only: within the attention tolerance,
+    and not bit-equal (the rounding is really applied)."""
+    g = torch.Generator().manual_seed(13)
+    kv, _ = make_cache(g, nblk=40, page=64)
+    bt = torch.randperm(40, generator=g).to(torch.int32)[None].repeat(2, 1)
+    q = (torch.randn(2, 32, 576, generator=g) / 4).to(torch.float16)
+    seq = torch.tensor([2500, 700], dtype=torch.int32)
+    o, lse = O.mla_decode(q, kv, bt, seq, SCALE)
+    o16, lse16 = O.mla_decode(q, kv, bt, seq, SCALE, fp16_acc=True)
+    torch.testing.assert_close(o16, o, rtol=2e-3, atol=1e-3)
+    assert (lse16 - lse).abs().max() <= 1e-4
+    assert not torch.equal(o16, o)
