@@ -17,7 +17,8 @@ GB/s); indexer prefill TFLOPS @64k"):
   and the CPU baseline (the oracle's PyTorch restatement on the host cores),
   one whole DSA decode layer step (cache writes, indexer, top-k, the two
   head projections and the attention) at the same shape, and the dense MLA
-  decode (sm70_mla_decode) at 4k / 32k / 131k context.
+  decode (sm70_mla_decode) at 4k / 32k / 131k context, and the dense varlen
+  MLA prefill attention on one causal 16k-token sequence.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L]
 Only one GPU is supported: --gpus N with N > 1 exits with a message.
@@ -176,7 +177,7 @@ def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
 
 SPARSE_PREFILL_T = 65536
 EXTRAS = ("sweep", "indexer_prefill", "sparse_prefill", "indexer_decode", "gemv", "k_store",
-          "dsa_layer", "dense_decode")
+          "dsa_layer", "dense_decode", "varlen_prefill")
 
 
 def sparse_prefill_flops(T=SPARSE_PREFILL_T, topk=2048, heads=64):
@@ -469,6 +470,35 @@ def bench_dense_decode(torch, pkg, dev):
     return out
 
 
+def bench_varlen_prefill(torch, pkg, dev, L=16384, H=64, dqk=192, dv=128):
+    """Dense varlen MLA prefill attention (the reference's _varlen_attention):
+    one causal sequence of L new tokens, H heads, qk 192 / v 128, fp16 and
+    bf16.  FLOPs count the unmasked (causal) scores only."""
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    cu = torch.tensor([0, L], dtype=torch.int32, device=dev)
+    flops = H * (L * (L + 1) / 2) * (dqk + dv) * 2
+    for dtype in (torch.float16, torch.bfloat16):
+        q = torch.randn(L, H, dqk, generator=g, device=dev).to(dtype)
+        k = torch.randn(L, H, dqk, generator=g, device=dev).to(dtype)
+        v = torch.randn(L, H, dv, generator=g, device=dev).to(dtype)
+
+        def fn():
+            pkg.mla_prefill.varlen_attention(q, k, v, cu, cu, dqk ** -0.5, True, True,
+                                             max_seqlen_q=L)
+
+        us = graph_time_per_call(torch, fn, 1, steps=5, warmup=1)
+        tf = flops / (us * 1e-6) / 1e12
+        out["fp16" if dtype == torch.float16 else "bf16"] = {
+            "ms": round(us / 1000, 3), "tflops": round(tf, 1),
+            "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)}
+        del q, k, v
+    out["workload"] = (f"one causal sequence of {L} tokens, {H} heads, qk {dqk} / v {dv}, "
+                       "causal FLOPs only")
+    return out
+
+
 def cpu_baseline(torch, d, idxs, qs, budget_s):
     """The oracle's PyTorch restatement (fp32) of the same decode layers on
     the host cores: gather -> dequant -> QK -> softmax -> PV."""
@@ -620,6 +650,10 @@ def main():
     if "dense_decode" in extras:
         line["dense_mla_decode"] = bench_dense_decode(torch, pkg, dev)
         log(f"dense mla decode: {line['dense_mla_decode']}")
+    if "varlen_prefill" in extras:
+        line["dense_varlen_prefill"] = bench_varlen_prefill(torch, pkg, dev)
+        log(f"dense varlen prefill: {line['dense_varlen_prefill']}")
+        torch.cuda.empty_cache()
     if "dsa_layer" in extras:
         line["dsa_layer_decode"] = bench_dsa_layer(torch, pkg, dev)
         log(f"dsa layer decode: {line['dsa_layer_decode']}")

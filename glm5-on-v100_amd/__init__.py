@@ -8,9 +8,9 @@ The directory name contains dashes, so it is imported through a loader that
 registers it as the module `glm5_on_v100_amd` (see __graft_entry__.py or
 tests/conftest.py).
 """
-from . import _lib, ops, _sm70_ops, _cache_ops, dsa_layer, synthetic  # noqa: F401
+from . import _lib, ops, _sm70_ops, _cache_ops, dsa_layer, mla_prefill, synthetic  # noqa: F401
 
-__all__ = ["_lib", "ops", "_sm70_ops", "_cache_ops", "dsa_layer", "synthetic",
+__all__ = ["_lib", "ops", "_sm70_ops", "_cache_ops", "dsa_layer", "mla_prefill", "synthetic",
            "load_library"]
 
 

@@ -30,6 +30,10 @@ SIGNATURES = {
     "mi355_dsa_mla_decode_workspace_size": (_c_size, [_c_int, _c_int, _c_int]),
     "mi355_dsa_mla_decode": (_c_int, [_p, _p, _p, _c_int, _c_int, _p, _c_i64, _c_int, _p, _c_int,
                                       _p, _c_f32, _p, _c_size, _p]),
+    "mi355_dsa_varlen_attention": (_c_int, [_p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int,
+                                            _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                            _c_i64, _c_i64, _c_i64, _p, _p, _c_int, _c_int,
+                                            _c_f32, _c_int, _p]),
     "mi355_dsa_head_proj": (_c_int, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _c_int, _c_int,
                                      _c_int, _c_int, _c_int, _p]),
     "mi355_dsa_concat_and_cache_mla": (_c_int, [_p, _c_int, _c_i64, _p, _c_i64, _p, _c_i64,

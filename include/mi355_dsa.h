@@ -113,6 +113,31 @@ int mi355_dsa_mla_decode(void* o, float* lse, const void* q, int B, int n_head,
                          size_t workspace_bytes, void* stream);
 
 /*
+ * Dense varlen attention (MLA prefill, multi-head form):
+ *   out[t,h,:] = softmax(scale * q[t,h,:] . k[j,h,:]) v[j,h,:]
+ * over the keys j of token t's sequence s: queries cu_seqlens_q[s] ..
+ * cu_seqlens_q[s+1]-1, keys cu_seqlens_k[s] .. cu_seqlens_k[s+1]-1 (int32
+ * device arrays of num_seqs + 1).  causal != 0: query i (0-based in its
+ * sequence of q_len) sees keys j <= i + k_len - q_len.  lse (nullable) is
+ * fp32 [n_head, total_q], natural log; a query with no key gets out = 0 and
+ * lse = -inf.  q/k/v/out are fp16 (bf16 = 0) or bf16 (bf16 = 1) with unit
+ * last-dim stride and the given element strides (multiples of 8; out: 4),
+ * q/k/v 16-byte aligned.  (d_qk, d_v) in {(192,128), (128,128), (64,64),
+ * (256,256)}.  max_q_len = the longest query run.
+ * Replaces the reference's dense MLA prefill attention, _varlen_attention
+ * (vllm/v1/attention/backends/mla/prefill/sm70_triton.py:54-187).
+ */
+int mi355_dsa_varlen_attention(void* out, float* lse, const void* q, const void* k,
+                               const void* v, int bf16, int num_seqs, int n_head, int d_qk,
+                               int d_v, int64_t q_tok_stride, int64_t q_head_stride,
+                               int64_t k_tok_stride, int64_t k_head_stride,
+                               int64_t v_tok_stride, int64_t v_head_stride,
+                               int64_t o_tok_stride, int64_t o_head_stride,
+                               const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                               int max_q_len, int total_q, float softmax_scale, int causal,
+                               void* stream);
+
+/*
  * Per-head projection of an MLA layer (fp16 in and out, fp32 accumulation):
  *   out[t,h,n]   = sum_k x[t,h,k] * wt[h,n,k]    (t < T, h < H, n < N, k < K)
  *   out[t,h,N+i] = x[t,h,K+i]                    (i < tail)

@@ -367,6 +367,44 @@ def mla_decode(q: torch.Tensor, kv_cache: torch.Tensor, bt: torch.Tensor,
     return o, lse
 
 
+def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     cu_q, cu_k, scale: float, causal: bool):
+    """Dense varlen attention as the reference's MLA prefill backend computes
+    it (vllm/v1/attention/backends/mla/prefill/sm70_triton.py:54-187), here
+    in fp64 without tiling: per sequence, s = scale * q k^T; with `causal`,
+    key j is masked for query i when j > i + (k_len - q_len) (:117-123,
+    :145-152); softmax over the unmasked keys.  A query with no key (k_len 0,
+    or every key masked) gets out = 0 and lse = -inf (:106-112, :175-185).
+    Returns out fp64 [total_q, H, Dv] and lse fp64 [H, total_q]."""
+    cu_q = [int(x) for x in cu_q]
+    cu_k = [int(x) for x in cu_k]
+    total_q, H, _ = q.shape
+    out = torch.zeros(total_q, H, v.shape[2], dtype=torch.float64)
+    lse = torch.full((H, total_q), float("-inf"), dtype=torch.float64)
+    for i in range(len(cu_q) - 1):
+        qs, qe, ks, ke = cu_q[i], cu_q[i + 1], cu_k[i], cu_k[i + 1]
+        q_len, k_len = qe - qs, ke - ks
+        if q_len == 0 or k_len == 0:
+            continue
+        qi = q[qs:qe].double().transpose(0, 1)           # [H, q_len, D]
+        ki = k[ks:ke].double().transpose(0, 1)
+        vi = v[ks:ke].double().transpose(0, 1)
+        sc = torch.matmul(qi, ki.transpose(1, 2)) * scale  # [H, q_len, k_len]
+        if causal:
+            qpos = torch.arange(q_len)[:, None] + (k_len - q_len)
+            sc = sc.masked_fill(torch.arange(k_len)[None, :] > qpos, float("-inf"))
+        m = sc.max(dim=2, keepdim=True).values
+        has = torch.isfinite(m)
+        msafe = torch.where(has, m, torch.zeros_like(m))
+        p = torch.exp(sc - msafe)
+        l = p.sum(dim=2, keepdim=True)
+        o = torch.matmul(p, vi) / torch.where(l > 0, l, torch.ones_like(l))
+        out[qs:qe] = o.transpose(0, 1)
+        lse[:, qs:qe] = torch.where(l > 0, msafe + torch.log(l),
+                                    torch.full_like(l, float("-inf"))).squeeze(2)
+    return out, lse
+
+
 # ---------------------------------------------------------------------------
 # fp8_ds_mla latent-cache writer (generator side; the reference's writer
 # concat_and_cache_ds_mla is not vendored, only its 656-B layout is:
