@@ -18,7 +18,8 @@ GB/s); indexer prefill TFLOPS @64k"):
   one whole DSA decode layer step (cache writes, indexer, top-k, the two
   head projections and the attention) at the same shape, and the dense MLA
   decode (sm70_mla_decode) at 4k / 32k / 131k context, and the dense varlen
-  MLA prefill attention on one causal 16k-token sequence.
+  MLA prefill attention on one causal 16k-token sequence, and the key-shard
+  indexer merge (tp=4, 4096 rows).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L]
 Only one GPU is supported: --gpus N with N > 1 exits with a message.
@@ -177,7 +178,7 @@ def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
 
 SPARSE_PREFILL_T = 65536
 EXTRAS = ("sweep", "indexer_prefill", "sparse_prefill", "indexer_decode", "gemv", "k_store",
-          "dsa_layer", "dense_decode", "varlen_prefill")
+          "dsa_layer", "dense_decode", "varlen_prefill", "shard_merge")
 
 
 def sparse_prefill_flops(T=SPARSE_PREFILL_T, topk=2048, heads=64):
@@ -499,6 +500,38 @@ def bench_varlen_prefill(torch, pkg, dev, L=16384, H=64, dqk=192, dv=128):
     return out
 
 
+def bench_shard_merge(torch, pkg, dev, R=4096, tp=4, K=2048):
+    """Key-shard indexer merge (sm70_indexer_shard_merge) of an all-gathered
+    payload [tp, R, 2K] as a 64k-context prefill produces it: shard s scored
+    positions [16384 s, +16384) and kept K of them.  HBM-bound, algorithmic
+    bytes = the payload read once + the [R, K] int32 output."""
+    ops = pkg._sm70_ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(12)
+    copies = 2
+    allfs = []
+    for _ in range(copies):
+        vals = torch.randn(tp, R, K, generator=g, device=dev)
+        span = 65536 // tp
+        pos = (torch.rand(tp, R, span, generator=g, device=dev).argsort(dim=2)[:, :, :K]
+               + span * torch.arange(tp, device=dev).view(tp, 1, 1)).to(torch.int32)
+        allfs.append(torch.cat([vals, pos.view(torch.float32)], dim=2).contiguous())
+        del vals, pos
+    out = torch.empty(R, K, dtype=torch.int32, device=dev)
+    e = torch.empty(0, dtype=torch.int32, device=dev)
+
+    def fn():
+        for a in allfs:
+            ops.sm70_indexer_shard_merge(out, a, e, 0, K)
+
+    us = graph_time_per_call(torch, fn, copies)
+    nbytes = tp * R * 2 * K * 4 + R * K * 4
+    gbps = nbytes / (us * 1e-6) / 1e9
+    del allfs
+    return {"us": round(us, 2), "gbps": round(gbps, 1), "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4),
+            "workload": f"tp={tp}, R={R} rows, K={K}"}
+
+
 def cpu_baseline(torch, d, idxs, qs, budget_s):
     """The oracle's PyTorch restatement (fp32) of the same decode layers on
     the host cores: gather -> dequant -> QK -> softmax -> PV."""
@@ -653,6 +686,10 @@ def main():
     if "varlen_prefill" in extras:
         line["dense_varlen_prefill"] = bench_varlen_prefill(torch, pkg, dev)
         log(f"dense varlen prefill: {line['dense_varlen_prefill']}")
+        torch.cuda.empty_cache()
+    if "shard_merge" in extras:
+        line["indexer_shard_merge"] = bench_shard_merge(torch, pkg, dev)
+        log(f"indexer shard merge: {line['indexer_shard_merge']}")
         torch.cuda.empty_cache()
     if "dsa_layer" in extras:
         line["dsa_layer_decode"] = bench_dsa_layer(torch, pkg, dev)

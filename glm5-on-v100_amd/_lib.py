@@ -34,6 +34,8 @@ SIGNATURES = {
                                             _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                             _c_i64, _c_i64, _c_i64, _p, _p, _c_int, _c_int,
                                             _c_f32, _c_int, _p]),
+    "mi355_dsa_indexer_shard_merge": (_c_int, [_p, _c_i64, _c_i64, _p, _c_int, _c_int, _c_int,
+                                               _p, _c_int, _p]),
     "mi355_dsa_head_proj": (_c_int, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p, _c_int, _c_int,
                                      _c_int, _c_int, _c_int, _p]),
     "mi355_dsa_concat_and_cache_mla": (_c_int, [_p, _c_int, _c_i64, _p, _c_i64, _p, _c_i64,

@@ -53,6 +53,15 @@ def sm70_mla_decode(o: torch.Tensor, lse: torch.Tensor, q: torch.Tensor,
     _op("sm70_mla_decode")(o, lse, q, kv_cache, block_table, seq_lens, scale)
 
 
+def sm70_indexer_shard_merge(out: torch.Tensor, allf: torch.Tensor, dst_rows: torch.Tensor,
+                             dst_base: int, topk: int) -> None:
+    """Exact top-K merge of the all-gathered key-shard candidates allf
+    [tp, R, 2K] into out rows dst_base + r (or dst_rows[r] when dst_base < 0),
+    positions ascending, -1 for -inf selections (the TP prefill indexer's
+    fused merge, reference/sparse_attn_indexer.py:985-1006)."""
+    _op("sm70_indexer_shard_merge")(out, allf, dst_rows, dst_base, topk)
+
+
 def sm70_sparse_mla_decode(o: torch.Tensor, lse: torch.Tensor, q: torch.Tensor,
                            kv_cache: torch.Tensor, idx: torch.Tensor,
                            block_table: torch.Tensor, seq_lens: torch.Tensor,

@@ -27,6 +27,9 @@ SCHEMAS = {
     "sm70_mla_decode": (
         "sm70_mla_decode(Tensor! o, Tensor! lse, Tensor q, Tensor kv_cache, "
         "Tensor block_table, Tensor seq_lens, float scale) -> ()"),
+    "sm70_indexer_shard_merge": (
+        "sm70_indexer_shard_merge(Tensor! out, Tensor allf, Tensor dst_rows, "
+        "int dst_base, int topk) -> ()"),
     "sm70_sparse_mla_decode": (
         "sm70_sparse_mla_decode(Tensor! o, Tensor! lse, Tensor q, "
         "Tensor kv_cache, Tensor idx, Tensor block_table, Tensor seq_lens, "
@@ -120,6 +123,29 @@ def mla_decode_impl(o, lse, q, kv_cache, block_table, seq_lens, scale):
         _lib.call("mi355_dsa_mla_decode", o.data_ptr(), lse.data_ptr(), q.data_ptr(), B, H,
                   kv_cache.data_ptr(), n_rows, page, block_table.data_ptr(), max_blocks,
                   seq_lens.data_ptr(), float(scale), ws.data_ptr(), ws_bytes, _stream(q))
+
+
+def indexer_shard_merge_impl(out, allf, dst_rows, dst_base, topk):
+    """sm70_mla_decode.cu:2411-2436 checks (K = 2048, tp in [2, 4])."""
+    _check(allf.is_cuda and allf.is_contiguous() and allf.dim() == 3,
+           "allf must be contiguous [tp, R, 2K] cuda")
+    _check(allf.dtype == torch.float32, "allf must be fp32")
+    _check(out.dtype == torch.int32 and out.dim() == 2, "out must be int32 [rows, >= K]")
+    tp, R = allf.size(0), allf.size(1)
+    _check(topk == 2048 and allf.size(2) == 2 * topk, "shard merge kernel supports K=2048 only")
+    _check(2 <= tp <= 4, "shard merge kernel supports tp in [2,4]")
+    _check(dst_base >= 0 or dst_rows.numel() == R, "need dst_rows when dst_base < 0")
+    _check((tp * topk) % 512 == 0, "ncand must be a multiple of 512")
+    _check(out.is_cuda and out.stride(1) == 1, "out must be a row-major cuda tensor")
+    if R == 0:
+        return
+    dr = None
+    if dst_base < 0:
+        dr = dst_rows.to(torch.int32).contiguous()
+    with torch.cuda.device(allf.device):
+        _lib.call("mi355_dsa_indexer_shard_merge", out.data_ptr(), out.stride(0), out.size(0),
+                  allf.data_ptr(), tp, R, topk, dr.data_ptr() if dr is not None else None,
+                  int(dst_base), _stream(allf))
 
 
 def sparse_mla_decode_impl(o, lse, q, kv_cache, idx, block_table, seq_lens, scale):
@@ -416,6 +442,7 @@ def attn_fp8_quantize(weight):
 
 
 IMPLS = {
+    "sm70_indexer_shard_merge": indexer_shard_merge_impl,
     "sm70_mla_decode": mla_decode_impl,
     "sm70_sparse_mla_decode": sparse_mla_decode_impl,
     "sm70_indexer_logits": indexer_logits_impl,

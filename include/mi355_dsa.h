@@ -113,6 +113,24 @@ int mi355_dsa_mla_decode(void* o, float* lse, const void* q, int B, int n_head,
                          size_t workspace_bytes, void* stream);
 
 /*
+ * Exact top-K merge of key-sharded indexer candidates.  allf fp32
+ * [tp, R, 2K]: per shard s and row r, K scores then K positions (int32
+ * bits).  Row r's output is the K candidates of largest
+ * (mono(score) << 32) | (tp*K - 1 - (s*K + c)) -- by score, ties to the lower
+ * column -- as positions (-1 for a selection at or below mono(-inf)), sorted
+ * ascending, written to out row dst_base + r (dst_base >= 0) or dst_rows[r]
+ * (int32 device array; rows outside [0, out_rows) are skipped).  out is int32
+ * with row stride out_stride >= K.  K a power of two <= 2048; tp*K a multiple
+ * of 512, at most 8192.
+ * Replaces sm70_indexer_shard_merge (csrc/attention/sm70_mla_decode.cu:
+ * 2055-2182, host :2411-2436); the all-gather that produces allf is the
+ * caller's.
+ */
+int mi355_dsa_indexer_shard_merge(int32_t* out, int64_t out_stride, int64_t out_rows,
+                                  const float* allf, int tp, int R, int K,
+                                  const int32_t* dst_rows, int dst_base, void* stream);
+
+/*
  * Dense varlen attention (MLA prefill, multi-head form):
  *   out[t,h,:] = softmax(scale * q[t,h,:] . k[j,h,:]) v[j,h,:]
  * over the keys j of token t's sequence s: queries cu_seqlens_q[s] ..

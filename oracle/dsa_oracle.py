@@ -405,6 +405,31 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return out, lse
 
 
+def shard_merge_rows(allf: torch.Tensor, K: int) -> torch.Tensor:
+    """Exact top-K merge of key-shard candidates, the reference's fused merge
+    (sm70_mla_decode.cu:2055-2182): allf fp32 [tp, R, 2K] (K scores, then K
+    positions as int32 bits, per shard and row).  Per row, the K largest
+    64-bit keys (mono(score) << 32) | (tp*K - 1 - col), col = s*K + c
+    (:2090-2100); a selection with mono <= mono(-inf) = 0x007FFFFF gives -1
+    (:2145-2152); positions sorted ascending (:2156-2173).  Returns int32
+    [R, K]."""
+    tp, R, _ = allf.shape
+    ncand = tp * K
+    vals = allf[:, :, :K].permute(1, 0, 2).reshape(R, ncand).contiguous()
+    pos = allf[:, :, K:].permute(1, 0, 2).reshape(R, ncand).contiguous().view(torch.int32)
+    u = vals.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    mono = torch.where(u >= 0x80000000, (~u) & 0xFFFFFFFF, u | 0x80000000)
+    col = torch.arange(ncand, dtype=torch.int64)
+    key = (mono << 32) | (ncand - 1 - col)
+    # keys are below 2^64; compare as int64 after flipping the sign bit
+    skey = key ^ (-(2 ** 63))
+    top = torch.argsort(skey, dim=1, descending=True)[:, :K]
+    sel_mono = mono.gather(1, top)
+    sel_pos = pos.to(torch.int64).gather(1, top)
+    sel = torch.where(sel_mono > 0x007FFFFF, sel_pos, torch.full_like(sel_pos, -1))
+    return sel.sort(dim=1).values.to(torch.int32)
+
+
 # ---------------------------------------------------------------------------
 # fp8_ds_mla latent-cache writer (generator side; the reference's writer
 # concat_and_cache_ds_mla is not vendored, only its 656-B layout is:

@@ -22,7 +22,8 @@ def test_header_declares_the_op_surface():
     names = declared_functions()
     for op in ["indexer_k_store", "indexer_logits", "indexer_logits_packed", "decode_topk",
                "persistent_topk", "sparse_mla_decode", "attn_fp8_gemv", "attn_fp8_dequant",
-               "selfcheck", "last_error", "concat_and_cache_mla", "head_proj", "mla_decode", "varlen_attention"]:
+               "selfcheck", "last_error", "concat_and_cache_mla", "head_proj", "mla_decode", "varlen_attention",
+               "indexer_shard_merge"]:
         assert f"mi355_dsa_{op}" in names
 
 
