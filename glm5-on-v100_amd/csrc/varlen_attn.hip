@@ -40,7 +40,6 @@ typedef __attribute__((address_space(3))) s16x4v lds_s16x4v;
 
 constexpr int kVaWaves = 4;
 constexpr int kVaThreads = 64 * kVaWaves;
-constexpr int kVaKT = 64;  // keys per tile
 
 __device__ const __align__(16) uint16_t kVaZero[8] = {};
 
@@ -79,12 +78,12 @@ __device__ __forceinline__ float from16(uint16_t x) {
   else return (float)__builtin_bit_cast(f16, x);
 }
 
-template <int DQK, int DV>
+template <int DQK, int DV, int KT>
 struct VaShape {
   static constexpr int PK = DQK / 8 + 1;  // K row pitch in 16-B pieces (one pad)
   static constexpr int PV = DV / 8 + 1;
-  static constexpr int RK = (kVaKT * PK + kVaThreads - 1) / kVaThreads;  // DMA rounds
-  static constexpr int RV = (kVaKT * PV + kVaThreads - 1) / kVaThreads;
+  static constexpr int RK = (KT * PK + kVaThreads - 1) / kVaThreads;  // DMA rounds
+  static constexpr int RV = (KT * PV + kVaThreads - 1) / kVaThreads;
   static constexpr int KBYTES = RK * kVaThreads * 16;
   static constexpr int VBYTES = RV * kVaThreads * 16;
   static constexpr int STAGE = KBYTES + VBYTES;
@@ -95,9 +94,11 @@ __device__ __forceinline__ void va_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <bool BF16, int DQK, int DV, int QB>
-__global__ void __launch_bounds__(kVaThreads) varlen_attn_kernel(VaArgs a) {
-  using Sh = VaShape<DQK, DV>;
+template <bool BF16, int DQK, int DV, int QB, int KT, int MINB>
+__global__ void __launch_bounds__(kVaThreads, MINB) varlen_attn_kernel(VaArgs a) {
+  using Sh = VaShape<DQK, DV, KT>;
+  constexpr int NKB = KT / 16;  // 16-key blocks per tile
+  constexpr int NKH = KT / 32;  // 32-key PV steps per tile
   constexpr int QROWS = 16 * QB * kVaWaves;
   constexpr int NS = DQK / 32;  // QK k-steps
   constexpr int NDT = DV / 16;  // O^T dim tiles
@@ -114,7 +115,7 @@ __global__ void __launch_bounds__(kVaThreads) varlen_attn_kernel(VaArgs a) {
   if (q0 >= q_len) return;
   const int offset = a.causal ? k_len - q_len : 0;
   const int kend = a.causal ? max(0, min(k_len, q0 + QROWS + offset)) : k_len;
-  const int n_kt = (kend + kVaKT - 1) / kVaKT;
+  const int n_kt = (kend + KT - 1) / KT;
 
   // ---- Q fragments (B operand): row q0 + 16(QB w + qb) + c, dims 32 s + 8 g ----
   u32x4 qf[QB][NS];
@@ -130,12 +131,12 @@ __global__ void __launch_bounds__(kVaThreads) varlen_attn_kernel(VaArgs a) {
 
   auto issue_tile = [&](int kt) {
     unsigned char* st = smem_raw + (kt & 1) * Sh::STAGE;
-    const int k0 = kt * kVaKT;
+    const int k0 = kt * KT;
 #pragma unroll
     for (int u = 0; u < Sh::RK; u++) {
       const int qq = kVaThreads * u + 64 * w + lane;
       const int r = qq / Sh::PK, ch = qq - r * Sh::PK;
-      const bool ok = r < kVaKT && ch < DQK / 8 && k0 + r < kend;
+      const bool ok = r < KT && ch < DQK / 8 && k0 + r < kend;
       const uint16_t* src = ok ? a.k + (int64_t)(ks + k0 + r) * a.k_st + (int64_t)h * a.k_sh + 8 * ch
                                : kVaZero;
       dma16(src, st + 16 * (kVaThreads * u + 64 * w));
@@ -144,7 +145,7 @@ __global__ void __launch_bounds__(kVaThreads) varlen_attn_kernel(VaArgs a) {
     for (int u = 0; u < Sh::RV; u++) {
       const int qq = kVaThreads * u + 64 * w + lane;
       const int r = qq / Sh::PV, ch = qq - r * Sh::PV;
-      const bool ok = r < kVaKT && ch < DV / 8 && k0 + r < kend;
+      const bool ok = r < KT && ch < DV / 8 && k0 + r < kend;
       const uint16_t* src = ok ? a.v + (int64_t)(ks + k0 + r) * a.v_st + (int64_t)h * a.v_sh + 8 * ch
                                : kVaZero;
       dma16(src, st + Sh::KBYTES + 16 * (kVaThreads * u + 64 * w));
@@ -174,18 +175,18 @@ __global__ void __launch_bounds__(kVaThreads) varlen_attn_kernel(VaArgs a) {
     lds_barrier();  // tile kt landed for every wave
     const unsigned char* kst = smem_raw + (kt & 1) * Sh::STAGE;
     const unsigned char* vst = kst + Sh::KBYTES;
-    const int k0 = kt * kVaKT;
+    const int k0 = kt * KT;
 
     // ---- S^T blocks: keys 16 kb + 4 g + r, query column c of block qb ----
-    f32x4 sacc[4][QB];
+    f32x4 sacc[NKB][QB];
 #pragma unroll
-    for (int kb = 0; kb < 4; kb++)
+    for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
       for (int qb = 0; qb < QB; qb++) sacc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NS; s++) {
 #pragma unroll
-      for (int kb = 0; kb < 4; kb++) {
+      for (int kb = 0; kb < NKB; kb++) {
         const u32x4 kf = *reinterpret_cast<const u32x4*>(kst + (16 * kb + c) * Sh::PK * 16 +
                                                          64 * s + 16 * g);
 #pragma unroll
@@ -194,14 +195,14 @@ __global__ void __launch_bounds__(kVaThreads) varlen_attn_kernel(VaArgs a) {
     }
 
     // ---- masks and online softmax per query column ----
-    u32x4 pb[2][QB], pl[2][QB];  // P^T operands: key halves kh (hi and, for bf16, lo parts)
+    u32x4 pb[NKH][QB], pl[NKH][QB];  // P^T operands per 32 keys (hi and, for bf16, lo parts)
 #pragma unroll
     for (int qb = 0; qb < QB; qb++) {
       const int i = q0 + 16 * (QB * w + qb) + c;  // query row of this column
       const int jmax = a.causal ? min(kend, i + offset + 1) : kend;  // keys < jmax are valid
       float mt = -1e30f;
 #pragma unroll
-      for (int kb = 0; kb < 4; kb++)
+      for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const int j = k0 + 16 * kb + 4 * g + r;
@@ -215,9 +216,9 @@ __global__ void __launch_bounds__(kVaThreads) varlen_attn_kernel(VaArgs a) {
       m_run[qb] = m_new;
       const float mb = m_new * a.scale_log2;
       float ls = 0.f;
-      float pv[4][4];
+      float pv[NKB][4];
 #pragma unroll
-      for (int kb = 0; kb < 4; kb++)
+      for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const float sv = sacc[kb][qb][r];
@@ -229,7 +230,7 @@ __global__ void __launch_bounds__(kVaThreads) varlen_attn_kernel(VaArgs a) {
 #pragma unroll
       for (int t = 0; t < NDT; t++) oacc[t][qb] *= alpha;
 #pragma unroll
-      for (int kh = 0; kh < 2; kh++) {
+      for (int kh = 0; kh < NKH; kh++) {
         uint16_t hi[8], lo[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -250,7 +251,7 @@ __global__ void __launch_bounds__(kVaThreads) varlen_attn_kernel(VaArgs a) {
     // (+16 for the second read), dims 16 t + 4 (i % 4) .. +3
     const unsigned char* vsrc = vst + (4 * g + (c >> 2)) * Sh::PV * 16 + 8 * (c & 3);
 #pragma unroll
-    for (int kh = 0; kh < 2; kh++) {
+    for (int kh = 0; kh < NKH; kh++) {
 #pragma unroll
       for (int t = 0; t < NDT; t++) {
         const s16x4v v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -294,11 +295,11 @@ __global__ void __launch_bounds__(kVaThreads) varlen_attn_kernel(VaArgs a) {
   }
 }
 
-template <bool BF16, int DQK, int DV, int QB>
+template <bool BF16, int DQK, int DV, int QB, int KT, int MINB>
 int launch_va(const VaArgs& a0, int num_seqs, int max_q_len, hipStream_t st) {
-  using Sh = VaShape<DQK, DV>;
+  using Sh = VaShape<DQK, DV, KT>;
   constexpr int QROWS = 16 * QB * kVaWaves;
-  auto kern = varlen_attn_kernel<BF16, DQK, DV, QB>;
+  auto kern = varlen_attn_kernel<BF16, DQK, DV, QB, KT, MINB>;
   static bool attr = false;
   if (!attr) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -317,10 +318,14 @@ int launch_va(const VaArgs& a0, int num_seqs, int max_q_len, hipStream_t st) {
 
 template <bool BF16>
 int dispatch_va(const VaArgs& a, int d_qk, int d_v, int num_seqs, int max_q_len, hipStream_t st) {
-  if (d_qk == 192 && d_v == 128) return launch_va<BF16, 192, 128, 2>(a, num_seqs, max_q_len, st);
-  if (d_qk == 128 && d_v == 128) return launch_va<BF16, 128, 128, 2>(a, num_seqs, max_q_len, st);
-  if (d_qk == 64 && d_v == 64) return launch_va<BF16, 64, 64, 2>(a, num_seqs, max_q_len, st);
-  if (d_qk == 256 && d_v == 256) return launch_va<BF16, 256, 256, 1>(a, num_seqs, max_q_len, st);
+#ifndef VA_KT
+#define VA_KT 64
+#define VA_MINB 1
+#endif
+  if (d_qk == 192 && d_v == 128) return launch_va<BF16, 192, 128, 2, VA_KT, VA_MINB>(a, num_seqs, max_q_len, st);
+  if (d_qk == 128 && d_v == 128) return launch_va<BF16, 128, 128, 2, VA_KT, VA_MINB>(a, num_seqs, max_q_len, st);
+  if (d_qk == 64 && d_v == 64) return launch_va<BF16, 64, 64, 2, 64, 1>(a, num_seqs, max_q_len, st);
+  if (d_qk == 256 && d_v == 256) return launch_va<BF16, 256, 256, 1, 64, 1>(a, num_seqs, max_q_len, st);
   return set_error(MI355_DSA_EINVAL,
                    "varlen_attention: head dims (%d, %d) not built; supported (qk, v): "
                    "(192, 128), (128, 128), (64, 64), (256, 256)", d_qk, d_v);
