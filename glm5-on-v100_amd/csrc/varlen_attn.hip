@@ -11,10 +11,10 @@
 // sm70_triton.py:54-187 (_varlen_attention) computes per sequence in fp32.
 //
 // Workgroup = (query tile of 64 QB rows, sequence, head), 4 waves; wave w
-// owns query rows [16 QB w, +16 QB).  Key tiles of 64 keys stream through
+// owns query rows [16 QB w, +16 QB).  Key tiles of KT keys stream through
 // two LDS stages by LDS-DMA (K and V rows at padded pitches, so the 16 rows
 // of an MFMA operand spread over the banks), the next tile in flight while
-// the current one is used.  Per tile and wave:
+// the current one is used; two workgroups share a CU.  Per tile and wave:
 //   * S^T = K Q^T (v_mfma_f32_16x16x32): keys are the A operand read from
 //     LDS, the wave's queries the B operand resident in registers;
 //   * online softmax per query column in exp2 with the scale folded in; the
@@ -318,14 +318,13 @@ int launch_va(const VaArgs& a0, int num_seqs, int max_q_len, hipStream_t st) {
 
 template <bool BF16>
 int dispatch_va(const VaArgs& a, int d_qk, int d_v, int num_seqs, int max_q_len, hipStream_t st) {
-#ifndef VA_KT
-#define VA_KT 64
-#define VA_MINB 1
-#endif
-  if (d_qk == 192 && d_v == 128) return launch_va<BF16, 192, 128, 2, VA_KT, VA_MINB>(a, num_seqs, max_q_len, st);
-  if (d_qk == 128 && d_v == 128) return launch_va<BF16, 128, 128, 2, VA_KT, VA_MINB>(a, num_seqs, max_q_len, st);
-  if (d_qk == 64 && d_v == 64) return launch_va<BF16, 64, 64, 2, 64, 1>(a, num_seqs, max_q_len, st);
-  if (d_qk == 256 && d_v == 256) return launch_va<BF16, 256, 256, 1, 64, 1>(a, num_seqs, max_q_len, st);
+  // 32-key tiles and two workgroups per CU: two waves per SIMD, so one
+  // wave's softmax overlaps the other's MFMAs (1.7x the 64-key tile at one
+  // wave per SIMD on the (192, 128) causal prefill)
+  if (d_qk == 192 && d_v == 128) return launch_va<BF16, 192, 128, 2, 32, 2>(a, num_seqs, max_q_len, st);
+  if (d_qk == 128 && d_v == 128) return launch_va<BF16, 128, 128, 2, 32, 2>(a, num_seqs, max_q_len, st);
+  if (d_qk == 64 && d_v == 64) return launch_va<BF16, 64, 64, 2, 32, 2>(a, num_seqs, max_q_len, st);
+  if (d_qk == 256 && d_v == 256) return launch_va<BF16, 256, 256, 1, 32, 2>(a, num_seqs, max_q_len, st);
   return set_error(MI355_DSA_EINVAL,
                    "varlen_attention: head dims (%d, %d) not built; supported (qk, v): "
                    "(192, 128), (128, 128), (64, 64), (256, 256)", d_qk, d_v);
