@@ -38,6 +38,14 @@ METRIC = ("sparse MLA decode µs/layer @180k ctx (HBM GB/s); "
           "indexer prefill TFLOPS @64k")
 HBM_PEAK_GBPS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
+# The reference's own published kernel figures (NVIDIA V100, other shapes;
+# reference README.md:42-44, sm70_mla_decode.cu:483-484 and :1805-1806,
+# sm70_attn_fp8.cu:10-12), quoted beside the matching extra records.
+V100_PUBLISHED = {
+    "indexer_prefill_tflops": 44.0,   # packed-Q logits, key spans 8k-49k, B=128
+    "sparse_prefill_tflops": 15.73,   # warp-specialised fp8 prefill, B=1024, ctx 48k
+    "fp8_gemv_m1_gbps": 630.0,        # weight-only GEMV, M=1
+}
 # algorithmic bytes of one C3 decode layer at B=4 (gathered 656-B rows,
 # q, o, lse, idx and the block-table entries read)
 DECODE_BYTES = 5_997_568
@@ -178,7 +186,7 @@ def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
 
 SPARSE_PREFILL_T = 65536
 EXTRAS = ("sweep", "indexer_prefill", "sparse_prefill", "indexer_decode", "gemv", "k_store",
-          "dsa_layer", "dense_decode", "varlen_prefill", "shard_merge")
+          "dsa_layer", "dense_decode", "varlen_prefill", "shard_merge", "c1")
 
 
 def sparse_prefill_flops(T=SPARSE_PREFILL_T, topk=2048, heads=64):
@@ -532,6 +540,66 @@ def bench_shard_merge(torch, pkg, dev, R=4096, tp=4, K=2048):
             "workload": f"tp={tp}, R={R} rows, K={K}"}
 
 
+def bench_c1(torch, pkg, dev, cpu_seconds=5.0, copies=16):
+    """Config C1, the reference's CPU-runnable case, as one pipeline: indexer
+    logits (with the top-k histogram) -> decode top-2048 -> sparse MLA decode,
+    B=1, 64 heads, 4096-token context, fp16 latent and indexer-K caches
+    (page 64, random block table), on the GPU (`copies` pipelines with their
+    own inputs per graph) and, beside it, the oracle's fp32 PyTorch
+    restatement of the same pipeline on the host cores."""
+    sys.path.insert(0, ROOT)
+    from oracle import dsa_oracle as O
+
+    ops = pkg._sm70_ops
+    ctx, page, H = 4096, 64, 64
+    nblk = ctx // page
+    g = torch.Generator()
+    g.manual_seed(1)
+    ins = []
+    for _ in range(copies):
+        ins.append(dict(
+            q=(torch.randn(1, H, 576, generator=g) / 24.0).to(torch.float16),
+            kv=(torch.randn(nblk, page, 576, generator=g) / 24.0).to(torch.float16),
+            iq=torch.randn(1, 32, 128, generator=g).to(torch.float16),
+            ik=torch.randn(nblk, page, 128, generator=g).to(torch.float16),
+            w=(torch.randn(1, 32, generator=g) / 32 ** 0.5).to(torch.float16),
+            bt=torch.randperm(nblk, generator=g).to(torch.int32)[None].contiguous(),
+            seq=torch.tensor([ctx], dtype=torch.int32)))
+    scale = 576 ** -0.5
+    gins = [{k: v.to(dev) for k, v in d.items()} for d in ins]
+    score = torch.empty(1, ctx, device=dev)
+    hist = torch.zeros(1, 4096, dtype=torch.int32, device=dev)
+    idx = torch.empty(1, 2048, dtype=torch.int32, device=dev)
+    o = torch.empty(1, H, 512, dtype=torch.float16, device=dev)
+    lse = torch.empty(1, H, device=dev)
+
+    def fn():
+        for d in gins:
+            hist.zero_()
+            ops.sm70_indexer_logits(score, d["iq"], d["ik"], d["w"], d["bt"], d["seq"], hist)
+            ops.sm70_decode_topk(idx, score, d["seq"], hist, 2048)
+            ops.sm70_sparse_mla_decode(o, lse, d["q"], d["kv"], idx, d["bt"], d["seq"], scale)
+
+    us = graph_time_per_call(torch, fn, copies)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        d = ins[n % copies]
+        sc, _ = O.indexer_logits(d["iq"], d["ik"], d["w"], d["bt"], d["seq"], ctx,
+                                 dtype=torch.float32)
+        ix = O.topk_rows(sc, d["seq"], 2048)
+        O.sparse_mla(d["q"], d["kv"], ix, d["bt"], d["seq"], scale, dtype=torch.float32)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= cpu_seconds or n >= 50:
+            break
+    cpu_us = el / n * 1e6
+    return {"gpu_us": round(us, 2), "cpu_us": round(cpu_us, 1), "cpu_threads": torch.get_num_threads(),
+            "cpu_pipelines": n, "gpu_over_cpu": round(cpu_us / us, 1),
+            "workload": ("C1: B=1, 64 heads, ctx 4096, topk 2048, fp16 caches; indexer logits + "
+                         "decode top-k + sparse MLA decode per pipeline; CPU = the oracle's fp32 "
+                         "restatement of the same pipeline")}
+
+
 def cpu_baseline(torch, d, idxs, qs, budget_s):
     """The oracle's PyTorch restatement (fp32) of the same decode layers on
     the host cores: gather -> dequant -> QK -> softmax -> PV."""
@@ -647,6 +715,7 @@ def main():
             "frac_fp16_peak": round(ptf / FP16_PEAK_TFLOPS, 4),
             "workload": ("65536-token causal prefill, indexer 32 heads x 128, fp16 "
                          "K cache, 128-row sub-chunks, causal-triangle FLOPs only"),
+            "reference_v100_published_tflops": V100_PUBLISHED["indexer_prefill_tflops"],
         }
         log(f"indexer prefill: {ptf:.1f} TFLOPS ({pms:.2f} ms)")
         torch.cuda.empty_cache()
@@ -667,6 +736,8 @@ def main():
         for fp8 in (True, False):
             key = "sparse_prefill_fp8" if fp8 else "sparse_prefill_fp16"
             line[key] = bench_sparse_prefill(torch, pkg, dev, fp8=fp8)
+            if fp8:
+                line[key]["reference_v100_published_tflops"] = V100_PUBLISHED["sparse_prefill_tflops"]
             log(f"sparse prefill ({key}): {line[key]['tflops']} TFLOPS ({line[key]['ms']} ms)")
             torch.cuda.empty_cache()
     if "indexer_decode" in extras:
@@ -675,6 +746,7 @@ def main():
         torch.cuda.empty_cache()
     if "gemv" in extras:
         line["fp8_gemv"] = bench_gemv(torch, pkg, dev)
+        line["fp8_gemv"]["reference_v100_published_m1_gbps"] = V100_PUBLISHED["fp8_gemv_m1_gbps"]
         log(f"fp8 gemv: {line['fp8_gemv']}")
     if "k_store" in extras:
         line["k_store"] = bench_k_store(torch, pkg, dev)
@@ -691,6 +763,9 @@ def main():
         line["indexer_shard_merge"] = bench_shard_merge(torch, pkg, dev)
         log(f"indexer shard merge: {line['indexer_shard_merge']}")
         torch.cuda.empty_cache()
+    if "c1" in extras:
+        line["c1_pipeline"] = bench_c1(torch, pkg, dev)
+        log(f"C1 pipeline: {line['c1_pipeline']}")
     if "dsa_layer" in extras:
         line["dsa_layer_decode"] = bench_dsa_layer(torch, pkg, dev)
         log(f"dsa layer decode: {line['dsa_layer_decode']}")
