@@ -251,12 +251,18 @@ constexpr int kPkCUs = 256;                // workgroups of one full round (one 
 
 __device__ const __align__(16) f16 kIdxZeroPiece[8] = {};  // source of unmapped key rows
 
-struct PkSmem {
-  f16 q[kPkRing][kPkSlot];
-  float w[kIdxHeads][kPkMaxQT];
-  int32_t sl[kPkMaxQT];
+// LDS of a workgroup whose tiles hold at most QTMAX queries: the Q ring
+// (one head of QTMAX queries per slot), the head weights, the causal lengths
+// (64 entries: wave 0 writes one per lane).
+template <int QTMAX>
+struct PkSmemT {
+  f16 q[kPkRing][QTMAX * kIdxHeadDim];
+  float w[kIdxHeads][QTMAX];
+  int32_t sl[64];
   int maxsl;
 };
+using PkSmem = PkSmemT<kPkMaxQT>;
+static_assert(kPkMaxQT * kIdxHeadDim == kPkSlot, "ring slot = one head of a full tile");
 
 // relu in one instruction (v_med3_f32 clamp to [0, FLT_MAX]; fmaxf would
 // first canonicalise its input under IEEE mode)
@@ -286,11 +292,21 @@ struct PkArgs {
   int n_full;  // workgroups that take a whole tile
 };
 
-// One workgroup tile: queries [q_base, q_base + 32 QB) x keys [p_base, +256).
-template <bool KFP8, int QB>
-__device__ __forceinline__ void pk_tile(const PkArgs& a, PkSmem& sh, int q_base, int p_base) {
-  constexpr int QT = 32 * QB;                          // queries of the tile
-  constexpr int QROUNDS = QT * 256 / 16 / kPkThreads;  // LDS-DMA ops per thread per head
+// One workgroup tile of NW waves: queries [q_base, q_base + QT) x keys
+// [p_base, +256), QT = 16 QB NW / 4 (wave w: keys 64 (w & 3), query blocks
+// QB (w >> 2) .. +QB).
+template <bool KFP8, int QB, int NW, typename SM>
+__device__ __forceinline__ void pk_tile(const PkArgs& a, SM& sh, int q_base, int p_base) {
+  constexpr int NT = 64 * NW;
+  constexpr int QT = 16 * QB * (NW / 4);          // queries of the tile
+  constexpr int QROUNDS = QT * 256 / 16 / NT;     // LDS-DMA ops per thread per head
+  constexpr int SLOT = sizeof(sh.q[0]) / sizeof(f16);
+  // fp16 key rows (64 KB) are staged in ring slots KSLOT0 .. : slots 2..5 of
+  // 16 KB slots (slots 0, 1 stay free for the first head pair), or the whole
+  // ring of 8 KB slots
+  constexpr int KSLOT0 = SLOT * 2 >= 16384 ? 2 : 0;
+  static_assert(QT * kIdxHeadDim <= SLOT, "ring slot too small for the tile");
+  static_assert((kPkRing - KSLOT0) * SLOT * 2 >= kPkKT * kIdxHeadDim * 2, "keys do not fit the ring");
   const f16* __restrict__ Qp = a.Qp;
   const int B = a.B, max_kv = a.max_kv, page_shift = a.page_shift, max_blocks = a.max_blocks;
   const int n_qt = (B + 15) >> 4;
@@ -309,14 +325,14 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, PkSmem& sh, int q_base,
   // of global memory.  Round u of a head moves query tiles qt0 + 2u and
   // qt0 + 2u + 1.
   const int qt0 = q_base >> 4;
-  const bool qfull = qt0 + 2 * QB <= n_qt;
+  const bool qfull = qt0 + QT / 16 <= n_qt;
   auto issue_q_round = [&](int h, int u) {
-    const int i = threadIdx.x + u * kPkThreads;  // LDS 16-byte unit
+    const int i = threadIdx.x + u * NT;  // LDS 16-byte unit
     const int qt = qt0 + (i >> 8);               // 256 units per tile
     const int st = (i >> 6) & 3, gg = (i >> 4) & 3, cc = i & 15;
     const int piece = (2 * st + (gg >> 1)) * 32 + cc * 2 + (gg & 1);
     const int64_t src = ((int64_t)h * n_qt + ((qfull || qt < n_qt) ? qt : 0)) * 2048 + piece * 8;
-    dma16(Qp + src, &sh.q[h % kPkRing][(u * kPkThreads + 64 * wave) * 8]);
+    dma16(Qp + src, &sh.q[h % kPkRing][(u * NT + 64 * wave) * 8]);
   };
   auto issue_q = [&](int h) {
 #pragma unroll
@@ -337,12 +353,12 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, PkSmem& sh, int q_base,
   const int qb0 = QB * half;                           // its first query block
   const int32_t* bt_row = a.block_table + (int64_t)q_base * max_blocks;
   const int page = 1 << page_shift;
-  constexpr int kKRounds = kPkKT * kIdxHeadDim * 2 / 16 / kPkThreads;  // 8
+  constexpr int kKRounds = kPkKT * kIdxHeadDim * 2 / 16 / NT;  // 8
   int32_t kbt[KFP8 ? 4 : kKRounds];
   if constexpr (!KFP8) {
 #pragma unroll
     for (int u = 0; u < kKRounds; u++) {
-      const int p = p_base + ((threadIdx.x + u * kPkThreads) >> 4);
+      const int p = p_base + ((threadIdx.x + u * NT) >> 4);
       const int pg = p >> page_shift;
       kbt[u] = (p < max_kv && pg < max_blocks) ? bt_row[pg] : -1;
     }
@@ -360,22 +376,22 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, PkSmem& sh, int q_base,
     const int q = q_base + threadIdx.x;
     sl_v = (q < B) ? a.seq_lens[q] : 0;
   }
-  constexpr int WPT = kIdxHeads * QT / kPkThreads;
+  constexpr int WPT = kIdxHeads * QT / NT;
   float wv[WPT];
 #pragma unroll
   for (int u = 0; u < WPT; u++) {
-    const int i = threadIdx.x + u * kPkThreads;
+    const int i = threadIdx.x + u * NT;
     const int h = i / QT, q = q_base + i % QT;
     wv[u] = (q < B) ? (float)a.W[(int64_t)q * kIdxHeads + h] : 0.f;
   }
   // A operands: this wave's keys (4 blocks of 16), dims 32s + 8g .. +8 for
   // the 4 x32 steps.
   f16x8 ka[4][4];
-  f16* const kl = sh.q[2];  // fp16 key rows, slots 2..5
+  f16* const kl = sh.q[KSLOT0];  // fp16 key rows
   if constexpr (!KFP8) {
 #pragma unroll
     for (int u = 0; u < kKRounds; u++) {
-      const int i = threadIdx.x + u * kPkThreads;  // LDS 16-byte unit
+      const int i = threadIdx.x + u * NT;  // LDS 16-byte unit
       const int key = i >> 4;
       const int p = p_base + key;
       const int64_t r = ((int64_t)kbt[u] << page_shift) + (p & (page - 1));
@@ -383,10 +399,12 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, PkSmem& sh, int q_base,
                            ? reinterpret_cast<const f16*>(a.Kv) + r * kIdxHeadDim +
                                  (((i & 15) ^ (key & 15)) << 3)
                            : kIdxZeroPiece;
-      dma16(src, &kl[(u * kPkThreads + 64 * wave) * 8]);
+      dma16(src, &kl[(u * NT + 64 * wave) * 8]);
     }
-    issue_q(0);
-    issue_q(1);
+    if constexpr (KSLOT0 > 0) {
+      issue_q(0);
+      issue_q(1);
+    }
   } else {
 #pragma unroll
     for (int kb = 0; kb < 4; kb++) {
@@ -416,7 +434,7 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, PkSmem& sh, int q_base,
   }
 #pragma unroll
   for (int u = 0; u < WPT; u++) {
-    const int i = threadIdx.x + u * kPkThreads;
+    const int i = threadIdx.x + u * NT;
     sh.w[i / QT][i % QT] = wv[u];
   }
   if (wave == 0) {
@@ -448,9 +466,9 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, PkSmem& sh, int q_base,
       for (int s2 = 0; s2 < 4; s2++)
         ka[kb][s2] = *reinterpret_cast<const f16x8*>(&kl[(key * 16 + ((4 * s2 + g) ^ c)) * 8]);
     }
-    lds_barrier();  // every wave holds its keys: slots 2..5 are free for Q
+    lds_barrier();  // every wave holds its keys: the key slots are free for Q
 #pragma unroll
-    for (int h = 2; h < 2 * kAhead; h++) issue_q(h);
+    for (int h = KSLOT0 > 0 ? 2 : 0; h < 2 * kAhead; h++) issue_q(h);
   }
 
   // Heads alternate between two accumulator sets: while the MFMAs of head h
@@ -586,14 +604,34 @@ __global__ void __launch_bounds__(kPkThreads) indexer_logits_packed_kernel(PkArg
   __shared__ PkSmem sh;
   const int id = blockIdx.x;
   if (id < a.n_full) {
-    pk_tile<KFP8, 2>(a, sh, (id / a.n_kt) * kPkMaxQT, (id % a.n_kt) * kPkKT);
+    pk_tile<KFP8, 2, kPkWaves>(a, sh, (id / a.n_kt) * kPkMaxQT, (id % a.n_kt) * kPkKT);
   } else {
     const int j = id - a.n_full;
     const int t = a.n_full + (j >> 1);
     const int q_base = (t / a.n_kt) * kPkMaxQT + 32 * (j & 1);
     if (q_base >= a.B) return;  // a half tile past the last query (no DMA issued yet)
-    pk_tile<KFP8, 1>(a, sh, q_base, (t % a.n_kt) * kPkKT);
+    pk_tile<KFP8, 1, kPkWaves>(a, sh, q_base, (t % a.n_kt) * kPkKT);
   }
+}
+
+// Four-wave workgroups over 32 queries x 256 keys (each wave: 64 keys x the
+// 32 queries, as a full tile's wave), ~68 KB of LDS with 8 KB ring slots,
+// so that two workgroups share a CU and one's prologue (64 KB of keys, the
+// first Q pairs) and epilogue (its score stores) run beside the other's
+// MFMAs.  Used for launches of at least kPkhMinTiles full tiles: 4-5 %
+// faster there, ~1 % slower on launches of a round or less.
+constexpr int kPkhWaves = 4;
+constexpr int kPkhQT = 32;
+constexpr int64_t kPkhMinTiles = 384;
+using PkSmemH = PkSmemT<kPkhQT>;
+
+template <bool KFP8>
+__global__ void __launch_bounds__(kPkhWaves * 64, 2) indexer_logits_packed_h_kernel(PkArgs a) {
+  __shared__ PkSmemH sh;
+  const int id = blockIdx.x;
+  const int q_base = (id / a.n_kt) * kPkhQT;
+  if (q_base >= a.B) return;
+  pk_tile<KFP8, 2, kPkhWaves>(a, sh, q_base, (id % a.n_kt) * kPkKT);
 }
 
 // Tiles of a launch with W full tiles that run as two half tiles.
@@ -688,10 +726,19 @@ extern "C" int mi355_dsa_indexer_logits_packed(
   a.n_kt = (int)n_kt;
   a.n_full = (int)(W - split);
   hipStream_t st = as_stream(stream);
-  if (k_fp8)
+  if (W >= kPkhMinTiles) {
+    // large launches: four-wave 32-query workgroups, two per CU
+    const int64_t gh = n_kt * ((B + kPkhQT - 1) / kPkhQT);
+    DSA_CHECK(gh <= INT32_MAX, "B x max_kv too large");
+    if (k_fp8)
+      indexer_logits_packed_h_kernel<true><<<dim3((unsigned)gh), kPkhWaves * 64, 0, st>>>(a);
+    else
+      indexer_logits_packed_h_kernel<false><<<dim3((unsigned)gh), kPkhWaves * 64, 0, st>>>(a);
+  } else if (k_fp8) {
     indexer_logits_packed_kernel<true><<<dim3((unsigned)grid), kPkThreads, 0, st>>>(a);
-  else
+  } else {
     indexer_logits_packed_kernel<false><<<dim3((unsigned)grid), kPkThreads, 0, st>>>(a);
+  }
   DSA_LAUNCH_CHECK("indexer_logits_packed");
   return MI355_DSA_OK;
 }

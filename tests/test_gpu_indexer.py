@@ -160,6 +160,10 @@ SPLIT = [
     (32, 128, 256 * 130, False),
     (33, 100, 256 * 140, False),
     (34, 128, 256 * 130, True),
+    # >= 384 full tiles: the four-wave 32-query kernel
+    (35, 128, 256 * 200, False),
+    (36, 100, 256 * 200, True),      # a partial 32-query tile
+    (37, 1000, 256 * 24, False),
 ]
 
 
