@@ -1,0 +1,75 @@
+"""GPU parity at the full C4 size (one 65,536-token causal prefill): the last
+1024-row indexer sub-chunk at the full 64k causal reach (the layer harness's
+sub-chunk, which takes the four-wave packed kernel), its row top-2048, and one
+4096-token fp8 sparse-prefill launch.  Checks: the packed logits equal the
+decode kernel bit for bit on dyadic inputs (every row), and the oracle on
+sampled rows; the top-k rows equal the oracle's exact top-k; the attention
+of sampled tokens matches the oracle within 2e-3 / 1e-3, lse 1e-4."""
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+T, PAGE = 65536, 64
+NBLK = T // PAGE
+
+
+@pytest.fixture(scope="module")
+def idx_chunk(dev):
+    g = torch.Generator().manual_seed(101)
+    k = (torch.randint(-8, 9, (T, 128), generator=g) / 8).to(torch.float16)
+    R = 1024
+    q = (torch.randint(-8, 9, (R, 32, 128), generator=g) / 8).to(torch.float16)
+    w = (torch.randint(-4, 5, (R, 32), generator=g) / 4).to(torch.float16)
+    bt_row = torch.randperm(NBLK, generator=g).to(torch.int32)
+    seq = torch.arange(T - R + 1, T + 1, dtype=torch.int32)   # causal lengths of rows 64512..65535
+    return k.view(NBLK, PAGE, 128), q, w, bt_row, seq
+
+
+def test_c4_last_indexer_subchunk(ops, dev, idx_chunk):
+    kc, q, w, bt_row, seq = idx_chunk
+    R = q.shape[0]
+    bt = bt_row[None].expand(R, NBLK).contiguous()
+    packed = torch.full((R, T), 7.0, device=dev)
+    ops.sm70_indexer_logits_packed(packed, O.pack_indexer_q(q).to(dev), kc.to(dev), w.to(dev),
+                                   bt.to(dev), seq.to(dev))
+    plain = torch.full((R, T), 7.0, device=dev)
+    ops.sm70_indexer_logits(plain, q.to(dev), kc.to(dev), w.to(dev), bt.to(dev), seq.to(dev), None)
+    assert torch.equal(packed, plain)
+    rows = [0, 1, 511, 1023]
+    want, _ = O.indexer_logits(q[rows], kc, w[rows], bt[rows], seq[rows], T)
+    assert torch.equal(packed.cpu()[rows], want)
+    # the row top-2048 of the same scores (persistent_topk, per-row lengths)
+    out = torch.empty(R, 2048, dtype=torch.int32, device=dev)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+    ops.persistent_topk(packed, seq.view(R, 1).to(dev), out, ws, 2048, T)
+    wt = O.topk_rows(packed.cpu()[rows], seq[rows], 2048)
+    assert torch.equal(out.cpu()[rows], wt)
+
+
+def test_c4_sparse_prefill_launch(ops, pkg, dev):
+    """The last 4096-token launch of the 64k causal prefill (64 heads, top-2048
+    spread over each token's causal range), fp8_ds_mla cache of the sequence."""
+    S = pkg.synthetic
+    g = torch.Generator(device=dev)
+    g.manual_seed(102)
+    sub = 4096
+    kv = S.latent_cache(T, True, g, dev)
+    bt = torch.randperm(NBLK, generator=g, device=dev).to(torch.int32)[None].expand(sub, NBLK).contiguous()
+    q = (torch.randn(sub, 64, 576, generator=g, device=dev) / 24.0).to(torch.float16)
+    t = torch.arange(T - sub, T, device=dev, dtype=torch.float64)
+    n = t + 1
+    j = torch.arange(2048, device=dev, dtype=torch.float64)
+    u = torch.rand(sub, 1, generator=g, device=dev, dtype=torch.float64)
+    idx = torch.floor((j[None] + u) * n[:, None] / 2048.0).to(torch.int32)
+    seq = n.to(torch.int32)
+    o = torch.empty(sub, 64, 512, dtype=torch.float16, device=dev)
+    lse = torch.empty(sub, 64, device=dev)
+    ops.sm70_sparse_mla_decode(o, lse, q, kv, idx, bt, seq, 576 ** -0.5)
+    sel = [0, 1, 2047, 4095]
+    ro, rl = O.sparse_mla(q[sel].cpu(), kv.cpu().view(NBLK, PAGE, 656), idx[sel].cpu(), bt[sel].cpu(),
+                          seq[sel].cpu(), 576 ** -0.5)
+    torch.testing.assert_close(o[sel].float().cpu(), ro, rtol=2e-3, atol=1e-3)
+    assert (lse[sel].cpu() - rl).abs().max() <= 1e-4

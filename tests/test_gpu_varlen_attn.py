@@ -48,6 +48,8 @@ CASES = [
     (5, [0, 333], None, 16, 128, 128, True),
     (6, [0, 200, 265], None, 4, 64, 64, True),
     (7, [0, 130, 400], None, 4, 256, 256, True),
+    (8, [0, 0, 50, 50, 90], [0, 10, 60, 60, 100], 4, 192, 128, False),  # empty query runs
+    (9, [0, 0, 50, 50, 90], [0, 10, 60, 60, 100], 4, 192, 128, True),
 ]
 
 
