@@ -186,7 +186,7 @@ def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
 
 SPARSE_PREFILL_T = 65536
 EXTRAS = ("sweep", "indexer_prefill", "sparse_prefill", "indexer_decode", "gemv", "k_store",
-          "dsa_layer", "dense_decode", "varlen_prefill", "shard_merge", "c1")
+          "dsa_layer", "dense_decode", "varlen_prefill", "shard_merge", "c1", "prefill_topk")
 
 
 def sparse_prefill_flops(T=SPARSE_PREFILL_T, topk=2048, heads=64):
@@ -600,6 +600,36 @@ def bench_c1(torch, pkg, dev, cpu_seconds=5.0, copies=16):
                          "restatement of the same pipeline")}
 
 
+def bench_prefill_topk(torch, pkg, dev, T=65536, sub=1024, K=2048):
+    """Row a4 at C4: persistent_topk over every sub-chunk of a 64k-token
+    causal prefill (row t keeps the top-2048 of its t + 1 scores), as the
+    layer harness calls it.  Scores are random fp32 rows in two alternating
+    256 MB buffers.  Algorithmic bytes: the causal scores read once plus the
+    int32 indices written."""
+    ops = pkg._sm70_ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(13)
+    bufs = [torch.randn(sub, T, generator=g, device=dev) for _ in range(2)]
+    out = torch.empty(sub, K, dtype=torch.int32, device=dev)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+    chunks = []
+    for i, lo in enumerate(range(0, T, sub)):
+        lens = torch.arange(lo + 1, lo + sub + 1, dtype=torch.int32, device=dev).view(sub, 1)
+        width = min(T, (lo + sub + 63) // 64 * 64)
+        chunks.append((bufs[i & 1][:, :width], lens, width))
+
+    def fn():
+        for sc, lens, width in chunks:
+            ops.persistent_topk(sc, lens, out, ws, K, width)
+
+    ms = graph_time_per_call(torch, fn, 1, steps=3, warmup=1) / 1000.0
+    nbytes = 4 * T * (T + 1) / 2 + 4 * T * K
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    del bufs
+    return {"ms": round(ms, 3), "gbps": round(gbps, 1), "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4),
+            "workload": f"64k causal rows in {sub}-row sub-chunks, top-{K} per row"}
+
+
 def cpu_baseline(torch, d, idxs, qs, budget_s):
     """The oracle's PyTorch restatement (fp32) of the same decode layers on
     the host cores: gather -> dequant -> QK -> softmax -> PV."""
@@ -762,6 +792,10 @@ def main():
     if "shard_merge" in extras:
         line["indexer_shard_merge"] = bench_shard_merge(torch, pkg, dev)
         log(f"indexer shard merge: {line['indexer_shard_merge']}")
+        torch.cuda.empty_cache()
+    if "prefill_topk" in extras:
+        line["prefill_topk"] = bench_prefill_topk(torch, pkg, dev)
+        log(f"prefill top-k: {line['prefill_topk']}")
         torch.cuda.empty_cache()
     if "c1" in extras:
         line["c1_pipeline"] = bench_c1(torch, pkg, dev)
