@@ -603,9 +603,10 @@ def bench_c1(torch, pkg, dev, cpu_seconds=5.0, copies=16):
 def bench_prefill_topk(torch, pkg, dev, T=65536, sub=1024, K=2048):
     """Row a4 at C4: persistent_topk over every sub-chunk of a 64k-token
     causal prefill (row t keeps the top-2048 of its t + 1 scores), as the
-    layer harness calls it.  Scores are random fp32 rows in two alternating
-    256 MB buffers.  Algorithmic bytes: the causal scores read once plus the
-    int32 indices written."""
+    layer harness calls it: each sub-chunk's scores are a contiguous
+    [1024, width] fp32 buffer (width = the chunk's reach rounded up to 64
+    keys), carved from two alternating 256 MB random buffers.  Algorithmic
+    bytes: the causal scores read once plus the int32 indices written."""
     ops = pkg._sm70_ops
     g = torch.Generator(device=dev)
     g.manual_seed(13)
@@ -616,7 +617,8 @@ def bench_prefill_topk(torch, pkg, dev, T=65536, sub=1024, K=2048):
     for i, lo in enumerate(range(0, T, sub)):
         lens = torch.arange(lo + 1, lo + sub + 1, dtype=torch.int32, device=dev).view(sub, 1)
         width = min(T, (lo + sub + 63) // 64 * 64)
-        chunks.append((bufs[i & 1][:, :width], lens, width))
+        sc = bufs[i & 1].view(-1)[:sub * width].view(sub, width)
+        chunks.append((sc, lens, width))
 
     def fn():
         for sc, lens, width in chunks:

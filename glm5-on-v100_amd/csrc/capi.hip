@@ -33,6 +33,15 @@ int check_launch(const char* what) {
   return MI355_DSA_OK;
 }
 
+int reserve_lds(const void* kernel, size_t bytes, const char* what) {
+  const hipError_t e =
+      hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess)
+    return set_error(MI355_DSA_EHIP, "%s: cannot reserve %zu bytes of LDS: %s", what, bytes,
+                     hipGetErrorString(e));
+  return MI355_DSA_OK;
+}
+
 // out[0..63]  : x32 MFMA probe results, out[64..127]: x16 probe results,
 // out[128..383]: bit-trick e4m3 decode of bytes 0..255 (value exactly),
 // out[384..639]: hardware v_cvt_pk_f32_fp8 decode of bytes 0..255,

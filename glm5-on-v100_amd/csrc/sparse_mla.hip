@@ -1597,8 +1597,9 @@ static int dense_splits(int B, int n_head, int max_kv) {
 static int launch_attn_f16(const MlaParams& prm, dim3 grid, hipStream_t st) {
   static bool attr = false;
   if (!attr) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(mla_attn_f16_kernel),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(HfSmem));
+    const int rc = reserve_lds(reinterpret_cast<const void*>(mla_attn_f16_kernel),
+                               sizeof(HfSmem), "mla_attn_f16");
+    if (rc) return rc;
     attr = true;
   }
   mla_attn_f16_kernel<<<grid, kPfThreads, sizeof(HfSmem), st>>>(prm);
@@ -1611,8 +1612,9 @@ static int launch_mla(const MlaParams& prm, dim3 grid, hipStream_t st) {
   auto kern = sparse_mla_kernel<KVFP8, HW, KW, NB>;
   static bool attr = false;
   if (!attr) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(Smem));
+    const int rc = reserve_lds(reinterpret_cast<const void*>(kern), sizeof(Smem),
+                               "sparse_mla_decode");
+    if (rc) return rc;
     attr = true;
   }
   kern<<<grid, HW * KW * 64, sizeof(Smem), st>>>(prm);
@@ -1705,8 +1707,9 @@ static int mla_decode_impl(
     if (kv_fp8) {
       static bool pattr = false;
       if (!pattr) {
-        hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_mla_prefill_fp8_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(P3Smem));
+        const int rc = reserve_lds(reinterpret_cast<const void*>(sparse_mla_prefill_fp8_kernel),
+                                   sizeof(P3Smem), "sparse_mla_prefill_fp8");
+        if (rc) return rc;
         pattr = true;
       }
       sparse_mla_prefill_fp8_kernel<<<grid, kPfThreads, sizeof(P3Smem), st>>>(prm);
@@ -1730,8 +1733,9 @@ static int mla_decode_impl(
   if (dma) {
     static bool attr = false;
     if (!attr) {
-      hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_mla_decode_dma_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(DmaSmem));
+      const int rc2 = reserve_lds(reinterpret_cast<const void*>(sparse_mla_decode_dma_kernel),
+                                  sizeof(DmaSmem), "sparse_mla_decode_dma");
+      if (rc2) return rc2;
       attr = true;
     }
     sparse_mla_decode_dma_kernel<<<grid, kDmaThreads, sizeof(DmaSmem), st>>>(prm);

@@ -36,28 +36,35 @@ struct TopkShared {
   uint32_t above;
 };
 
+// Inclusive prefix sum over the 64 lanes of a wave (all lanes active):
+// row_shr DPP steps within each 16-lane row, then the row totals read with
+// v_readlane.  No LDS traffic.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true);  // row_shr:2
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, true);  // row_shr:4
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, true);  // row_shr:8
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)x, 15);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)x, 31);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)x, 47);
+  const int row = (int)(threadIdx.x & 63) >> 4;
+  return x + (row >= 1 ? r0 : 0u) + (row >= 2 ? r1 : 0u) + (row >= 3 ? r2 : 0u);
+}
+
 // Block-wide exclusive prefix sum over NT threads; *total gets the full sum.
 // wsum needs NT/64 + 1 words.
 template <int NT>
 __device__ uint32_t block_excl_scan_n(uint32_t v, uint32_t* wsum, uint32_t* total) {
   constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  const uint32_t x = wave_incl_scan(v);
   if (lane == 63) wsum[wave] = x;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t run = 0;
-    for (int w = 0; w < NW; w++) {
-      const uint32_t t = wsum[w];
-      wsum[w] = run;
-      run += t;
-    }
-    wsum[NW] = run;
+  if (wave == 0) {  // exclusive scan of the NW wave sums, in wave 0's lanes
+    const uint32_t t = lane < NW ? wsum[lane] : 0u;
+    const uint32_t y = wave_incl_scan(t);
+    if (lane < NW) wsum[lane] = y - t;
+    if (lane == NW - 1) wsum[NW] = y;
   }
   __syncthreads();
   const uint32_t res = wsum[wave] + x - v;
@@ -71,9 +78,10 @@ __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* wsum, uint32_t* total)
 }
 
 // Bin T of an nbins histogram with above(T) < need <= above(T) + hist[T],
-// where above(T) counts keys in bins > T.  Requires need <= total.
-__device__ void find_threshold(TopkShared& sh, int nbins, uint32_t need, int* T,
-                               uint32_t* above) {
+// where above(T) counts keys in bins > T.  Requires need <= total.  SH has
+// hist, wsum (kTkWaves + 1 words), T and above.
+template <class SH>
+__device__ void find_threshold(SH& sh, int nbins, uint32_t need, int* T, uint32_t* above) {
   const int per = nbins >= kTkThreads ? nbins / kTkThreads : 1;
   const int lo = threadIdx.x * per;
   uint32_t cs = 0;
@@ -106,17 +114,17 @@ __device__ void find_threshold(TopkShared& sh, int nbins, uint32_t need, int* T,
 // kTkU independent loads in flight per step (a plain strided loop would
 // wait for one load per iteration).
 constexpr int kTkU = 16;
-template <typename F>
+template <int U = kTkU, typename F>
 __device__ __forceinline__ void row_pass(const float* __restrict__ row, int L, F f) {
-  for (int base = 0; base < L; base += kTkThreads * kTkU) {
-    float v[kTkU];
+  for (int base = 0; base < L; base += kTkThreads * U) {
+    float v[U];
 #pragma unroll
-    for (int u = 0; u < kTkU; u++) {
+    for (int u = 0; u < U; u++) {
       const int p = base + u * kTkThreads + (int)threadIdx.x;
       v[u] = (p < L) ? row[p] : 0.f;
     }
 #pragma unroll
-    for (int u = 0; u < kTkU; u++) {
+    for (int u = 0; u < U; u++) {
       const int p = base + u * kTkThreads + (int)threadIdx.x;
       if (p < L) f(p, mono_key(v[u]));
     }
@@ -273,13 +281,411 @@ static int launch_topk(const float* score, int n_rows, int64_t row_stride,
   static bool attr_set = false;
   const size_t smem = sizeof(TopkShared);
   if (!attr_set) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(topk_row_kernel<HAVE_HIST>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(topk_row_kernel<HAVE_HIST>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+      return set_error(MI355_DSA_EHIP, "topk: cannot reserve %zu bytes of LDS", smem);
     attr_set = true;
   }
   topk_row_kernel<HAVE_HIST><<<n_rows, kTkThreads, smem, st>>>(score, row_stride, seq_lens,
                                                               hist, idx, K);
   return check_launch("topk");
+}
+
+// ===========================================================================
+// Whole-row top-k in two reads of the row (persistent_topk, and decode calls
+// with more rows than the two-kernel path takes):
+//  * read 1 builds the 12-bit level-1 histogram (skipped when the caller's
+//    histogram counts exactly L keys).  Its threshold bin leaves `und` keys
+//    undecided; while they exceed the LDS list, one more read of the row
+//    builds the next 10-bit histogram among them (only heavily tied rows).
+//  * read 2 marks every key above the undecided prefix in an LDS bitmap of
+//    positions (one wave ballot covers 64 positions, two whole words) and
+//    appends the undecided keys, with their positions, to an LDS list.
+//  * The remaining 10-bit digits are selected on the list in LDS; list keys
+//    above the exact k-th key tau join the bitmap, keys equal to tau go to
+//    a second bitmap.  When the row reads already reached tau, read 2 fills
+//    the second bitmap directly.
+//  * One block scan over the two bitmaps' popcounts gives each thread its
+//    output offset; it writes the positions of its words in ascending order,
+//    taking the lowest positions among the ties at tau.
+// LDS: the 16 KB histogram, two bitmaps of row_stride bits and the list,
+// sized on the host so two workgroups share a CU at the C4 row width.
+// ===========================================================================
+struct Tk2Head {
+  uint32_t hist[kTopkBins];
+  uint32_t wsum[kTkWaves + 1];
+  uint64_t wsum64[kTkWaves + 1];
+  int T;
+  uint32_t above;
+  uint32_t n_list;
+};
+// loads in flight per thread in the row reads (8 keeps 64 VGPRs, two
+// 1024-thread workgroups per CU)
+constexpr int kTk2U = 8;
+constexpr int kTk2HeadBytes = (int)((sizeof(Tk2Head) + 15) / 16 * 16);
+
+// wave_incl_scan of two packed 32-bit counts whose sums stay below 2^32.
+__device__ __forceinline__ uint64_t wave_incl_scan64(uint64_t x) {
+  const uint32_t lo = wave_incl_scan((uint32_t)x);
+  const uint32_t hi = wave_incl_scan((uint32_t)(x >> 32));
+  return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
+// Block-wide exclusive prefix sum of 64-bit values (two 32-bit counts
+// packed, neither of which can carry into the other).
+__device__ uint64_t block_excl_scan64(uint64_t v, uint64_t* wsum, uint64_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t x = wave_incl_scan64(v);
+  if (lane == 63) wsum[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    const uint64_t t = lane < kTkWaves ? wsum[lane] : 0ull;
+    const uint64_t y = wave_incl_scan64(t);
+    if (lane < kTkWaves) wsum[lane] = y - t;
+    if (lane == kTkWaves - 1) wsum[kTkWaves] = y;
+  }
+  __syncthreads();
+  const uint64_t res = wsum[wave] + x - v;
+  *total = wsum[kTkWaves];
+  __syncthreads();
+  return res;
+}
+
+// Appends (key, p) of the lanes with `take` to the LDS list with one LDS
+// atomic per wave; *n_list counts every append, also those past cap.
+__device__ __forceinline__ void list_append(bool take, uint32_t key, int p, uint32_t* n_list,
+                                            uint32_t* lkey, int32_t* lpos, int cap) {
+  const uint64_t m = __ballot(take);
+  if (m == 0ull) return;
+  const int lane = threadIdx.x & 63;
+  uint32_t b0 = 0;
+  if (lane == 0) b0 = atomicAdd(n_list, (uint32_t)__popcll(m));
+  b0 = __shfl(b0, 0, 64);
+  if (take) {
+    const uint32_t j = b0 + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+    if (j < (uint32_t)cap) {
+      lkey[j] = key;
+      lpos[j] = p;
+    }
+  }
+}
+
+// Read-1 layout of one step of kTk2U values per lane over kTkThreads *
+// kTk2U positions: with V4 each lane loads 16-byte groups of 4 consecutive
+// positions (rows 16-byte aligned, stride a multiple of 4 floats), else
+// single floats; both are coalesced per wave.
+template <bool V4>
+__device__ __forceinline__ int r1_pos(int base, int e) {
+  return V4 ? base + (((e >> 2) * kTkThreads + (int)threadIdx.x) << 2) + (e & 3)
+            : base + e * kTkThreads + (int)threadIdx.x;
+}
+
+// Loads one step; positions >= L read as 0 (with V4 a group that starts
+// below L <= row_stride lies wholly inside the row).
+template <bool V4>
+__device__ __forceinline__ void r1_load(const float* __restrict__ row, int base, int L,
+                                        float (&v)[kTk2U]) {
+  if (V4) {
+#pragma unroll
+    for (int u = 0; u < kTk2U / 4; u++) {
+      const int p = r1_pos<true>(base, 4 * u);
+      const float4 x = (p < L) ? *reinterpret_cast<const float4*>(row + p)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[4 * u] = x.x;
+      v[4 * u + 1] = x.y;
+      v[4 * u + 2] = x.z;
+      v[4 * u + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kTk2U; e++) {
+      const int p = r1_pos<false>(base, e);
+      v[e] = (p < L) ? row[p] : 0.f;
+    }
+  }
+}
+
+// nw2 = bitmap words (2 * ceil(row_stride / 64)); cap = list entries.
+template <bool HAVE_HIST, bool V4>
+__global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu(8))) topk_row2_kernel(
+    const float* __restrict__ score, int64_t row_stride,
+    const int32_t* __restrict__ seq_lens, const uint32_t* __restrict__ hist_in,
+    int32_t* __restrict__ idx, int K, int nw2, int cap) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  Tk2Head& sh = *reinterpret_cast<Tk2Head*>(smem_raw);
+  uint32_t* gtm = reinterpret_cast<uint32_t*>(smem_raw + kTk2HeadBytes);
+  uint32_t* eqm = gtm + nw2;
+  uint32_t* lkey = eqm + nw2;
+  int32_t* lpos = reinterpret_cast<int32_t*>(lkey + cap);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int r = blockIdx.x;
+  const float* row = score + (int64_t)r * row_stride;
+  int32_t* out = idx + (int64_t)r * K;
+  int L = seq_lens[r];
+  if (L > row_stride) L = (int)row_stride;
+  if (L < 0) L = 0;
+  if (L <= K) {
+    for (int p = tid; p < K; p += kTkThreads) out[p] = (p < L) ? p : -1;
+    return;
+  }
+  // ---- read 1: level-1 histogram, bits [20,32) ----
+  bool rebuild = !HAVE_HIST;
+  if (HAVE_HIST) {
+    const uint32_t* h = hist_in + (int64_t)r * kTopkBins;
+    uint32_t part = 0;
+    for (int i = tid; i < kTopkBins; i += kTkThreads) {
+      sh.hist[i] = h[i];
+      part += h[i];
+    }
+    uint32_t total;
+    block_excl_scan(part, sh.wsum, &total);
+    rebuild = (total != (uint32_t)L);
+  }
+  // A rebuilding read 1 also lists the keys of level-1 bin >= te, with te
+  // taken from the first chunk's histogram so that about 1.5 k keys of a
+  // row with stationary scores qualify.  When the exact threshold bin is
+  // >= te and the list did not overflow, the list holds every key the
+  // selection can take and the second read is skipped; otherwise it runs.
+  bool spec = false;
+  uint32_t te = 0;
+  if (rebuild) {
+    constexpr int kS0 = kTkThreads * kTk2U;  // positions per step
+    for (int i = tid; i < kTopkBins; i += kTkThreads) sh.hist[i] = 0u;
+    if (tid == 0) sh.n_list = 0u;
+    __syncthreads();
+    // double buffered: the next step's loads are in flight while this one
+    // is counted and listed
+    float v[kTk2U], w[kTk2U];
+    r1_load<V4>(row, 0, L, v);
+    for (int base = 0; base < L; base += kS0) {
+      if (base + kS0 < L) r1_load<V4>(row, base + kS0, L, w);
+#pragma unroll
+      for (int e = 0; e < kTk2U; e++) {
+        const int p = r1_pos<V4>(base, e);
+        if (p < L) atomicAdd(&sh.hist[mono_key(v[e]) >> 20], 1u);
+      }
+      if (base == 0) {
+        __syncthreads();
+        const int S = min(L, kS0);
+        uint64_t tgt = (3ull * (uint64_t)K * S + 2ull * L - 1) / (2ull * L);
+        tgt = tgt < 1 ? 1 : (tgt > (uint64_t)S ? (uint64_t)S : tgt);
+        int Te;
+        uint32_t ab;
+        find_threshold(sh, kTopkBins, (uint32_t)tgt, &Te, &ab);
+        te = (uint32_t)Te;
+      }
+      // candidates of the step: one LDS atomic per wave for all of them
+      uint64_t m[kTk2U];
+      uint32_t cnt = 0;
+#pragma unroll
+      for (int e = 0; e < kTk2U; e++) {
+        const int p = r1_pos<V4>(base, e);
+        m[e] = __ballot(p < L && (mono_key(v[e]) >> 20) >= te);
+        cnt += (uint32_t)__popcll(m[e]);
+      }
+      if (cnt != 0u) {
+        uint32_t b0 = 0;
+        if (lane == 0) b0 = atomicAdd(&sh.n_list, cnt);
+        b0 = __builtin_amdgcn_readlane(b0, 0);
+        const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+        for (int e = 0; e < kTk2U; e++) {
+          if ((m[e] >> lane) & 1ull) {
+            const uint32_t j = b0 + (uint32_t)__popcll(m[e] & below);
+            if (j < (uint32_t)cap) {
+              lkey[j] = mono_key(v[e]);
+              lpos[j] = r1_pos<V4>(base, e);
+            }
+          }
+          b0 += (uint32_t)__popcll(m[e]);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < kTk2U; e++) v[e] = w[e];
+    }
+    __syncthreads();
+    spec = true;
+  }
+  int T;
+  uint32_t above;
+  find_threshold(sh, kTopkBins, (uint32_t)K, &T, &above);
+  uint32_t need = (uint32_t)K - above;   // keys still to take among the undecided
+  uint32_t prefix = (uint32_t)T;         // undecided: (key >> shift) == prefix
+  int shift = 20;
+  uint32_t und = sh.hist[T];
+  const int nwl = 2 * ((L + 63) >> 6);  // words covering [0, L) in whole wave steps
+  bool list_mode;
+  if (spec && (uint32_t)T >= te && sh.n_list <= (uint32_t)cap) {
+    // every key of bin >= T is on the list (so und <= cap)
+    for (int i = tid; i < nwl; i += kTkThreads) {
+      gtm[i] = 0u;
+      eqm[i] = 0u;
+    }
+    __syncthreads();
+    list_mode = true;
+  } else {
+    // ---- narrow on the row while the undecided keys overflow the list ----
+    while (und > (uint32_t)cap && und != need && shift > 0) {
+      const int s2 = shift - 10;
+      __syncthreads();
+      for (int i = tid; i < 1024; i += kTkThreads) sh.hist[i] = 0u;
+      __syncthreads();
+      row_pass<kTk2U>(row, L, [&](int, uint32_t key) {
+        if ((key >> shift) == prefix) atomicAdd(&sh.hist[(key >> s2) & 1023u], 1u);
+      });
+      __syncthreads();
+      find_threshold(sh, 1024, need, &T, &above);
+      need -= above;
+      prefix = (prefix << 10) | (uint32_t)T;
+      shift = s2;
+      und = sh.hist[T];
+    }
+    // ---- read 2: bitmap of the keys above the prefix; list of the undecided ----
+    // undecided keys that are all taken need no list: they go to the tie bitmap
+    list_mode = shift > 0 && und != need;
+    __syncthreads();
+    if (list_mode)
+      for (int i = tid; i < nwl; i += kTkThreads) eqm[i] = 0u;
+    if (tid == 0) sh.n_list = 0u;
+    __syncthreads();
+    for (int base = 0; base < L; base += kTkThreads * kTk2U) {
+      float v[kTk2U];
+#pragma unroll
+      for (int u = 0; u < kTk2U; u++) {
+        const int p = base + u * kTkThreads + tid;
+        v[u] = (p < L) ? row[p] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kTk2U; u++) {
+        const int p = base + u * kTkThreads + tid;
+        const int p0 = p - lane;  // first position of this wave step, a multiple of 64
+        const uint32_t key = mono_key(v[u]);
+        const uint32_t hi = key >> shift;
+        const bool gt = p < L && hi > prefix;
+        const bool un = p < L && hi == prefix;
+        const uint64_t mg = __ballot(gt);
+        const uint64_t mu = __ballot(un);
+        if (p0 < L && lane == 0) {
+          gtm[p0 >> 5] = (uint32_t)mg;
+          gtm[(p0 >> 5) + 1] = (uint32_t)(mg >> 32);
+          if (!list_mode) {
+            eqm[p0 >> 5] = (uint32_t)mu;
+            eqm[(p0 >> 5) + 1] = (uint32_t)(mu >> 32);
+          }
+        }
+        if (list_mode) list_append(un, key, p, &sh.n_list, lkey, lpos, cap);
+      }
+    }
+    __syncthreads();
+  }
+  // ---- remaining digits on the list, in LDS ----
+  if (list_mode) {
+    const int n_list = min((int)sh.n_list, cap);
+    // a bin holding exactly the keys still needed is taken whole
+    while (shift > 0 && und != need) {
+      const int s2 = shift - 10;
+      __syncthreads();  // every thread has read und
+      for (int i = tid; i < 1024; i += kTkThreads) sh.hist[i] = 0u;
+      __syncthreads();
+      for (int i = tid; i < n_list; i += kTkThreads) {
+        const uint32_t k = lkey[i];
+        if ((k >> shift) == prefix) atomicAdd(&sh.hist[(k >> s2) & 1023u], 1u);
+      }
+      __syncthreads();
+      find_threshold(sh, 1024, need, &T, &above);
+      need -= above;
+      prefix = (prefix << 10) | (uint32_t)T;
+      shift = s2;
+      und = sh.hist[T];
+    }
+    // keys above the final prefix are taken; those equal to it are the ties
+    for (int i = tid; i < n_list; i += kTkThreads) {
+      const uint32_t k = lkey[i] >> shift;
+      const int p = lpos[i];
+      if (k > prefix) atomicOr(&gtm[p >> 5], 1u << (p & 31));
+      else if (k == prefix) atomicOr(&eqm[p >> 5], 1u << (p & 31));
+    }
+    __syncthreads();
+  }
+  // ---- output: positions ascending, the lowest `need` positions of the tau ties ----
+  const uint32_t take_eq = need;
+  const int nwu = (L + 31) >> 5;
+  const int per = (nwu + kTkThreads - 1) / kTkThreads;
+  const int w0 = tid * per, w1 = min(w0 + per, nwu);
+  uint64_t cnt = 0;
+  for (int w = w0; w < w1; w++)
+    cnt += (uint64_t)__popc(gtm[w]) | ((uint64_t)__popc(eqm[w]) << 32);
+  uint64_t tot;
+  const uint64_t ex = block_excl_scan64(cnt, sh.wsum64, &tot);
+  uint32_t g = (uint32_t)ex, e = (uint32_t)(ex >> 32);
+  for (int w = w0; w < w1; w++) {
+    const uint32_t gw = gtm[w], ew = eqm[w];
+    uint32_t m = gw | ew;
+    while (m != 0u) {
+      const int bit = __ffs(m) - 1;
+      m &= m - 1u;
+      const int pos = (w << 5) + bit;
+      if ((gw >> bit) & 1u) {
+        // o < K always holds by construction; the bound keeps a logic error
+        // from ever writing outside the row
+        const uint32_t o = g + (e < take_eq ? e : take_eq);
+        if (o < (uint32_t)K) out[o] = pos;
+        g++;
+      } else {
+        if (e < take_eq && g + e < (uint32_t)K) out[g + e] = pos;
+        e++;
+      }
+    }
+  }
+}
+
+// LDS plan of topk_row2_kernel for a row width: bitmap words and list
+// capacity.  Returns false when the bitmaps leave no room for a list of k
+// entries (then the three-read kernel runs).
+static bool topk_row2_plan(int64_t row_stride, int k, int* nw2, int* cap, size_t* smem) {
+  constexpr size_t kLdsMax = 160 * 1024;
+  constexpr size_t kLdsHalf = 80 * 1024;  // two workgroups per CU
+  const int64_t words = 2 * ((row_stride + 63) / 64);
+  const size_t fixed = (size_t)kTk2HeadBytes + (size_t)words * 2 * sizeof(uint32_t);
+  // prefer two workgroups per CU when the list still holds 2k entries
+  size_t budget = kLdsHalf;
+  if (fixed + (size_t)2 * k * 8 > budget) budget = kLdsMax;
+  if (fixed + (size_t)k * 8 > budget) return false;
+  *nw2 = (int)words;
+  *cap = (int)((budget - fixed) / 8);
+  *smem = fixed + (size_t)(*cap) * 8;
+  return true;
+}
+
+template <bool HAVE_HIST, bool V4>
+static int launch_topk_row2_v(const float* score, int n_rows, int64_t row_stride,
+                              const int32_t* seq_lens, const uint32_t* hist, int32_t* idx, int K,
+                              int nw2, int cap, size_t smem, hipStream_t st) {
+  auto kern = topk_row2_kernel<HAVE_HIST, V4>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+      return set_error(MI355_DSA_EHIP, "topk: cannot reserve 160 KB of LDS");
+    attr_set = true;
+  }
+  kern<<<n_rows, kTkThreads, smem, st>>>(score, row_stride, seq_lens, hist, idx, K, nw2, cap);
+  return check_launch("topk row2");
+}
+
+template <bool HAVE_HIST>
+static int launch_topk_row2(const float* score, int n_rows, int64_t row_stride,
+                            const int32_t* seq_lens, const uint32_t* hist, int32_t* idx, int K,
+                            hipStream_t st) {
+  int nw2 = 0, cap = 0;
+  size_t smem = 0;
+  if (!topk_row2_plan(row_stride, K, &nw2, &cap, &smem))
+    return launch_topk<HAVE_HIST>(score, n_rows, row_stride, seq_lens, hist, idx, K, st);
+  if (row_stride % 4 == 0 && aligned_to(score, 16))
+    return launch_topk_row2_v<HAVE_HIST, true>(score, n_rows, row_stride, seq_lens, hist, idx, K,
+                                               nw2, cap, smem, st);
+  return launch_topk_row2_v<HAVE_HIST, false>(score, n_rows, row_stride, seq_lens, hist, idx, K,
+                                              nw2, cap, smem, st);
 }
 
 // ===========================================================================
@@ -621,16 +1027,19 @@ extern "C" int mi355_dsa_decode_topk(int32_t* idx, const float* score,
     if (rc) return rc;
     static bool attr = false;
     if (!attr) {
-      hipFuncSetAttribute(reinterpret_cast<const void*>(topk_select_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(SelShared));
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(topk_select_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)sizeof(SelShared)) != hipSuccess)
+        return set_error(MI355_DSA_EHIP, "decode_topk: cannot reserve %zu bytes of LDS",
+                         sizeof(SelShared));
       attr = true;
     }
     topk_select_kernel<<<B, kTkThreads, sizeof(SelShared), st>>>(score, max_kv, seq_lens, h, idx,
                                                                  k, n_tiles, ws);
     return check_launch("decode_topk select");
   }
-  return launch_topk<true>(score, B, max_kv, seq_lens,
-                           reinterpret_cast<const uint32_t*>(hist), idx, k, st);
+  return launch_topk_row2<true>(score, B, max_kv, seq_lens,
+                                reinterpret_cast<const uint32_t*>(hist), idx, k, st);
 }
 
 extern "C" size_t mi355_dsa_persistent_topk_workspace_size(int n_rows, int row_stride,
@@ -654,6 +1063,6 @@ extern "C" int mi355_dsa_persistent_topk(const float* score, int n_rows, int row
   DSA_CHECK(max_seq_len >= 0, "max_seq_len must be >= 0");
   if (n_rows == 0) return MI355_DSA_OK;
   DSA_CHECK(idx && score && seq_lens, "null pointer argument");
-  return launch_topk<false>(score, n_rows, row_stride, seq_lens, nullptr, idx, k,
-                            as_stream(stream));
+  return launch_topk_row2<false>(score, n_rows, row_stride, seq_lens, nullptr, idx, k,
+                                 as_stream(stream));
 }

@@ -26,6 +26,12 @@ def scores(kind, B, W, g):
         return torch.round(torch.randn(B, W, generator=g) * 2) / 2
     if kind == "equal":
         return torch.full((B, W), 0.25)
+    if kind == "narrow":  # one level-1 bin holds most keys: the select narrows on the row
+        return 1.0 + torch.randn(B, W, generator=g) * 1e-3
+    if kind == "rising":  # scores grow along the row: a first-chunk threshold estimate overflows
+        return torch.arange(W).float().expand(B, W) * 1e-3 + torch.randn(B, W, generator=g)
+    if kind == "falling":  # scores shrink along the row: the estimate lies above the threshold
+        return -torch.arange(W).float().expand(B, W) * 1e-3 + torch.randn(B, W, generator=g)
     if kind == "mixed":
         s = torch.randn(B, W, generator=g) * 1e3
         s[:, ::3] = float("-inf")
@@ -95,6 +101,45 @@ def test_persistent_topk(ops, dev, case):
     ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
     ops.persistent_topk(s.to(dev), seq.view(B, 1).to(dev), out, ws, 2048, W)
     assert torch.equal(out.cpu(), cref.topk_rows(s, seq, 2048))
+
+
+WIDE_CASES = [
+    ("narrow", 2, 40000, [40000, 39000]),   # level-1 bin over the LDS list: a 10-bit row pass first
+    ("equal", 1, 30000, [30000]),           # ties down to the last digit: bitmap of ties from the row
+    ("randn", 2, 184320, [184320, 100000]),  # wide rows: one workgroup per CU, larger list
+    ("ties", 1, 600000, [600000]),          # bitmaps past the LDS budget: three-read kernel
+    ("randn", 2, 30001, [30001, 29998]),    # row stride not a multiple of 4: 4-byte loads
+    ("rising", 2, 50000, [50000, 30000]),   # candidate estimate overflows: second read
+    ("falling", 2, 50000, [50000, 30000]),  # estimate above the threshold bin: second read
+]
+
+
+@pytest.mark.parametrize("case", WIDE_CASES, ids=[f"{c[0]}-{c[1]}x{c[2]}" for c in WIDE_CASES])
+def test_persistent_topk_select_paths(ops, dev, case):
+    """Every branch of the whole-row select: list overflow narrowed on the
+    row, all-tied rows, wide rows and the fallback for very wide rows."""
+    kind, B, W, seq = case
+    g = torch.Generator().manual_seed(3 * B + W)
+    s = scores(kind, B, W, g)
+    seq = torch.tensor(seq, dtype=torch.int32)
+    out = torch.full((B, 2048), 77, dtype=torch.int32, device=dev)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+    ops.persistent_topk(s.to(dev), seq.view(B, 1).to(dev), out, ws, 2048, W)
+    assert torch.equal(out.cpu(), cref.topk_rows(s, seq, 2048))
+
+
+def test_decode_topk_many_rows_bad_hist(ops, dev):
+    """More rows than the two-kernel path takes, with histograms that do not
+    count the rows: each row's histogram is rebuilt from its scores."""
+    g = torch.Generator().manual_seed(21)
+    B, W = 80, 6000
+    s = scores("narrow", B, W, g)
+    seq = torch.tensor([W - 13 * i for i in range(B)], dtype=torch.int32)
+    h = hist_of(s, seq)
+    h[::2] = 0
+    idx = torch.empty(B, 2048, dtype=torch.int32, device=dev)
+    ops.sm70_decode_topk(idx, s.to(dev), seq.to(dev), h.to(dev), 2048)
+    assert torch.equal(idx.cpu(), cref.topk_rows(s, seq, 2048))
 
 
 def test_persistent_topk_causal_block(ops, dev):
