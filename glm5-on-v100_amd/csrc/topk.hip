@@ -441,11 +441,14 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
     block_excl_scan(part, sh.wsum, &total);
     rebuild = (total != (uint32_t)L);
   }
-  // A rebuilding read 1 also lists the keys of level-1 bin >= te, with te
-  // taken from the first chunk's histogram so that about 1.5 k keys of a
-  // row with stationary scores qualify.  When the exact threshold bin is
-  // >= te and the list did not overflow, the list holds every key the
-  // selection can take and the second read is skipped; otherwise it runs.
+  // A rebuilding read 1 lists the keys of level-1 bin >= te, with te taken
+  // from the histogram of the first step so that about 1.5 k keys of a row
+  // with stationary scores qualify; past the first step it builds no
+  // histogram.  When at least k and at most cap keys were listed, the list
+  // holds every key of the bins from te up, so the threshold bin (>= te)
+  // and its neighbours' counts come from a histogram of the list, and the
+  // second read is skipped.  Otherwise a histogram read of the row follows
+  // and the second read runs.
   bool spec = false;
   uint32_t te = 0;
   if (rebuild) {
@@ -459,12 +462,12 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
     r1_load<V4>(row, 0, L, v);
     for (int base = 0; base < L; base += kS0) {
       if (base + kS0 < L) r1_load<V4>(row, base + kS0, L, w);
-#pragma unroll
-      for (int e = 0; e < kTk2U; e++) {
-        const int p = r1_pos<V4>(base, e);
-        if (p < L) atomicAdd(&sh.hist[mono_key(v[e]) >> 20], 1u);
-      }
       if (base == 0) {
+#pragma unroll
+        for (int e = 0; e < kTk2U; e++) {
+          const int p = r1_pos<V4>(base, e);
+          if (p < L) atomicAdd(&sh.hist[mono_key(v[e]) >> 20], 1u);
+        }
         __syncthreads();
         const int S = min(L, kS0);
         uint64_t tgt = (3ull * (uint64_t)K * S + 2ull * L - 1) / (2ull * L);
@@ -475,23 +478,26 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
         te = (uint32_t)Te;
       }
       // candidates of the step: one LDS atomic per wave for all of them
+      bool tk[kTk2U];
       uint64_t m[kTk2U];
       uint32_t cnt = 0;
 #pragma unroll
       for (int e = 0; e < kTk2U; e++) {
-        const int p = r1_pos<V4>(base, e);
-        m[e] = __ballot(p < L && (mono_key(v[e]) >> 20) >= te);
+        tk[e] = r1_pos<V4>(base, e) < L && (mono_key(v[e]) >> 20) >= te;
+        m[e] = __ballot(tk[e]);
         cnt += (uint32_t)__popcll(m[e]);
       }
       if (cnt != 0u) {
         uint32_t b0 = 0;
         if (lane == 0) b0 = atomicAdd(&sh.n_list, cnt);
         b0 = __builtin_amdgcn_readlane(b0, 0);
-        const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
         for (int e = 0; e < kTk2U; e++) {
-          if ((m[e] >> lane) & 1ull) {
-            const uint32_t j = b0 + (uint32_t)__popcll(m[e] & below);
+          if (tk[e]) {
+            // rank among the wave's taking lanes below this one
+            const uint32_t j = b0 + __builtin_amdgcn_mbcnt_hi(
+                                        (uint32_t)(m[e] >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m[e], 0u));
             if (j < (uint32_t)cap) {
               lkey[j] = mono_key(v[e]);
               lpos[j] = r1_pos<V4>(base, e);
@@ -504,7 +510,17 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
       for (int e = 0; e < kTk2U; e++) v[e] = w[e];
     }
     __syncthreads();
-    spec = true;
+    const uint32_t n_list = sh.n_list;
+    spec = n_list >= (uint32_t)K && n_list <= (uint32_t)cap;
+    __syncthreads();  // every thread has read n_list and the first-step histogram
+    for (int i = tid; i < kTopkBins; i += kTkThreads) sh.hist[i] = 0u;
+    __syncthreads();
+    if (spec) {  // level-1 histogram of the listed keys
+      for (int i = tid; i < (int)n_list; i += kTkThreads) atomicAdd(&sh.hist[lkey[i] >> 20], 1u);
+    } else {     // the estimate missed: level-1 histogram of the whole row
+      row_pass<kTk2U>(row, L, [&](int, uint32_t key) { atomicAdd(&sh.hist[key >> 20], 1u); });
+    }
+    __syncthreads();
   }
   int T;
   uint32_t above;
@@ -515,8 +531,8 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
   uint32_t und = sh.hist[T];
   const int nwl = 2 * ((L + 63) >> 6);  // words covering [0, L) in whole wave steps
   bool list_mode;
-  if (spec && (uint32_t)T >= te && sh.n_list <= (uint32_t)cap) {
-    // every key of bin >= T is on the list (so und <= cap)
+  if (spec) {
+    // T >= te: every key of bin >= T is on the list (so und <= cap)
     for (int i = tid; i < nwl; i += kTkThreads) {
       gtm[i] = 0u;
       eqm[i] = 0u;
