@@ -7,16 +7,21 @@
 // are written in ascending order and the tail is padded with -1.  When
 // seq_len <= k every valid position is selected.
 //
-// Design for gfx950: one 1024-thread workgroup per row, no inter-workgroup
-// synchronisation (the reference's co-resident spin grid needs a forward-
-// progress guarantee that a plain launch does not give).  A 3-level radix
-// select (12 + 12 + 8 bits) on LDS histograms finds the exact k-th key tau
-// and how many keys equal to tau are taken; levels stop early once a bin is
-// taken whole.  The decode path starts from the level-1 histogram the
-// indexer kernel already built.  A final pass does an ordered compaction:
-// each thread owns 16 consecutive positions (staged through LDS so the HBM
-// reads stay coalesced) and one packed block scan yields every thread's
-// output offset, so the result is deterministic.
+// Design for gfx950: no inter-workgroup synchronisation (the reference's
+// co-resident spin grid needs a forward-progress guarantee that a plain
+// launch does not give).  Three kernels share the exact radix select on LDS
+// histograms (a 12-bit level-1 digit, then 10- or 12-bit digits):
+//  * topk_row2_kernel, one 1024-thread workgroup per row, two per CU: the
+//    row is read once or twice (a candidate list in LDS, position bitmaps
+//    and one block scan give the ordered output); persistent_topk and decode
+//    calls with many rows.
+//  * topk_row_kernel / topk_row_select: the same contract in up to four
+//    reads with an ordered compaction pass; rows too wide for the bitmaps
+//    and the decode select kernel's fallback.
+//  * topk_scan_kernel + topk_select_kernel: decode calls with few rows,
+//    spread over the row's 1024-key tiles.
+// The decode paths start from the level-1 histogram the indexer kernel
+// already built.  Every path is deterministic.
 #include "capi_internal.h"
 #include "dsa_common.h"
 
