@@ -186,7 +186,8 @@ def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
 
 SPARSE_PREFILL_T = 65536
 EXTRAS = ("sweep", "indexer_prefill", "sparse_prefill", "indexer_decode", "gemv", "k_store",
-          "dsa_layer", "dense_decode", "varlen_prefill", "shard_merge", "c1", "prefill_topk")
+          "dsa_layer", "dense_decode", "varlen_prefill", "shard_merge", "c1", "prefill_topk",
+          "dsa_layer_prefill")
 
 
 def sparse_prefill_flops(T=SPARSE_PREFILL_T, topk=2048, heads=64):
@@ -632,6 +633,58 @@ def bench_prefill_topk(torch, pkg, dev, T=65536, sub=1024, K=2048):
             "workload": f"64k causal rows in {sub}-row sub-chunks, top-{K} per row"}
 
 
+def bench_dsa_layer_prefill(torch, pkg, dev, T=65536, P=128, V=128, sub=1024, steps=2):
+    """One DSA prefill layer step at the C4 shape through the layer harness:
+    one causal request of 64k tokens, 64 heads, top-2048.  Per 1024-row
+    sub-chunk the packed indexer logits and persistent_topk, then the
+    q_nope -> latent projection, sparse MLA prefill on the fp8_ds_mla cache
+    and the W_UV projection.  The step has host-side control flow (the
+    sub-chunk loop, the token -> request map), so it runs eagerly, timed
+    with events on the current stream after one untimed call."""
+    S = pkg.synthetic
+    m = pkg.dsa_layer
+    H, page = 64, 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(17)
+    npg = T // page
+    kv = S.latent_cache(T, True, g, dev)
+    kc = torch.randn(npg, page, 128, generator=g, device=dev).to(torch.float16)
+    bt = torch.randperm(npg, generator=g, device=dev).to(torch.int32)[None]
+    w = m.DsaLayerWeights(
+        (torch.randn(H, P, 512, generator=g, device=dev) / P ** 0.5).to(torch.float16),
+        (torch.randn(H, 512, V, generator=g, device=dev) / 512 ** 0.5).to(torch.float16),
+        (P + 64) ** -0.5)
+    layer = m.DsaLayer(w, kv, kc)
+    q = (torch.randn(T, H, P + 64, generator=g, device=dev) / 8).to(torch.float16)
+    iq = torch.randn(T, 32, 128, generator=g, device=dev).to(torch.float16)
+    iw = (torch.randn(T, 32, generator=g, device=dev) / 32 ** 0.5).to(torch.float16)
+    causal = torch.arange(1, T + 1, dtype=torch.int32, device=dev)
+    reach = [min(T, lo + sub) for lo in range(0, T, sub)]
+
+    def run():
+        return layer.prefill(q, iq, iw, [0, T], bt, causal, sub_rows=sub, reach=reach)
+
+    run()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        run()
+    e1.record(st)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = (8192.0 * T * (T + 1) / 2 + sparse_prefill_flops(T)[0]
+             + 2.0 * T * H * 512 * (P + V))
+    del layer, kv, kc, q, iq, iw
+    return {"ms": round(ms, 2), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "workload": f"one DSA prefill layer: one causal request of {T} tokens, {H} heads "
+                        f"(q_nope {P}, v {V}), indexer in {sub}-row sub-chunks + persistent_topk "
+                        "+ q_latent + sparse MLA prefill (fp8_ds_mla) + W_UV; eager, host "
+                        "control flow included"}
+
+
 def cpu_baseline(torch, d, idxs, qs, budget_s):
     """The oracle's PyTorch restatement (fp32) of the same decode layers on
     the host cores: gather -> dequant -> QK -> softmax -> PV."""
@@ -798,6 +851,10 @@ def main():
     if "prefill_topk" in extras:
         line["prefill_topk"] = bench_prefill_topk(torch, pkg, dev)
         log(f"prefill top-k: {line['prefill_topk']}")
+        torch.cuda.empty_cache()
+    if "dsa_layer_prefill" in extras:
+        line["dsa_layer_prefill"] = bench_dsa_layer_prefill(torch, pkg, dev)
+        log(f"dsa layer prefill: {line['dsa_layer_prefill']}")
         torch.cuda.empty_cache()
     if "c1" in extras:
         line["c1_pipeline"] = bench_c1(torch, pkg, dev)

@@ -19,7 +19,11 @@
 // k (KW, partial sums reduced through LDS), so both shapes of the layer give
 // 512 workgroups per call: W_UK_T (K = 128, N = 512) as NW = 4, and W_UV
 // (K = 512, N = 128) as KW = 4.  Large T is split over a second grid axis.
-// Accumulation is fp32; out is rounded to fp16 once (RNE).
+// Prefill calls (T >= 512) take a wide variant that covers a head's whole N
+// per workgroup, so each token fragment is loaded once per wave and feeds
+// eight MFMAs.  Both compute D^T = W^T X^T, so a lane stores four
+// consecutive output columns of one token.  Accumulation is fp32; out is
+// rounded to fp16 once (RNE).
 #include <algorithm>
 
 #include "capi_internal.h"
@@ -39,6 +43,7 @@ struct HpArgs {
   int T, H, N, K, tail;
   int n_blocks;  // workgroups per head along n
   int t_chunk;   // tokens per workgroup along grid y (multiple of 16)
+  int out8;      // out rows take 8-byte stores (aligned base and strides)
 };
 
 template <int NW, int KW>
@@ -47,7 +52,8 @@ __global__ __launch_bounds__(256) void head_proj_kernel(HpArgs a) {
   const int g = lane >> 4, c = lane & 15;
   const int h = blockIdx.x / a.n_blocks, nb = blockIdx.x % a.n_blocks;
   const int wn = wave % NW, wk = wave / NW;
-  const int n = (nb * NW + wn) * 16 + c;
+  const int n0 = (nb * NW + wn) * 16;  // the wave's 16 output columns
+  const int n = n0 + c;                 // weight row this lane loads
   const int kp = a.K / KW;
   const int nkb = kp / 32;
   const int k0 = wk * kp + 8 * g;
@@ -70,10 +76,13 @@ __global__ __launch_bounds__(256) void head_proj_kernel(HpArgs a) {
 #pragma unroll
     for (int i = 0; i < kHpMaxKb; ++i)
       if (i < nkb) av[i] = live ? *reinterpret_cast<const f16x8*>(xrow + 32 * i) : zero;
+    // D^T = W^T X^T: the weight fragment is the A operand, the tokens' the
+    // B operand, so a lane's D column is one token and its four rows are
+    // consecutive output columns (one 8-byte store)
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < kHpMaxKb; ++i)
-      if (i < nkb) acc = mfma16x16x32(av[i], b[i], acc);
+      if (i < nkb) acc = mfma16x16x32(b[i], av[i], acc);
     if constexpr (KW > 1) {
       if (wk > 0) red[((wk - 1) * NW + wn) * 64 + lane] = acc;
       __syncthreads();
@@ -83,12 +92,15 @@ __global__ __launch_bounds__(256) void head_proj_kernel(HpArgs a) {
       }
       __syncthreads();
     }
-    if (wk == 0) {
-      // D: lane holds column n, rows 4g .. 4g+3 of the tile
+    if (wk == 0 && live) {
+      // lane: token ta, columns n0 + 4g .. +3
+      f16* op = a.out + (int64_t)ta * a.o_st + (int64_t)h * a.o_sh + n0 + 4 * g;
+      if (a.out8) {
+        const f16x4 o = {(f16)acc[0], (f16)acc[1], (f16)acc[2], (f16)acc[3]};
+        *reinterpret_cast<f16x4*>(op) = o;
+      } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = t0 + 4 * g + j;
-        if (t < t_end) a.out[(int64_t)t * a.o_st + (int64_t)h * a.o_sh + n] = (f16)acc[j];
+        for (int j = 0; j < 4; ++j) op[j] = (f16)acc[j];
       }
     }
   }
@@ -103,6 +115,102 @@ __global__ __launch_bounds__(256) void head_proj_kernel(HpArgs a) {
           a.x + (int64_t)t * a.x_st + (int64_t)h * a.x_sh + a.K + v);
       *reinterpret_cast<f16x8*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + a.N + v) = val;
     }
+  }
+}
+
+// Prefill shapes (many tokens): a workgroup covers all N columns of a head
+// for a run of tokens.  Wave (wn, wk) of NW x KW holds NTW column tiles of
+// 16 x its K / KW slice of the weight in registers, so every token fragment
+// it loads feeds NTW MFMAs (the decode-shaped kernel above feeds one); the
+// next 16-token tile is prefetched; with KW > 1 the partial sums meet in
+// LDS, each wave reducing and storing NTW / KW of the tiles; the carried
+// columns are copied inside the token loop.
+constexpr int kHpWideKb = 4;     // 32-wide k blocks per wave (K = 128 KW)
+constexpr int kHpWideNt = 8;     // column tiles per wave
+constexpr int kHpWideMinT = 512; // tokens from which a call takes the wide kernel
+constexpr int kHpWideWgs = 512;  // workgroups per call (two per CU)
+
+template <int NW, int KW>
+__global__ __launch_bounds__(256) void head_proj_wide_kernel(HpArgs a) {
+  constexpr int NTW = kHpWideNt, KB = kHpWideKb;
+  constexpr int NSH = NTW / KW;  // tiles each wave reduces and stores
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 4, c = lane & 15;
+  const int h = blockIdx.x / a.n_blocks, nb = blockIdx.x % a.n_blocks;
+  const int wn = wave % NW, wk = wave / NW;
+  const int nw0 = (nb * NW + wn) * NTW * 16;  // first column of the wave
+  const int k0 = wk * 32 * KB + 8 * g;
+
+  f16x8 b[NTW][KB];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const f16* wrow = a.wt + ((int64_t)h * a.N + nw0 + 16 * j + c) * a.K + k0;
+#pragma unroll
+    for (int i = 0; i < KB; ++i) b[j][i] = *reinterpret_cast<const f16x8*>(wrow + 32 * i);
+  }
+  __shared__ f32x4 red[KW > 1 ? KW * NW * NTW * 64 : 1];
+
+  const int t_begin = blockIdx.y * a.t_chunk;
+  const int t_end = min(a.T, t_begin + a.t_chunk);
+  const f16x8 zero = {};
+  auto load_x = [&](int t0, f16x8 (&xv)[KB]) {
+    const int ta = t0 + c;
+    const bool live = ta < t_end;
+    const f16* xrow = a.x + (int64_t)(live ? ta : t_begin) * a.x_st + (int64_t)h * a.x_sh + k0;
+#pragma unroll
+    for (int i = 0; i < KB; ++i) xv[i] = live ? *reinterpret_cast<const f16x8*>(xrow + 32 * i) : zero;
+  };
+  f16x8 cur[KB], nxt[KB];
+  load_x(t_begin, cur);
+  for (int t0 = t_begin; t0 < t_end; t0 += 16) {
+    if (t0 + 16 < t_end) load_x(t0 + 16, nxt);
+    f32x4 acc[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < KB; ++i) acc[j] = mfma16x16x32(b[j][i], cur[i], acc[j]);
+    }
+    const int ta = t0 + c;  // D column of this lane: token ta, rows 4g .. 4g+3
+    f16* orow = a.out + (int64_t)ta * a.o_st + (int64_t)h * a.o_sh + nw0 + 4 * g;
+    if constexpr (KW > 1) {
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) red[((wk * NW + wn) * NTW + j) * 64 + lane] = acc[j];
+      __syncthreads();
+#pragma unroll
+      for (int jj = 0; jj < NSH; ++jj) {
+        const int j = wk * NSH + jj;
+        f32x4 v = red[((0 * NW + wn) * NTW + j) * 64 + lane];
+#pragma unroll
+        for (int q = 1; q < KW; ++q) v += red[((q * NW + wn) * NTW + j) * 64 + lane];
+        if (ta < t_end) {
+          const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+          *reinterpret_cast<f16x4*>(orow + 16 * j) = o;
+        }
+      }
+      __syncthreads();
+    } else {
+      if (ta < t_end) {
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          const f16x4 o = {(f16)acc[j][0], (f16)acc[j][1], (f16)acc[j][2], (f16)acc[j][3]};
+          *reinterpret_cast<f16x4*>(orow + 16 * j) = o;
+        }
+      }
+    }
+    // carried columns of the tile's tokens (block 0 of the head)
+    if (a.tail > 0 && nb == 0) {
+      const int per_tok = a.tail / 8;
+      for (int it = threadIdx.x; it < 16 * per_tok; it += 256) {
+        const int t = t0 + it / per_tok, v = (it % per_tok) * 8;
+        if (t < t_end)
+          *reinterpret_cast<f16x8*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + a.N + v) =
+              *reinterpret_cast<const f16x8*>(a.x + (int64_t)t * a.x_st + (int64_t)h * a.x_sh +
+                                               a.K + v);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < KB; ++i) cur[i] = nxt[i];
   }
 }
 
@@ -157,13 +265,33 @@ extern "C" int mi355_dsa_head_proj(void* out, int64_t out_tok_stride, int64_t ou
   a.N = N;
   a.K = K;
   a.tail = tail;
+  a.out8 = aligned_to(out, 8) && out_tok_stride % 4 == 0 && out_head_stride % 4 == 0;
+  hipStream_t st = as_stream(stream);
+  // many tokens: the wide kernel (whole head per workgroup) when the shape
+  // fits it; K = 128 KW and N a multiple of its column span
+  const int wide_cols = (4 / KW) * kHpWideNt * 16;
+  if (T >= kHpWideMinT && K == 32 * kHpWideKb * KW && N % wide_cols == 0 && a.out8) {
+    a.n_blocks = N / wide_cols;
+    const int gxw = H * a.n_blocks;
+    const int tiles = (T + 15) / 16;
+    const int n_chunks = std::max(1, std::min(tiles, kHpWideWgs / std::max(gxw, 1)));
+    a.t_chunk = (tiles + n_chunks - 1) / n_chunks * 16;
+    const dim3 grid(gxw, (T + a.t_chunk - 1) / a.t_chunk);
+    if (KW == 4)
+      head_proj_wide_kernel<1, 4><<<grid, 256, 0, st>>>(a);
+    else if (KW == 2)
+      head_proj_wide_kernel<2, 2><<<grid, 256, 0, st>>>(a);
+    else
+      head_proj_wide_kernel<4, 1><<<grid, 256, 0, st>>>(a);
+    DSA_LAUNCH_CHECK("head_proj");
+    return MI355_DSA_OK;
+  }
   // weight-sized grid along x; split tokens along y until ~2048 workgroups
   const int gx = H * (N / (16 * NW));
   const int tiles = (T + 15) / 16;
   const int n_chunks = std::max(1, std::min(tiles, 2048 / std::max(gx, 1)));
   a.t_chunk = (tiles + n_chunks - 1) / n_chunks * 16;
   const int chunks = (T + a.t_chunk - 1) / a.t_chunk;
-  hipStream_t st = as_stream(stream);
   if (KW == 4)
     launch_hp<1, 4>(a, chunks, st);
   else if (KW == 2)

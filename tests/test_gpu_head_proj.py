@@ -34,7 +34,9 @@ SHAPES = [  # T, H, P, V
     (4, 64, 128, 128),
     (1, 64, 128, 128),
     (17, 16, 192, 256),     # partial token tile, GLM-sized nope / v dims
-    (3000, 8, 128, 128),    # several token chunks
+    (3000, 8, 128, 128),    # several token chunks (the wide many-token kernel)
+    (1000, 8, 256, 256),    # wide kernel with K split over two waves per column group
+    (1500, 16, 128, 128),
     (2, 128, 64, 512),      # small K, wide V
 ]
 
