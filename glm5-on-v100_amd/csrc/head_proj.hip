@@ -130,7 +130,7 @@ constexpr int kHpWideNt = 8;     // column tiles per wave
 constexpr int kHpWideMinT = 512; // tokens from which a call takes the wide kernel
 constexpr int kHpWideWgs = 512;  // workgroups per call (two per CU)
 
-template <int NW, int KW>
+template <int NW, int KW, bool TAIL>
 __global__ __launch_bounds__(256) void head_proj_wide_kernel(HpArgs a) {
   constexpr int NTW = kHpWideNt, KB = kHpWideKb;
   constexpr int NSH = NTW / KW;  // tiles each wave reduces and stores
@@ -148,22 +148,47 @@ __global__ __launch_bounds__(256) void head_proj_wide_kernel(HpArgs a) {
 #pragma unroll
     for (int i = 0; i < KB; ++i) b[j][i] = *reinterpret_cast<const f16x8*>(wrow + 32 * i);
   }
+  // The weight loads complete here, once: vmcnt also counts stores, so a
+  // wait for them inside the token loop would drain the output stores.
+#pragma unroll
+  for (int j = 0; j < NTW; ++j)
+#pragma unroll
+    for (int i = 0; i < KB; ++i) asm volatile("" ::"v"(b[j][i]));
   __shared__ f32x4 red[KW > 1 ? KW * NW * NTW * 64 : 1];
 
+  // Every load and store of the token loop is unconditional, so the
+  // compiler's wait before a tile's MFMAs covers that tile's loads only.
+  // Token indices are clamped to the chunk's last token: a lane past the
+  // end loads, computes and stores that token's row again (the same bits).
   const int t_begin = blockIdx.y * a.t_chunk;
-  const int t_end = min(a.T, t_begin + a.t_chunk);
-  const f16x8 zero = {};
+  const int t_last = min(a.T, t_begin + a.t_chunk) - 1;
   auto load_x = [&](int t0, f16x8 (&xv)[KB]) {
-    const int ta = t0 + c;
-    const bool live = ta < t_end;
-    const f16* xrow = a.x + (int64_t)(live ? ta : t_begin) * a.x_st + (int64_t)h * a.x_sh + k0;
+    const int ta = min(t0 + c, t_last);
+    const f16* xrow = a.x + (int64_t)ta * a.x_st + (int64_t)h * a.x_sh + k0;
 #pragma unroll
-    for (int i = 0; i < KB; ++i) xv[i] = live ? *reinterpret_cast<const f16x8*>(xrow + 32 * i) : zero;
+    for (int i = 0; i < KB; ++i) xv[i] = *reinterpret_cast<const f16x8*>(xrow + 32 * i);
   };
+  // carried columns: 8 of them for one token of the tile per thread (the
+  // 16 * tail / 8 pieces of a tile, repeated over the 256 threads)
+  const int per_tok = TAIL ? a.tail / 8 : 1;
+  const int item = TAIL ? (int)threadIdx.x % (16 * per_tok) : 0;
+  const int tail_dt = item / per_tok, tail_v = (item % per_tok) * 8;
+
   f16x8 cur[KB], nxt[KB];
   load_x(t_begin, cur);
-  for (int t0 = t_begin; t0 < t_end; t0 += 16) {
-    if (t0 + 16 < t_end) load_x(t0 + 16, nxt);
+  // the first tile completes before the loop too, so that the loop head
+  // needs no wait for it
+#pragma unroll
+  for (int i = 0; i < KB; ++i) asm volatile("" ::"v"(cur[i]));
+  for (int t0 = t_begin; t0 <= t_last; t0 += 16) {
+    f16x8 tailv;
+    int tt = 0;
+    if constexpr (TAIL) {
+      tt = min(t0 + tail_dt, t_last);
+      tailv = *reinterpret_cast<const f16x8*>(a.x + (int64_t)tt * a.x_st +
+                                              (int64_t)h * a.x_sh + a.K + tail_v);
+    }
+    load_x(t0 + 16, nxt);  // the last step re-reads the chunk's last token
     f32x4 acc[NTW];
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
@@ -171,7 +196,8 @@ __global__ __launch_bounds__(256) void head_proj_wide_kernel(HpArgs a) {
 #pragma unroll
       for (int i = 0; i < KB; ++i) acc[j] = mfma16x16x32(b[j][i], cur[i], acc[j]);
     }
-    const int ta = t0 + c;  // D column of this lane: token ta, rows 4g .. 4g+3
+    // D column of this lane: token ta, rows (output columns) 4g .. 4g+3
+    const int ta = min(t0 + c, t_last);
     f16* orow = a.out + (int64_t)ta * a.o_st + (int64_t)h * a.o_sh + nw0 + 4 * g;
     if constexpr (KW > 1) {
 #pragma unroll
@@ -183,32 +209,20 @@ __global__ __launch_bounds__(256) void head_proj_wide_kernel(HpArgs a) {
         f32x4 v = red[((0 * NW + wn) * NTW + j) * 64 + lane];
 #pragma unroll
         for (int q = 1; q < KW; ++q) v += red[((q * NW + wn) * NTW + j) * 64 + lane];
-        if (ta < t_end) {
-          const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
-          *reinterpret_cast<f16x4*>(orow + 16 * j) = o;
-        }
+        const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+        *reinterpret_cast<f16x4*>(orow + 16 * j) = o;
       }
       __syncthreads();
     } else {
-      if (ta < t_end) {
 #pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-          const f16x4 o = {(f16)acc[j][0], (f16)acc[j][1], (f16)acc[j][2], (f16)acc[j][3]};
-          *reinterpret_cast<f16x4*>(orow + 16 * j) = o;
-        }
+      for (int j = 0; j < NTW; ++j) {
+        const f16x4 o = {(f16)acc[j][0], (f16)acc[j][1], (f16)acc[j][2], (f16)acc[j][3]};
+        *reinterpret_cast<f16x4*>(orow + 16 * j) = o;
       }
     }
-    // carried columns of the tile's tokens (block 0 of the head)
-    if (a.tail > 0 && nb == 0) {
-      const int per_tok = a.tail / 8;
-      for (int it = threadIdx.x; it < 16 * per_tok; it += 256) {
-        const int t = t0 + it / per_tok, v = (it % per_tok) * 8;
-        if (t < t_end)
-          *reinterpret_cast<f16x8*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + a.N + v) =
-              *reinterpret_cast<const f16x8*>(a.x + (int64_t)t * a.x_st + (int64_t)h * a.x_sh +
-                                               a.K + v);
-      }
-    }
+    if constexpr (TAIL)
+      *reinterpret_cast<f16x8*>(a.out + (int64_t)tt * a.o_st + (int64_t)h * a.o_sh + a.N +
+                                tail_v) = tailv;
 #pragma unroll
     for (int i = 0; i < KB; ++i) cur[i] = nxt[i];
   }
@@ -270,19 +284,29 @@ extern "C" int mi355_dsa_head_proj(void* out, int64_t out_tok_stride, int64_t ou
   // many tokens: the wide kernel (whole head per workgroup) when the shape
   // fits it; K = 128 KW and N a multiple of its column span
   const int wide_cols = (4 / KW) * kHpWideNt * 16;
-  if (T >= kHpWideMinT && K == 32 * kHpWideKb * KW && N % wide_cols == 0 && a.out8) {
+  if (T >= kHpWideMinT && K == 32 * kHpWideKb * KW && N % wide_cols == 0 && a.out8 &&
+      2 * tail <= 256) {
     a.n_blocks = N / wide_cols;
     const int gxw = H * a.n_blocks;
     const int tiles = (T + 15) / 16;
     const int n_chunks = std::max(1, std::min(tiles, kHpWideWgs / std::max(gxw, 1)));
     a.t_chunk = (tiles + n_chunks - 1) / n_chunks * 16;
     const dim3 grid(gxw, (T + a.t_chunk - 1) / a.t_chunk);
-    if (KW == 4)
-      head_proj_wide_kernel<1, 4><<<grid, 256, 0, st>>>(a);
-    else if (KW == 2)
-      head_proj_wide_kernel<2, 2><<<grid, 256, 0, st>>>(a);
-    else
-      head_proj_wide_kernel<4, 1><<<grid, 256, 0, st>>>(a);
+    if (tail > 0) {
+      if (KW == 4)
+        head_proj_wide_kernel<1, 4, true><<<grid, 256, 0, st>>>(a);
+      else if (KW == 2)
+        head_proj_wide_kernel<2, 2, true><<<grid, 256, 0, st>>>(a);
+      else
+        head_proj_wide_kernel<4, 1, true><<<grid, 256, 0, st>>>(a);
+    } else {
+      if (KW == 4)
+        head_proj_wide_kernel<1, 4, false><<<grid, 256, 0, st>>>(a);
+      else if (KW == 2)
+        head_proj_wide_kernel<2, 2, false><<<grid, 256, 0, st>>>(a);
+      else
+        head_proj_wide_kernel<4, 1, false><<<grid, 256, 0, st>>>(a);
+    }
     DSA_LAUNCH_CHECK("head_proj");
     return MI355_DSA_OK;
   }
