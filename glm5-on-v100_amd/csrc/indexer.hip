@@ -72,6 +72,31 @@ __device__ __forceinline__ void load_key_frag(KeyFrag& f, const void* kv,
   }
 }
 
+// load_key_frag without branches, for workgroups inside the row: an
+// unmapped row (row < 0) loads row 0 of the cache instead (n_kv_rows >= 1)
+// and the caller replaces that key's score by the zero key's score, 0.  Its
+// bytes reach only that key's MFMA column.  Every lane then issues the same
+// global loads, so the compiler can count the memory operations in flight
+// (vmcnt, which also counts stores) and waits for exactly the ones needed.
+template <bool KFP8>
+__device__ __forceinline__ void load_key_frag_nb(KeyFrag& f, const void* kv, int64_t row) {
+  const int g = (threadIdx.x & 63) >> 4;
+  const int64_t r = row < 0 ? 0 : row;
+  if constexpr (KFP8) {
+    const uint8_t* rp = reinterpret_cast<const uint8_t*>(kv) + r * (int64_t)kIdxkFp8RowBytes;
+    const u32x4_a4* p = reinterpret_cast<const u32x4_a4*>(rp + 32 * g);
+    f.v[0] = p[0];
+    f.v[1] = p[1];
+    f.scale = *reinterpret_cast<const float*>(rp + 128) * 256.0f;
+  } else {
+    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const f16*>(kv) +
+                                                    r * kIdxHeadDim + 8 * g);
+#pragma unroll
+    for (int i = 0; i < 4; i++) f.v[i] = p[4 * i];
+    f.scale = 1.f;
+  }
+}
+
 // B operand for step s from a key fragment (dims 32s + 8g .. +8 for fp16
 // rows, 32g + 8s .. +8 for fp8 rows).
 template <bool KFP8>
@@ -158,49 +183,103 @@ __global__ void __launch_bounds__(kIdxWaves * 64) indexer_logits_kernel(
   // wave w owns blocks w, w+4, w+8, ... ; stage i covers its blocks
   // [i*kIdxGroup, (i+1)*kIdxGroup) in that order.
   auto blk_of = [&](int stage, int j) { return (stage * kIdxGroup + j) * kIdxWaves + wave; };
-#pragma unroll
-  for (int j = 0; j < kIdxGroup; j++) load_key_frag<KFP8>(cur[j], Kv, key_row(blk_of(0, j)));
 
-  for (int st = 0; st < n_groups; st++) {
-    if (16 * blk_of(st, 0) + p_lo >= p_hi) break;
-    if (st + 1 < n_groups) {
+  // Score of one 16-key block for this lane's key (the same sum in the four
+  // lanes g of a key: the butterfly only reorders commutative additions).
+  auto block_score = [&](const KeyFrag& f) {
+    float v = 0.f;
 #pragma unroll
-      for (int j = 0; j < kIdxGroup; j++)
-        load_key_frag<KFP8>(nxt[j], Kv, key_row(blk_of(st + 1, j)));
+    for (int t = 0; t < 2; t++) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; s++) acc = mfma16x16x32(qa[t][s], key_operand<KFP8>(f, s), acc);
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float d = acc[r];
+        if constexpr (KFP8) d *= f.scale;
+        v += (d > 0.f ? d : 0.f) * wv[t][r];
+      }
     }
+    v += shfl_xor_f(v, 16);
+    v += shfl_xor_f(v, 32);
+    return v;
+  };
+
+  if (p_lo + kIdxPPB <= max_kv && n_kv_rows > 0) {
+    // Whole workgroup inside the row: no branch around any global load or
+    // store.  Every lane stores its key's score (the four lanes of a key
+    // write the same bits), so the waits before a stage's MFMAs count
+    // exactly the operations issued after its keys and never drain the next
+    // stage's loads or the score stores.
+    auto row_nb = [&](int blk) -> int64_t {  // key_row without branches
+      const int p = p_lo + 16 * blk + c;
+      const int32_t pb = s_bt[(p >> page_shift) - pg0];
+      const int64_t row = ((int64_t)pb << page_shift) + (p & (page - 1));
+      return (p >= seq_len || pb < 0 || row >= n_kv_rows) ? -1 : row;
+    };
+    int64_t rcur[kIdxGroup], rnxt[kIdxGroup];
 #pragma unroll
     for (int j = 0; j < kIdxGroup; j++) {
-      const int p0 = p_lo + 16 * blk_of(st, j);
-      if (p0 < p_hi) {
-        float v = 0.f;
+      rcur[j] = row_nb(blk_of(0, j));
+      load_key_frag_nb<KFP8>(cur[j], Kv, rcur[j]);
+    }
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int st = 0; st < n_groups; st++) {
+      if (st + 1 < n_groups) {
 #pragma unroll
-          for (int s = 0; s < 4; s++) acc = mfma16x16x32(qa[t][s], key_operand<KFP8>(cur[j], s), acc);
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            float d = acc[r];
-            if constexpr (KFP8) d *= cur[j].scale;
-            v += (d > 0.f ? d : 0.f) * wv[t][r];
-          }
+        for (int j = 0; j < kIdxGroup; j++) {
+          rnxt[j] = row_nb(blk_of(st + 1, j));
+          load_key_frag_nb<KFP8>(nxt[j], Kv, rnxt[j]);
         }
-        v += shfl_xor_f(v, 16);
-        v += shfl_xor_f(v, 32);
-        const int p = p0 + c;
-        if (g == 0 && p < p_hi) {
-          if (p < seq_len) {
-            srow[p] = v;
-            if (hist != nullptr) atomicAdd(&s_hist[mono_key(v) >> 20], 1u);
-          } else {
-            srow[p] = -INFINITY;
-          }
+      }
+#pragma unroll
+      for (int j = 0; j < kIdxGroup; j++) {
+        float v = block_score(cur[j]);
+        if (rcur[j] < 0) v = 0.f;  // unmapped row: the zero key's score
+        const int p = p_lo + 16 * blk_of(st, j) + c;
+        const bool live = p < seq_len;
+        srow[p] = live ? v : -INFINITY;
+        if (hist != nullptr && g == 0 && live) atomicAdd(&s_hist[mono_key(v) >> 20], 1u);
+      }
+      if (st + 1 < n_groups) {
+#pragma unroll
+        for (int j = 0; j < kIdxGroup; j++) {
+          cur[j] = nxt[j];
+          rcur[j] = rnxt[j];
         }
       }
     }
-    if (st + 1 < n_groups) {
+  } else {
+    // the row's last workgroup: blocks past p_hi are skipped
 #pragma unroll
-      for (int j = 0; j < kIdxGroup; j++) cur[j] = nxt[j];
+    for (int j = 0; j < kIdxGroup; j++) load_key_frag<KFP8>(cur[j], Kv, key_row(blk_of(0, j)));
+    for (int st = 0; st < n_groups; st++) {
+      if (16 * blk_of(st, 0) + p_lo >= p_hi) break;
+      if (st + 1 < n_groups) {
+#pragma unroll
+        for (int j = 0; j < kIdxGroup; j++)
+          load_key_frag<KFP8>(nxt[j], Kv, key_row(blk_of(st + 1, j)));
+      }
+#pragma unroll
+      for (int j = 0; j < kIdxGroup; j++) {
+        const int p0 = p_lo + 16 * blk_of(st, j);
+        if (p0 < p_hi) {
+          const float v = block_score(cur[j]);
+          const int p = p0 + c;
+          if (g == 0 && p < p_hi) {
+            if (p < seq_len) {
+              srow[p] = v;
+              if (hist != nullptr) atomicAdd(&s_hist[mono_key(v) >> 20], 1u);
+            } else {
+              srow[p] = -INFINITY;
+            }
+          }
+        }
+      }
+      if (st + 1 < n_groups) {
+#pragma unroll
+        for (int j = 0; j < kIdxGroup; j++) cur[j] = nxt[j];
+      }
     }
   }
 

@@ -66,6 +66,34 @@ def test_logits_and_hist(ops, dev, case):
         assert torch.equal(hist[b].cpu().long(), ref)
 
 
+@pytest.mark.parametrize("fp8", [False, True], ids=["fp16", "fp8"])
+def test_unmapped_pages_in_full_workgroups(ops, dev, fp8):
+    """Block-table entries that are -1 or point past the cache, inside
+    workgroups that lie wholly in the row (the branch-free path) and in the
+    row's last one: those positions score 0 below seq_len, -inf above."""
+    q, kc, w, bt, _ = make_case(11, 3, 60, 64, fp8, True, 3500, [3500] * 3)
+    bt[0, 3] = -1            # positions 192..255 of row 0
+    bt[1, 20] = 60 + 5       # past the 60-page cache: positions 1280..1343 of row 1
+    bt[2, 54] = -1           # in the row's last (partial) workgroup
+    seq = torch.tensor([3500, 3000, 3490], dtype=torch.int32)
+    score = torch.full((3, 3500), 7.0, device=dev)
+    hist = torch.zeros(3, 4096, dtype=torch.int32, device=dev)
+    ops.sm70_indexer_logits(score, q.to(dev), kc.to(dev), w.to(dev), bt.to(dev), seq.to(dev), hist)
+    got = score.cpu()
+    want, _ = O.indexer_logits(q, kc, w, bt, seq, 3500)
+    assert torch.equal(got[0, 192:256], torch.zeros(64)) and torch.equal(got[1, 1280:1344], torch.zeros(64))
+    assert torch.equal(torch.isinf(got), torch.isinf(want))
+    fin = torch.isfinite(want)
+    if fp8:
+        tol = 1e-5 * want[fin].abs().max().item() + 1e-6
+        assert (got[fin] - want[fin]).abs().max().item() <= tol
+    else:
+        assert torch.equal(got[fin], want[fin])
+    for b in range(3):  # histogram == bincount of the kernel's own scores over p < seq_len
+        ref = torch.bincount((O.mono_key(got[b, :int(seq[b])]) >> 20).long(), minlength=4096)
+        assert torch.equal(hist[b].cpu().long(), ref)
+
+
 def test_duplicate_keys_score_identically(ops, dev):
     g = torch.Generator().manual_seed(11)
     page, nblk = 64, 32
