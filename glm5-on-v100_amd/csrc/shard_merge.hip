@@ -114,11 +114,15 @@ __global__ void __launch_bounds__(kSmThreads) shard_merge_kernel(
   const int tid = threadIdx.x;
 
   // ---- candidates: column col = tid + 512 i = s K + c ----
+  // The loops over i skip (continue) rather than stop at nper, so they
+  // unroll with fixed registers; the loads are unconditional (steps past
+  // nper re-read column tid, whose value is never used), so all of a
+  // thread's loads are in flight together.  A break made a runtime loop:
+  // one load, then one wait, per step.
   uint32_t key[kSmMaxPer];
 #pragma unroll
   for (int i = 0; i < kSmMaxPer; i++) {
-    if (i >= nper) break;
-    const int col = tid + i * kSmThreads;
+    const int col = tid + (i < nper ? i : 0) * kSmThreads;
     const int s = col / K, c = col - s * K;
     key[i] = mono_of(allf[((int64_t)s * R + r) * (2 * K) + c]);
   }
@@ -128,7 +132,7 @@ __global__ void __launch_bounds__(kSmThreads) shard_merge_kernel(
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < kSmMaxPer; i++) {
-    if (i >= nper) break;
+    if (i >= nper) continue;
     atomicAdd(&sh.hist[key[i] >> 20], 1u);
   }
   __syncthreads();
@@ -144,7 +148,7 @@ __global__ void __launch_bounds__(kSmThreads) shard_merge_kernel(
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kSmMaxPer; i++) {
-      if (i >= nper) break;
+      if (i >= nper) continue;
       if ((key[i] >> 20) == prefix) atomicAdd(&sh.hist[(key[i] >> 8) & 0xFFFu], 1u);
     }
     __syncthreads();
@@ -158,7 +162,7 @@ __global__ void __launch_bounds__(kSmThreads) shard_merge_kernel(
       __syncthreads();
 #pragma unroll
       for (int i = 0; i < kSmMaxPer; i++) {
-        if (i >= nper) break;
+        if (i >= nper) continue;
         if ((key[i] >> 8) == prefix) atomicAdd(&sh.hist[key[i] & 0xFFu], 1u);
       }
       __syncthreads();
@@ -205,7 +209,7 @@ __global__ void __launch_bounds__(kSmThreads) shard_merge_kernel(
     uint32_t eq_base = 0;
 #pragma unroll
     for (int i = 0; i < kSmMaxPer; i++) {
-      if (i >= nper) break;  // uniform: every thread runs the same scans
+      if (i >= nper) continue;  // uniform: every thread runs the same scans
       const uint32_t kk = key[i] >> shift;
       if (kk > prefix) emit(i);
       const uint32_t eq = kk == prefix ? 1u : 0u;
@@ -217,7 +221,7 @@ __global__ void __launch_bounds__(kSmThreads) shard_merge_kernel(
   } else {
 #pragma unroll
     for (int i = 0; i < kSmMaxPer; i++) {
-      if (i >= nper) break;
+      if (i >= nper) continue;
       const uint32_t kk = key[i] >> shift;
       if (kk > prefix || (kk == prefix && atomicAdd(&sh.eq_cnt, 1u) < need)) emit(i);
     }
