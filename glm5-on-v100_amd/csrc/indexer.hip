@@ -450,18 +450,18 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, SM& sh, int q_base, int
       kbt[kb] = (p < max_kv && pg < max_blocks) ? bt_row[pg] : -1;
     }
   }
-  int sl_v = 0;  // wave 0: query q_base + lane
-  if (threadIdx.x < QT) {
-    const int q = q_base + threadIdx.x;
-    sl_v = (q < B) ? a.seq_lens[q] : 0;
-  }
+  // Causal lengths and head weights: loaded unconditionally from clamped
+  // query indices (queries past B are zeroed where the values reach LDS),
+  // so the loads are in flight together and do not hold up the key DMAs
+  // below behind one wait each.
+  const int sl_raw = a.seq_lens[min(q_base + (int)(threadIdx.x & 63), B - 1)];  // wave 0's lanes
   constexpr int WPT = kIdxHeads * QT / NT;
-  float wv[WPT];
+  f16 wv[WPT];
 #pragma unroll
   for (int u = 0; u < WPT; u++) {
     const int i = threadIdx.x + u * NT;
     const int h = i / QT, q = q_base + i % QT;
-    wv[u] = (q < B) ? (float)a.W[(int64_t)q * kIdxHeads + h] : 0.f;
+    wv[u] = a.W[(int64_t)min(q, B - 1) * kIdxHeads + h];
   }
   // A operands: this wave's keys (4 blocks of 16), dims 32s + 8g .. +8 for
   // the 4 x32 steps.
@@ -514,9 +514,10 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, SM& sh, int q_base, int
 #pragma unroll
   for (int u = 0; u < WPT; u++) {
     const int i = threadIdx.x + u * NT;
-    sh.w[i / QT][i % QT] = wv[u];
+    sh.w[i / QT][i % QT] = (q_base + i % QT < B) ? (float)wv[u] : 0.f;
   }
   if (wave == 0) {
+    const int sl_v = (lane < QT && q_base + lane < B) ? sl_raw : 0;  // query q_base + lane
     sh.sl[lane] = sl_v;
     int m = sl_v;
 #pragma unroll
