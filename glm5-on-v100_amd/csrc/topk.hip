@@ -778,12 +778,18 @@ __global__ void __launch_bounds__(kScanThreads) topk_scan_kernel(
     if (threadIdx.x == 0) *cnt = 0;
     return;
   }
-  // positions of the tile, coalesced, staged in LDS
+  // positions of the tile, coalesced, staged in LDS; the loads are
+  // unconditional (clamped to L - 1, the value then dropped) so all four are
+  // in flight at once rather than one wait each
   const float* row = score + (int64_t)b * max_kv;
+  constexpr int kPer = kScanTile / kScanThreads;
+  float sv[kPer];
 #pragma unroll
-  for (int e = 0; e < kScanTile / kScanThreads; e++) {
+  for (int e = 0; e < kPer; e++) sv[e] = row[min(p0 + e * kScanThreads + (int)threadIdx.x, L - 1)];
+#pragma unroll
+  for (int e = 0; e < kPer; e++) {
     const int p = p0 + e * kScanThreads + (int)threadIdx.x;
-    sh.v[e * kScanThreads + threadIdx.x] = (p < L) ? row[p] : 0.f;
+    sh.v[e * kScanThreads + threadIdx.x] = (p < L) ? sv[e] : 0.f;
   }
   // ---- T1 from the histogram: thread t owns bins [16t, 16t+16) ----
   const uint32_t* h = hist + (int64_t)b * kTopkBins;
