@@ -27,11 +27,17 @@ __global__ void __launch_bounds__(256) k_store_f16_vec_kernel(
     u32x4* __restrict__ kv, int64_t n_tok, int chunks, int64_t n_rows) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.y + threadIdx.y;
   if (t >= n_tok) return;
+  // the lane's first chunk is loaded with the slot, before the slot is
+  // checked: one memory round trip instead of two
   const int64_t row = slot[t];
-  if (row < 0 || row >= n_rows) return;
   const u32x4* src = k + t * chunks;
+  const int c0 = threadIdx.x;
+  const u32x4 v0 = src[c0 < chunks ? c0 : 0];
+  asm volatile("" ::"v"(v0));  // keeps the load ahead of the check (not sunk past it)
+  if (row < 0 || row >= n_rows) return;
   u32x4* dst = kv + row * chunks;
-  for (int c = threadIdx.x; c < chunks; c += blockDim.x) dst[c] = src[c];
+  if (c0 < chunks) dst[c0] = v0;
+  for (int c = c0 + blockDim.x; c < chunks; c += blockDim.x) dst[c] = src[c];
 }
 
 // fp16 copy, element-wise fallback for unaligned buffers / odd head_dim.
@@ -92,11 +98,14 @@ __global__ void __launch_bounds__(256) concat_cache_mla_kernel(
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= n_tok) return;  // wave-uniform
+  // the token's data is loaded with its slot, before the slot is checked:
+  // one memory round trip instead of two (lanes 8.. re-read a RoPE piece
+  // they do not store)
   const int64_t row = (int64_t)slot[t];
-  if (row < 0 || row >= n_rows) return;  // wave-uniform
   const u32x4 raw = *reinterpret_cast<const u32x4*>(kv_c + t * kv_c_stride + 16 * lane);
-  u32x4 rope = {0u, 0u, 0u, 0u};
-  if (lane < 8) rope = *reinterpret_cast<const u32x4*>(k_pe + t * k_pe_stride + 16 * lane);
+  const u32x4 rope = *reinterpret_cast<const u32x4*>(k_pe + t * k_pe_stride + 16 * (lane & 7));
+  asm volatile("" ::"v"(raw), "v"(rope));  // keeps the loads ahead of the check
+  if (row < 0 || row >= n_rows) return;  // wave-uniform
   if constexpr (!FP8) {
     uint8_t* rp = kv + row * (int64_t)(kLatentDim * 2);
     *reinterpret_cast<u32x4*>(rp + 16 * lane) = raw;
