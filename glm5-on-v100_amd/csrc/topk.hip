@@ -894,7 +894,15 @@ __global__ void __launch_bounds__(kTkThreads) topk_select_kernel(
   SelShared& sh = *reinterpret_cast<SelShared*>(smem_raw);
   const int b = blockIdx.x;
   int32_t* out = idx + (int64_t)b * K;
+  // The row's length, its scan metadata and thread t's tile count (this
+  // path has n_tiles <= 1024) do not depend on each other: they are loaded
+  // together, one memory round trip, before any of them is tested.
+  const uint32_t cnt_own =
+      (uint32_t)ws.counts[(int64_t)b * n_tiles + min((int)threadIdx.x, n_tiles - 1)];
+  const int status = ws.meta[(int64_t)b * 4 + 2];
+  const uint32_t above1 = (uint32_t)ws.meta[(int64_t)b * 4 + 1];
   int L = seq_lens[b];
+  asm volatile("" ::"v"(cnt_own), "v"(status), "v"(above1), "v"(L));
   L = L < 0 ? 0 : (L > max_kv ? max_kv : L);
   if (L <= K) {
     for (int p = threadIdx.x; p < K; p += kTkThreads) out[p] = (p < L) ? p : -1;
@@ -902,22 +910,20 @@ __global__ void __launch_bounds__(kTkThreads) topk_select_kernel(
   }
   const float* row = score + (int64_t)b * max_kv;
   const uint32_t* hrow = hist + (int64_t)b * kTopkBins;
-  const int status = ws.meta[(int64_t)b * 4 + 2];
   if (status != 0) {  // histogram inconsistent with L: rebuild from the row
     topk_row_select(sh.u.full, row, L, K, out, nullptr);
     return;
   }
-  const int used_tiles = (L + kScanTile - 1) / kScanTile;
-  const uint32_t above1 = (uint32_t)ws.meta[(int64_t)b * 4 + 1];
+  const int used_tiles = (L + kScanTile - 1) / kScanTile;  // <= n_tiles <= 1024
   // ---- tile offsets of the candidate lists ----
-  int total_c = 0;
-  for (int t0 = 0; t0 < used_tiles; t0 += kTkThreads) {
-    const int t = t0 + threadIdx.x;
-    const uint32_t n = (t < used_tiles) ? (uint32_t)ws.counts[(int64_t)b * n_tiles + t] : 0u;
+  int total_c;
+  {
+    const int t = threadIdx.x;
+    const uint32_t n = t < used_tiles ? cnt_own : 0u;
     uint32_t tot;
     const uint32_t ex = block_excl_scan_n<kTkThreads>(n, sh.wsum, &tot);
-    if (t < used_tiles && t <= 1024) sh.u.c.toff[t] = total_c + (int)ex;
-    total_c += (int)tot;
+    if (t < used_tiles) sh.u.c.toff[t] = (int)ex;
+    total_c = (int)tot;
   }
   if (total_c > kTkCandCap || used_tiles > 1024) {
     __syncthreads();
