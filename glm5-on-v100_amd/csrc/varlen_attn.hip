@@ -124,9 +124,10 @@ __global__ void __launch_bounds__(kVaThreads, MINB) varlen_attn_kernel(VaArgs a)
     const int i = q0 + 16 * (QB * w + qb) + c;
     const uint16_t* qrow = a.q + (int64_t)(qs + (i < q_len ? i : 0)) * a.q_st + (int64_t)h * a.q_sh +
                            8 * g;
+    // rows past q_len read row 0 of the sequence: their MFMA columns and
+    // softmax state are their own, and their outputs are not stored
 #pragma unroll
-    for (int s = 0; s < NS; s++)
-      qf[qb][s] = i < q_len ? *reinterpret_cast<const u32x4*>(qrow + 32 * s) : (u32x4){0, 0, 0, 0};
+    for (int s = 0; s < NS; s++) qf[qb][s] = *reinterpret_cast<const u32x4*>(qrow + 32 * s);
   }
 
   auto issue_tile = [&](int kt) {
@@ -165,6 +166,13 @@ __global__ void __launch_bounds__(kVaThreads, MINB) varlen_attn_kernel(VaArgs a)
   }
 
   if (n_kt > 0) issue_tile(0);
+  // Q completes here, together with tile 0 (one round trip).  The compiler
+  // does not count the tile DMAs issued by inline asm, so a wait for Q left
+  // to the loop would be vmcnt(0) on every step and drain the next tile.
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++)
+#pragma unroll
+    for (int s = 0; s < NS; s++) asm volatile("" ::"v"(qf[qb][s]));
   for (int kt = 0; kt < n_kt; kt++) {
     if (kt + 1 < n_kt) {
       issue_tile(kt + 1);
