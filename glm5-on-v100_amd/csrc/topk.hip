@@ -385,17 +385,20 @@ __device__ __forceinline__ int r1_pos(int base, int e) {
             : base + e * kTkThreads + (int)threadIdx.x;
 }
 
-// Loads one step; positions >= L read as 0 (with V4 a group that starts
-// below L <= row_stride lies wholly inside the row).
+// Loads one step.  The loads are unconditional: a position >= L reads the
+// row's last group (V4; a group that starts below L <= row_stride lies
+// wholly inside the row) or element, and every use tests p < L.  Loads
+// under a branch would make the compiler's wait before a step's first use
+// vmcnt(0), draining the next step's prefetch as well.
 template <bool V4>
 __device__ __forceinline__ void r1_load(const float* __restrict__ row, int base, int L,
                                         float (&v)[kTk2U]) {
   if (V4) {
+    const int last = (L - 1) & ~3;
 #pragma unroll
     for (int u = 0; u < kTk2U / 4; u++) {
-      const int p = r1_pos<true>(base, 4 * u);
-      const float4 x = (p < L) ? *reinterpret_cast<const float4*>(row + p)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int p = min(r1_pos<true>(base, 4 * u), last);
+      const float4 x = *reinterpret_cast<const float4*>(row + p);
       v[4 * u] = x.x;
       v[4 * u + 1] = x.y;
       v[4 * u + 2] = x.z;
@@ -403,10 +406,7 @@ __device__ __forceinline__ void r1_load(const float* __restrict__ row, int base,
     }
   } else {
 #pragma unroll
-    for (int e = 0; e < kTk2U; e++) {
-      const int p = r1_pos<false>(base, e);
-      v[e] = (p < L) ? row[p] : 0.f;
-    }
+    for (int e = 0; e < kTk2U; e++) v[e] = row[min(r1_pos<false>(base, e), L - 1)];
   }
 }
 
@@ -466,7 +466,7 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
     float v[kTk2U], w[kTk2U];
     r1_load<V4>(row, 0, L, v);
     for (int base = 0; base < L; base += kS0) {
-      if (base + kS0 < L) r1_load<V4>(row, base + kS0, L, w);
+      r1_load<V4>(row, base + kS0, L, w);  // past the row: re-reads its last group, unused
       if (base == 0) {
 #pragma unroll
         for (int e = 0; e < kTk2U; e++) {
