@@ -24,10 +24,10 @@ def _op(name: str):
 
 def sm70_attn_fp8_gemv(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor,
                        s: torch.Tensor) -> None:
-    """fp8-e4m3 weight-only GEMV y[M,N] = x[M,K] @ W[N,K]^T (M <= 8).
-
-    w: uint8 e4m3 bits [N,K]; s: fp32 [128,128]-block scale_inv
-    [ceil(N/128), ceil(K/128)]."""
+    """Matrix-vector product with an fp8 weight: y (fp16 [M, N]) receives
+    x (fp16 [M, K], 1 <= M <= 8) times the transpose of the dequantized
+    weight, where w holds one e4m3 byte per weight element [N, K] and s
+    (fp32) one multiplier per 128 x 128 block of w."""
     _op("sm70_attn_fp8_gemv")(y, x, w, s)
 
 
@@ -41,7 +41,9 @@ def _sm70_attn_fp8_quantize(weight: torch.Tensor) -> tuple[torch.Tensor, torch.T
 
 
 def sm70_attn_fp8_dequant(out: torch.Tensor, w: torch.Tensor, s: torch.Tensor) -> None:
-    """Dequantize fp8-e4m3 block-scaled weights into an fp16 scratch [N,K]."""
+    """Expands the e4m3 weight w [N, K] with its 128 x 128 block multipliers s
+    into fp16 values written to out [N, K] (used for batches too large for
+    the GEMV)."""
     _op("sm70_attn_fp8_dequant")(out, w, s)
 
 
@@ -73,10 +75,11 @@ def sm70_sparse_mla_decode(o: torch.Tensor, lse: torch.Tensor, q: torch.Tensor,
 def sm70_indexer_logits(score: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                         weights: torch.Tensor, block_table: torch.Tensor,
                         seq_lens: torch.Tensor, hist: torch.Tensor | None = None) -> None:
-    """DSA indexer logits -> score [B, max_kv] fp32 (pad = -inf).
-
-    hist (optional): pre-zeroed int32 [B, 4096]; the kernel also builds the
-    level-1 top-k histogram for sm70_decode_topk."""
+    """Fills score [B, max_kv] (fp32) with each position's indexer logit:
+    the weighted sum over the 32 indexer heads of relu(q . k); positions at
+    or past seq_len get -inf.  When hist (int32 [B, 4096], zeroed by the
+    caller) is given, the same launch counts every valid score into its
+    12-bit monotone-key bin, the first level that sm70_decode_topk uses."""
     _op("sm70_indexer_logits")(score, q, k_cache, weights, block_table, seq_lens, hist)
 
 

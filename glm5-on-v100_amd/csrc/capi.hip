@@ -4,7 +4,10 @@
 // csrc/attention/sm70_mla_decode.cu:511-540 and :2807-2818).
 #include <string.h>
 
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 
 #include "capi_internal.h"
 #include "dsa_common.h"
@@ -34,11 +37,23 @@ int check_launch(const char* what) {
 }
 
 int reserve_lds(const void* kernel, size_t bytes, const char* what) {
+  // The dynamic-LDS limit is a per-device property of a kernel: it is set once
+  // per (device, kernel) for the largest size asked so far, under a lock so
+  // that concurrent first calls from several host threads are safe.
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, size_t> done;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return set_error(MI355_DSA_EHIP, "%s: no current HIP device", what);
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = done.find({dev, kernel});
+  if (it != done.end() && it->second >= bytes) return MI355_DSA_OK;
   const hipError_t e =
       hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
   if (e != hipSuccess)
     return set_error(MI355_DSA_EHIP, "%s: cannot reserve %zu bytes of LDS: %s", what, bytes,
                      hipGetErrorString(e));
+  done[{dev, kernel}] = bytes;
   return MI355_DSA_OK;
 }
 

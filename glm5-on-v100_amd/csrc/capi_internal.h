@@ -19,7 +19,8 @@ void clear_error();
 // Converts a pending HIP launch error (if any) into MI355_DSA_EHIP.
 int check_launch(const char* what);
 
-// Raises a kernel's dynamic LDS limit to `bytes`; MI355_DSA_EHIP on failure.
+// Raises a kernel's dynamic LDS limit to `bytes` on the current device (once
+// per device and kernel; thread-safe); MI355_DSA_EHIP on failure.
 int reserve_lds(const void* kernel, size_t bytes, const char* what);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

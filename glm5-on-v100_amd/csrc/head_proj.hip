@@ -169,7 +169,12 @@ __global__ __launch_bounds__(256) void head_proj_wide_kernel(HpArgs a) {
     for (int i = 0; i < KB; ++i) xv[i] = *reinterpret_cast<const f16x8*>(xrow + 32 * i);
   };
   // carried columns: 8 of them for one token of the tile per thread (the
-  // 16 * tail / 8 pieces of a tile, repeated over the 256 threads)
+  // 16 * tail / 8 pieces of a tile, repeated over the 256 threads).  The
+  // repeats are deliberate: the store stays unconditional, so the loop's
+  // waits keep counting it.  At the layer's shapes (q_latent: K 128, N 512;
+  // v_up: K 512, N 128) n_blocks is 1, the repeated stores of a piece come
+  // from one workgroup and meet in one L2 line, and HBM sees each carried
+  // byte once; with n_blocks > 1 every column block stores them again.
   const int per_tok = TAIL ? a.tail / 8 : 1;
   const int item = TAIL ? (int)threadIdx.x % (16 * per_tok) : 0;
   const int tail_dt = item / per_tok, tail_v = (item % per_tok) * 8;

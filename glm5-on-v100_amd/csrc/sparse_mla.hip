@@ -76,6 +76,9 @@ struct MlaParams {
   int64_t n_kv_rows;
   float scale_h;    // fp16-rounded softmax scale
   float empty_lse;  // lse of a (token, head) with no valid key
+  // 1: a key in range whose row does not resolve is a zero key with score 0
+  // (row code -2); 0: such a key is masked (-1)
+  int zero_unresolved;
 };
 
 template <int HW, int KW, int NB>
@@ -191,23 +194,23 @@ __device__ __forceinline__ void resolve_bt(const MlaParams& p, int b, int seq_le
   }
 }
 
-// Row codes: >= 0 a cache row; -1 a masked key; -2 (dense mode only) a
-// position below seq_len whose row does not resolve -- it reads as a zero
-// row and stays in the softmax with score 0, as the reference's dense kernel
-// does (sm70_mla_decode.cu:762-771).
+// Row codes: >= 0 a cache row; -1 a masked key; -2 a position below seq_len
+// (and inside the block table) whose row does not resolve, when
+// p.zero_unresolved is set -- it reads as a zero row and stays in the
+// softmax with score 0, as the reference's dense kernel (sm70_mla_decode.cu:
+// 762-771) and split-decode kernel (:970-992, :1047-1053) do.
 template <int NT>
 __device__ __forceinline__ void resolve_store(const MlaParams& p, int n, int base, int seq_len,
                                               const int pos[kResU], const int pg[kResU],
                                               const int blk[kResU], int32_t* rows) {
-  const bool dense = p.idx == nullptr;
 #pragma unroll
   for (int u = 0; u < kResU; u++) {
     const int j = base + u * NT + (int)threadIdx.x;
     if (j < n) {
       const int64_t row = (int64_t)blk[u] * p.page_size + (pos[u] - pg[u] * p.page_size);
       const bool bad = blk[u] < 0 || row >= p.n_kv_rows;
-      const bool in_range = pos[u] >= 0 && pos[u] < seq_len;
-      rows[j] = bad ? ((dense && in_range) ? -2 : -1) : (int32_t)row;
+      const bool in_range = pos[u] >= 0 && pos[u] < seq_len && pg[u] < p.max_blocks;
+      rows[j] = bad ? ((p.zero_unresolved && in_range) ? -2 : -1) : (int32_t)row;
     }
   }
 }
@@ -688,7 +691,7 @@ __device__ __forceinline__ f32x4 dma_qk(const uint8_t* cb, int kbase, const int3
   for (int r = 0; r < 4; r++) {
     const float v = acc[4][r] + ksc[r][0] * acc[0][r] + ksc[r][1] * acc[1][r] +
                     ksc[r][2] * acc[2][r] + ksc[r][3] * acc[3][r];
-    sv[r] = vv[r] >= 0 ? v : -INFINITY;
+    sv[r] = vv[r] != -1 ? v : -INFINITY;  // -2: zero row, a valid key
   }
   return sv;
 }
@@ -748,7 +751,8 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
     const bool ok = jk < nkeys && pos >= 0 && pos < seq_len && pg < p.max_blocks;
     const int blk = ok ? (bt_in_lds ? sh.bt[pg] : bt_row[pg]) : -1;
     const int64_t row = (int64_t)blk * p.page_size + (pos - pg * p.page_size);
-    sh.rows[jk] = (blk < 0 || row >= p.n_kv_rows) ? -1 : (int32_t)row;
+    sh.rows[jk] = (blk < 0 || row >= p.n_kv_rows) ? ((ok && p.zero_unresolved) ? -2 : -1)
+                                                   : (int32_t)row;
   }
   lds_barrier();
   if (nchunks > 0) dma_chunk(kv, sh.rows, sh.buf[0]);
@@ -1076,7 +1080,7 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
     float mt = -1e30f;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      s4[r] = vv[r] >= 0 ? s4[r] : -INFINITY;
+      s4[r] = vv[r] != -1 ? s4[r] : -INFINITY;  // -2: zero row, a valid key
       mt = fmaxf(mt, s4[r]);
     }
     mt = max8(mt);
@@ -1155,7 +1159,9 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
         const int j = base + u * kPfThreads + (int)threadIdx.x;
         if (j < ntiles * kPfTileKeys) {
           const int64_t row = (int64_t)blk[u] * p.page_size + (pos[u] - pg[u] * p.page_size);
-          sh.rows[j] = (blk[u] < 0 || row >= p.n_kv_rows) ? -1 : (int32_t)row;
+          const bool in_range = pos[u] >= 0 && pos[u] < seq_len && pg[u] < p.max_blocks;
+          sh.rows[j] = (blk[u] < 0 || row >= p.n_kv_rows)
+                           ? ((in_range && p.zero_unresolved) ? -2 : -1) : (int32_t)row;
         }
       }
     }
@@ -1595,13 +1601,9 @@ static int dense_splits(int B, int n_head, int max_kv) {
 }
 
 static int launch_attn_f16(const MlaParams& prm, dim3 grid, hipStream_t st) {
-  static bool attr = false;
-  if (!attr) {
-    const int rc = reserve_lds(reinterpret_cast<const void*>(mla_attn_f16_kernel),
-                               sizeof(HfSmem), "mla_attn_f16");
-    if (rc) return rc;
-    attr = true;
-  }
+  const int rc = reserve_lds(reinterpret_cast<const void*>(mla_attn_f16_kernel), sizeof(HfSmem),
+                             "mla_attn_f16");
+  if (rc) return rc;
   mla_attn_f16_kernel<<<grid, kPfThreads, sizeof(HfSmem), st>>>(prm);
   return check_launch("mla_attn_f16");
 }
@@ -1610,13 +1612,8 @@ template <bool KVFP8, int HW, int KW, int NB>
 static int launch_mla(const MlaParams& prm, dim3 grid, hipStream_t st) {
   using Smem = MlaSmem<HW, KW, NB>;
   auto kern = sparse_mla_kernel<KVFP8, HW, KW, NB>;
-  static bool attr = false;
-  if (!attr) {
-    const int rc = reserve_lds(reinterpret_cast<const void*>(kern), sizeof(Smem),
-                               "sparse_mla_decode");
-    if (rc) return rc;
-    attr = true;
-  }
+  const int rc = reserve_lds(reinterpret_cast<const void*>(kern), sizeof(Smem), "sparse_mla_decode");
+  if (rc) return rc;
   kern<<<grid, HW * KW * 64, sizeof(Smem), st>>>(prm);
   return check_launch("sparse_mla_decode");
 }
@@ -1681,6 +1678,10 @@ static int mla_decode_impl(
   // sm70_mla_decode.cu:2511) leaves lse = -1e30 + ln 1 for an empty token;
   // its dense decode writes -inf (:891-894)
   prm.empty_lse = (!dense && B >= 32 && n_head <= 16) ? -1e30f : -INFINITY;
+  // an in-range key whose row does not resolve: the reference's prefill
+  // kernel masks it (:1617-1628, :1705), its split-decode and dense kernels
+  // read a zero row that keeps score 0 (:970-992, :762-771)
+  prm.zero_unresolved = (dense || !(B >= 32 && n_head <= 16)) ? 1 : 0;
   hipStream_t st = as_stream(stream);
 
   if (dense) {
@@ -1705,13 +1706,9 @@ static int mla_decode_impl(
     prm.n_splits = 1;
     const dim3 grid(B, (n_head + 63) / 64);
     if (kv_fp8) {
-      static bool pattr = false;
-      if (!pattr) {
-        const int rc = reserve_lds(reinterpret_cast<const void*>(sparse_mla_prefill_fp8_kernel),
-                                   sizeof(P3Smem), "sparse_mla_prefill_fp8");
-        if (rc) return rc;
-        pattr = true;
-      }
+      const int rc = reserve_lds(reinterpret_cast<const void*>(sparse_mla_prefill_fp8_kernel),
+                                 sizeof(P3Smem), "sparse_mla_prefill_fp8");
+      if (rc) return rc;
       sparse_mla_prefill_fp8_kernel<<<grid, kPfThreads, sizeof(P3Smem), st>>>(prm);
       return check_launch("sparse_mla_decode");
     }
@@ -1731,13 +1728,9 @@ static int mla_decode_impl(
   const dim3 grid(S, (n_head + 15) / 16, B);
   int rc;
   if (dma) {
-    static bool attr = false;
-    if (!attr) {
-      const int rc2 = reserve_lds(reinterpret_cast<const void*>(sparse_mla_decode_dma_kernel),
-                                  sizeof(DmaSmem), "sparse_mla_decode_dma");
-      if (rc2) return rc2;
-      attr = true;
-    }
+    const int rc2 = reserve_lds(reinterpret_cast<const void*>(sparse_mla_decode_dma_kernel),
+                                sizeof(DmaSmem), "sparse_mla_decode_dma");
+    if (rc2) return rc2;
     sparse_mla_decode_dma_kernel<<<grid, kDmaThreads, sizeof(DmaSmem), st>>>(prm);
     rc = check_launch("sparse_mla_decode");
   } else {

@@ -283,14 +283,9 @@ template <bool HAVE_HIST>
 static int launch_topk(const float* score, int n_rows, int64_t row_stride,
                        const int32_t* seq_lens, const uint32_t* hist, int32_t* idx,
                        int K, hipStream_t st) {
-  static bool attr_set = false;
   const size_t smem = sizeof(TopkShared);
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(topk_row_kernel<HAVE_HIST>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
-      return set_error(MI355_DSA_EHIP, "topk: cannot reserve %zu bytes of LDS", smem);
-    attr_set = true;
-  }
+  const int rc = reserve_lds(reinterpret_cast<const void*>(topk_row_kernel<HAVE_HIST>), smem, "topk");
+  if (rc) return rc;
   topk_row_kernel<HAVE_HIST><<<n_rows, kTkThreads, smem, st>>>(score, row_stride, seq_lens,
                                                               hist, idx, K);
   return check_launch("topk");
@@ -683,13 +678,8 @@ static int launch_topk_row2_v(const float* score, int n_rows, int64_t row_stride
                               const int32_t* seq_lens, const uint32_t* hist, int32_t* idx, int K,
                               int nw2, int cap, size_t smem, hipStream_t st) {
   auto kern = topk_row2_kernel<HAVE_HIST, V4>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-      return set_error(MI355_DSA_EHIP, "topk: cannot reserve 160 KB of LDS");
-    attr_set = true;
-  }
+  const int rc = reserve_lds(reinterpret_cast<const void*>(kern), 160 * 1024, "topk row2");
+  if (rc) return rc;
   kern<<<n_rows, kTkThreads, smem, st>>>(score, row_stride, seq_lens, hist, idx, K, nw2, cap);
   return check_launch("topk row2");
 }
@@ -1058,15 +1048,9 @@ extern "C" int mi355_dsa_decode_topk(int32_t* idx, const float* score,
     topk_scan_kernel<<<dim3(n_tiles, B), kScanThreads, 0, st>>>(score, max_kv, seq_lens, h, k, ws);
     int rc = check_launch("decode_topk scan");
     if (rc) return rc;
-    static bool attr = false;
-    if (!attr) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(topk_select_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)sizeof(SelShared)) != hipSuccess)
-        return set_error(MI355_DSA_EHIP, "decode_topk: cannot reserve %zu bytes of LDS",
-                         sizeof(SelShared));
-      attr = true;
-    }
+    rc = reserve_lds(reinterpret_cast<const void*>(topk_select_kernel), sizeof(SelShared),
+                     "decode_topk");
+    if (rc) return rc;
     topk_select_kernel<<<B, kTkThreads, sizeof(SelShared), st>>>(score, max_kv, seq_lens, h, idx,
                                                                  k, n_tiles, ws);
     return check_launch("decode_topk select");

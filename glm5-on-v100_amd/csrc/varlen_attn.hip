@@ -308,15 +308,8 @@ int launch_va(const VaArgs& a0, int num_seqs, int max_q_len, hipStream_t st) {
   using Sh = VaShape<DQK, DV, KT>;
   constexpr int QROWS = 16 * QB * kVaWaves;
   auto kern = varlen_attn_kernel<BF16, DQK, DV, QB, KT, MINB>;
-  static bool attr = false;
-  if (!attr) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 2 * Sh::STAGE) !=
-        hipSuccess)
-      return set_error(MI355_DSA_EHIP, "varlen_attention: cannot reserve %d bytes of LDS",
-                       2 * Sh::STAGE);
-    attr = true;
-  }
+  const int rc = reserve_lds(reinterpret_cast<const void*>(kern), 2 * Sh::STAGE, "varlen_attention");
+  if (rc) return rc;
   VaArgs a = a0;
   a.n_qtiles = (max_q_len + QROWS - 1) / QROWS;
   if (a.n_qtiles == 0) return MI355_DSA_OK;

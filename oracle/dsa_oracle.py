@@ -249,31 +249,49 @@ def scaled_q(q: torch.Tensor, scale: float) -> torch.Tensor:
 
 def sparse_mla(q: torch.Tensor, kv_cache: torch.Tensor, idx: torch.Tensor,
                bt: torch.Tensor, seq_lens: torch.Tensor, scale: float,
-               dtype=torch.float64, empty_lse: float | None = None):
+               dtype=torch.float64, empty_lse: float | None = None,
+               zero_unresolved: bool | None = None):
     """Reference sparse attention for every token/head.  A selected entry j
-    is used iff 0 <= idx < seq_len and its row resolves inside the cache
-    (sm70_mla_decode.cu:977-992).  Returns (o fp32 [B,H,512], lse fp32
-    [B,H]); tokens with no valid key get o = 0 and lse = empty_lse, by
-    default the op's: -1e30 when the reference dispatches to its prefill
-    kernel (B >= 32 and H <= 16, sm70_mla_decode.cu:2511, lse = m_init + ln 1
-    at :1789-1793), else -inf (merge convention, :1175-1183)."""
+    takes part iff 0 <= idx < seq_len (sm70_mla_decode.cu:1047-1053).  Its
+    row is bt[b, idx / page] * page + idx % page; when that row does not
+    resolve (negative block, or row outside the cache) the reference's two
+    kernels differ, and the op follows the reference's dispatch
+    (sm70_mla_decode.cu:2511):
+      * B >= 32 and H <= 16 (its prefill kernel): the key is masked
+        (row -1 -> invalid, :1617-1628, :1705);
+      * otherwise (its split-decode kernel): the key reads as a zero row and
+        stays in the softmax with score 0 (:970-992 zero-fills the tile,
+        :1047-1053 tests only the position range).
+    zero_unresolved=None picks that rule; True/False forces one.  An entry
+    whose page index is past the block table's width is masked either way
+    (the reference reads its table out of bounds there, which defines
+    nothing).  Returns (o fp32 [B,H,512], lse fp32 [B,H]); tokens with no
+    key get o = 0 and lse = empty_lse, by default the op's: -1e30 on the
+    prefill-kernel shapes (lse = m_init + ln 1, :1789-1793), else -inf
+    (merge convention, :1175-1183)."""
     B, H, D = q.shape
     page = kv_cache.shape[-2]
     row_w = kv_cache.shape[-1]
     n_rows = kv_cache.numel() // row_w
     o = torch.zeros(B, H, 512, dtype=torch.float32)
+    prefill_shape = B >= 32 and H <= 16
     if empty_lse is None:
-        empty_lse = -1e30 if (B >= 32 and H <= 16) else float("-inf")
+        empty_lse = -1e30 if prefill_shape else float("-inf")
+    if zero_unresolved is None:
+        zero_unresolved = not prefill_shape
     lse = torch.full((B, H), empty_lse, dtype=torch.float32)
     qs = scaled_q(q, scale).to(dtype)
     for b in range(B):
         sel = idx[b].to(torch.int64)
         L = int(seq_lens[b])
         valid = (sel >= 0) & (sel < L)
+        in_table = valid & (torch.div(sel, page, rounding_mode="floor") < bt.shape[1])
         rows = resolve_rows(torch.where(valid, sel, torch.zeros_like(sel)),
                             bt[b], page, n_rows)
         rows = torch.where(valid, rows, torch.full_like(rows, -1))
         use = rows >= 0
+        if zero_unresolved:
+            use = use | in_table  # unresolved rows stay as zero keys
         if not bool(use.any()):
             continue
         kv = latent_rows_fp16(kv_cache, rows[use]).to(dtype)  # [n, 576]

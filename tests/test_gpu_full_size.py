@@ -1,7 +1,7 @@
 """GPU parity at the full C4 size (one 65,536-token causal prefill): the last
 1024-row indexer sub-chunk at the full 64k causal reach (the layer harness's
 sub-chunk, which takes the four-wave packed kernel), its row top-2048, and one
-4096-token fp8 sparse-prefill launch.  Checks: the packed logits equal the
+4096-token sparse-prefill launch on each cache type (fp8_ds_mla, fp16).  Checks: the packed logits equal the
 decode kernel bit for bit on dyadic inputs (every row), and the oracle on
 sampled rows; the top-k rows equal the oracle's exact top-k; the attention
 of sampled tokens matches the oracle within 2e-3 / 1e-3, lse 1e-4."""
@@ -49,14 +49,16 @@ def test_c4_last_indexer_subchunk(ops, dev, idx_chunk):
     assert torch.equal(out.cpu()[rows], wt)
 
 
-def test_c4_sparse_prefill_launch(ops, pkg, dev):
+@pytest.mark.parametrize("fp8", [True, False], ids=["fp8", "fp16"])
+def test_c4_sparse_prefill_launch(ops, pkg, dev, fp8):
     """The last 4096-token launch of the 64k causal prefill (64 heads, top-2048
-    spread over each token's causal range), fp8_ds_mla cache of the sequence."""
+    spread over each token's causal range), fp8_ds_mla or fp16 latent cache of
+    the sequence."""
     S = pkg.synthetic
     g = torch.Generator(device=dev)
     g.manual_seed(102)
     sub = 4096
-    kv = S.latent_cache(T, True, g, dev)
+    kv = S.latent_cache(T, fp8, g, dev)
     bt = torch.randperm(NBLK, generator=g, device=dev).to(torch.int32)[None].expand(sub, NBLK).contiguous()
     q = (torch.randn(sub, 64, 576, generator=g, device=dev) / 24.0).to(torch.float16)
     t = torch.arange(T - sub, T, device=dev, dtype=torch.float64)
@@ -69,7 +71,7 @@ def test_c4_sparse_prefill_launch(ops, pkg, dev):
     lse = torch.empty(sub, 64, device=dev)
     ops.sm70_sparse_mla_decode(o, lse, q, kv, idx, bt, seq, 576 ** -0.5)
     sel = [0, 1, 2047, 4095]
-    ro, rl = O.sparse_mla(q[sel].cpu(), kv.cpu().view(NBLK, PAGE, 656), idx[sel].cpu(), bt[sel].cpu(),
+    ro, rl = O.sparse_mla(q[sel].cpu(), kv.cpu().view(NBLK, PAGE, kv.shape[-1]), idx[sel].cpu(), bt[sel].cpu(),
                           seq[sel].cpu(), 576 ** -0.5)
     torch.testing.assert_close(o[sel].float().cpu(), ro, rtol=2e-3, atol=1e-3)
     assert (lse[sel].cpu() - rl).abs().max() <= 1e-4

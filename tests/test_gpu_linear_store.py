@@ -20,7 +20,8 @@ def test_selfcheck(pkg, lib, dev):
     assert rc == 0, msg
 
 
-@pytest.mark.parametrize("n_tok,page,nblk", [(1, 64, 2), (333, 64, 8), (4096, 16, 300)])
+@pytest.mark.parametrize("n_tok,page,nblk", [(1, 64, 2), (333, 64, 8), (4096, 16, 300),
+                                             (65536, 64, 1100)])  # C5b: 64k tokens
 def test_k_store_fp16(ops, dev, n_tok, page, nblk):
     g = torch.Generator().manual_seed(n_tok)
     k = torch.randn(n_tok, 128, generator=g).to(torch.float16)
@@ -118,7 +119,7 @@ def test_gemv_baseline_shapes(ops, dev, N, K):
     s = torch.rand((N + 127) // 128, (K + 127) // 128, generator=g, device=dev) * 1e-4
     table = _decode_table(dev)
     w32 = table[wq.long()] * s.repeat_interleave(128, 0)[:N].repeat_interleave(128, 1)[:, :K]
-    for M in (1, 4):
+    for M in (1, 2, 3, 4):
         x = torch.randn(M, K, generator=g, device=dev).to(torch.float16)
         y = torch.empty(M, N, dtype=torch.float16, device=dev)
         ops.sm70_attn_fp8_gemv(y, x, wq, s)

@@ -90,6 +90,61 @@ def test_decode_invalid_entries(ops, dev):
     assert torch.all(o[2] == 0) and torch.all(torch.isinf(lse[2]))
 
 
+UNRESOLVED = [
+    # B, H, fp8, topk: kernel path -> rule for a position below seq_len on a bad block
+    (4, 64, True, 2048),    # fp8 split decode (LDS-DMA kernel): zero key
+    (2, 64, False, 1024),   # fp16 split decode (register-staged kernel): zero key
+    (300, 64, True, 256),   # fp8 prefill configuration: zero key (64 heads)
+    (300, 64, False, 256),  # fp16 prefill configuration: zero key
+    (40, 16, True, 256),    # B >= 32, H <= 16 (the reference's prefill kernel): masked
+    (300, 16, False, 256),  # same rule in the prefill configuration: masked
+]
+
+
+def make_unresolved(seed, B, H, fp8, topk, nblk=40, page=64, seq_len=2500):
+    """Half of every token's selected positions lie on pages whose table
+    entry is -1 or names a block past the cache (pages 3 and 7), the other
+    half on good pages; latent values are O(1) so that the zero-key and
+    masking rules give clearly different outputs."""
+    g = torch.Generator().manual_seed(seed)
+    lat = torch.randn(nblk * page, 576, generator=g)
+    kv = (O.dsmla_rows(lat).view(nblk, page, 656) if fp8
+          else lat.to(torch.float16).view(nblk, page, 576))
+    mb = (seq_len + page - 1) // page
+    bt = torch.stack([torch.randperm(nblk, generator=g)[:mb] for _ in range(B)]).to(torch.int32)
+    bt[:, 3] = -1
+    bt[:, 7] = nblk + 5
+    bad = torch.cat([torch.arange(3 * page, 4 * page), torch.arange(7 * page, 8 * page)])
+    good = torch.tensor([p for p in range(seq_len) if p // page not in (3, 7)])
+    idx = torch.empty(B, topk, dtype=torch.int32)
+    for b in range(B):
+        nb = min(topk // 2, bad.numel())
+        sel = torch.cat([bad[torch.randperm(bad.numel(), generator=g)[:nb]],
+                         good[torch.randperm(good.numel(), generator=g)[:topk - nb]]])
+        idx[b] = sel.sort().values.to(torch.int32)
+    q = (torch.randn(B, H, 576, generator=g) * 0.05).to(torch.float16)
+    seq = torch.full((B,), seq_len, dtype=torch.int32)
+    return q, kv, idx, bt, seq
+
+
+@pytest.mark.parametrize("case", UNRESOLVED, ids=[f"B{c[0]}H{c[1]}{'fp8' if c[2] else 'fp16'}"
+                                                 for c in UNRESOLVED])
+def test_unresolved_rows_follow_reference_dispatch(ops, dev, case):
+    """Selected positions below seq_len whose block-table entry is -1 or
+    names a block past the cache: zero keys with score 0 on the reference's
+    split-decode shapes, masked on its prefill-kernel shapes (B >= 32 and
+    H <= 16), as the oracle states.  The other rule's answer is checked to
+    be far outside the tolerance, so the test separates the two."""
+    B, H, fp8, topk = case
+    q, kv, idx, bt, seq = make_unresolved(70 + B + H, B, H, fp8, topk)
+    o, lse = run(ops, dev, q, kv, idx, bt, seq)
+    ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
+    check(o, lse, ro, rl)
+    zero = not (B >= 32 and H <= 16)
+    _, alt_lse = O.sparse_mla(q[:2], kv, idx[:2], bt[:2], seq[:2], SCALE, zero_unresolved=not zero)
+    assert (lse[:2] - alt_lse).abs().min().item() > 100 * LSE_ATOL
+
+
 @pytest.mark.parametrize("B,H,expect", [(40, 16, -1e30), (300, 16, -1e30), (40, 64, -math.inf),
                                          (31, 16, -math.inf)])
 def test_empty_token_lse_convention(ops, dev, B, H, expect):

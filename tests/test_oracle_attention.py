@@ -202,3 +202,94 @@ def test_dense_fp16_accumulation_stays_near_exact():
     torch.testing.assert_close(o16, o, rtol=2e-3, atol=1e-3)
     assert (lse16 - lse).abs().max() <= 1e-4
     assert not torch.equal(o16, o)
+
+
+def _e4m3_by_hand(b: int) -> float:
+    """OCP e4m3fn byte -> value from the format's definition (sign, 4-bit
+    exponent with bias 7, 3-bit mantissa, exponent 0 = subnormal)."""
+    sign = -1.0 if b & 0x80 else 1.0
+    e, m = (b >> 3) & 0xF, b & 7
+    if e == 0:
+        return sign * (m / 8.0) * 2.0 ** -6
+    return sign * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+
+
+def _dsmla_row_by_hand(codes, scales, rope):
+    """656-byte fp8_ds_mla row assembled byte by byte: 512 e4m3 codes, the 4
+    fp32 tile scales at bytes 512 + 4t (little endian), 64 fp16 RoPE values
+    at bytes 528 + 2i (sm70_mla_decode.cu:74-100)."""
+    import struct
+    raw = bytes(codes) + struct.pack("<4f", *scales) + struct.pack("<64e", *rope)
+    assert len(raw) == 656
+    return torch.tensor(list(raw), dtype=torch.uint8)
+
+
+def test_fp8_reader_per_tile_known_answer():
+    """The fp8_ds_mla branch of latent_rows_fp16, pinned value by value on a
+    row with four distinct tile scales: dim d < 512 reads
+    fp16_rn(e4m3(byte d) * scale[d // 128]); dims 512..575 are the RoPE
+    fp16 bits copied.  A tile-index, byte-offset or rounding mistake changes
+    at least one of the 576 values."""
+    import numpy as np
+    rng = np.random.default_rng(7)
+    codes = [int(c) for c in rng.integers(0, 256, 512)]
+    codes = [c if (c & 0x7F) != 0x7F else c ^ 1 for c in codes]  # no NaN codes
+    codes[0], codes[1], codes[130], codes[300] = 0x00, 0x80, 0x7E, 0x01  # +0, -0, 448, min denormal
+    scales = [0.25, 3.0, 1.0 / 96.0, 5.5]
+    rope = [float(np.float16(x)) for x in rng.standard_normal(64)]
+    row = _dsmla_row_by_hand(codes, scales, rope)
+    page = 4
+    kv = torch.zeros(2, page, 656, dtype=torch.uint8)
+    kv[1, 2] = row  # physical row 6
+    got = O.latent_rows_fp16(kv, torch.tensor([6, -1]))
+    want = [float(np.float16(_e4m3_by_hand(codes[d]) * np.float32(scales[d // 128])))
+            for d in range(512)] + rope
+    assert got[0].double().tolist() == want
+    assert torch.all(got[1] == 0)
+    # bit-level: the RoPE half of the row is copied, not converted
+    assert torch.equal(got[0, 512:].view(torch.int16),
+                       row[528:].view(torch.int16))
+    # one selected key: o is the key's value part, lse = q_s . k summed by hand
+    q = torch.tensor(rng.standard_normal((1, 2, 576)) * 0.3, dtype=torch.float16)
+    bt = torch.tensor([[1, 0]], dtype=torch.int32)   # position 2 -> block 1, row 6
+    idx = torch.tensor([[2, -1, -1]], dtype=torch.int32)
+    o, lse = O.sparse_mla(q, kv, idx, bt, torch.tensor([4], dtype=torch.int32), SCALE)
+    assert o[0].double().tolist() == [want[:512]] * 2
+    s16 = float(np.float16(SCALE))
+    for h in range(2):
+        qs = [float(np.float16(float(q[0, h, d]) * s16)) for d in range(576)]
+        dot = math.fsum(qs[d] * want[d] for d in range(576))
+        assert abs(float(lse[0, h]) - dot) <= 1e-6 + 2.0 ** -23 * abs(dot)  # fp32 lse rounding
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_unresolved_row_is_zero_key_on_split_decode_shapes(fp8):
+    """A selected position below seq_len whose page maps to block -1, or to a
+    block past the cache, is a zero key with score 0 on the reference's
+    split-decode shapes (sm70_mla_decode.cu:970-992, :1047-1053), and masked
+    on its prefill-kernel shapes, B >= 32 and H <= 16 (:1617-1628, :1705).
+    Closed forms: with one resolvable key of score s and n zero keys,
+    o = e^s v / (e^s + n) and lse = ln(e^s + n); masked, o = v and lse = s."""
+    g = torch.Generator().manual_seed(11)
+    page = 8
+    kv, _ = make_cache(g, nblk=3, page=page, fp8=fp8)
+    n_rows = 3 * page
+    bt_row = torch.tensor([2, -1, 7, 0], dtype=torch.int32)  # block 7 is past the cache
+    for B, H, zero in ((1, 4, True), (32, 16, False)):
+        bt = bt_row.expand(B, 4).contiguous()
+        q = torch.randn(B, H, 576, generator=g).to(torch.float16)
+        # position 3 -> block 2 (resolves); 9 -> block -1; 17 -> block 7 (row >= n_rows);
+        # 30 -> block 0 but >= seq_len (masked either way); 33 -> page 4, past the table
+        idx = torch.tensor([3, 9, 17, 30, 33], dtype=torch.int32).expand(B, 5).contiguous()
+        seq = torch.full((B,), 29, dtype=torch.int32)
+        o, lse = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
+        K = O.latent_rows_fp16(kv, torch.tensor([2 * page + 3]))[0].double()
+        assert 2 * page + 3 < n_rows
+        s = O.scaled_q(q, SCALE).double() @ K  # [B, H]
+        if zero:
+            w = torch.exp(s) / (torch.exp(s) + 2.0)
+            assert torch.allclose(o.double(), w[..., None] * K[:512], atol=1e-6)
+            assert torch.allclose(lse.double(), torch.log(torch.exp(s) + 2.0), atol=1e-6)
+        else:
+            assert torch.allclose(o.double(), K[:512].expand(B, H, 512), atol=1e-6)
+            assert torch.allclose(lse.double(), s, atol=1e-6)
