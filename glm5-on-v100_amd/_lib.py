@@ -53,6 +53,10 @@ SIGNATURES = {
     "mi355_dsa_sparse_mla_decode": (_c_int, [_p, _p, _p, _c_int, _c_int, _p, _c_int, _c_i64,
                                              _c_int, _p, _c_int, _p, _c_int, _p, _c_f32, _p,
                                              _c_size, _p]),
+    "mi355_dsa_sparse_mla_noalloc_max_bytes": (_c_size, []),
+    "mi355_dsa_sparse_mla_decode_noalloc": (_c_int, [_p, _p, _p, _c_int, _c_int, _p, _c_int,
+                                                     _c_i64, _c_int, _p, _c_int, _p, _c_int, _p,
+                                                     _c_f32, _p]),
     "mi355_dsa_attn_fp8_gemv": (_c_int, [_p, _p, _p, _p, _c_int, _c_int, _c_int, _p]),
     "mi355_dsa_attn_fp8_dequant": (_c_int, [_p, _p, _p, _c_int, _c_int, _p]),
     "mi355_dsa_attn_fp8_quantize": (_c_int, [_p, _p, _p, _c_int, _c_int, _p]),

@@ -49,6 +49,8 @@
 //    their overlapping top-k sets hit in L2.
 #include <float.h>
 
+#include <mutex>
+
 #include "capi_internal.h"
 #include "dsa_common.h"
 
@@ -1752,6 +1754,66 @@ extern "C" int mi355_dsa_sparse_mla_decode(
   return mla_decode_impl(o, lse, q, B, n_head, kv_cache, kv_fp8, n_kv_rows, page_size, idx,
                          topk, block_table, max_blocks, seq_lens, scale, workspace,
                          workspace_bytes, stream, false);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of mi355_dsa_sparse_mla_decode.  Its split partials
+// live in a file-scope device array of kNoAllocScratchBytes instead of a
+// caller workspace.  Host code never uses the array's name as an address:
+// the device address comes from hipGetSymbolAddress, once per device, with
+// that device current, on the entry point's first call there.  Every call on
+// a device shares that device's array (the kernels write every partial they
+// read, so nothing needs clearing between calls); calls that overlap on one
+// device race on it.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kNoAllocMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kNoAllocMaxDevices];  // zero-initialised: not yet looked up
+
+static int noalloc_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+    return set_error(MI355_DSA_EHIP, "sparse_mla_decode_noalloc: no current HIP device");
+  if (dev >= kNoAllocMaxDevices)
+    return set_error(MI355_DSA_EINVAL, "sparse_mla_decode_noalloc: device %d >= %d", dev,
+                     kNoAllocMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return set_error(MI355_DSA_EHIP, "sparse_mla_decode_noalloc: scratch lookup failed: %s",
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MI355_DSA_OK;
+}
+
+extern "C" size_t mi355_dsa_sparse_mla_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int mi355_dsa_sparse_mla_decode_noalloc(
+    void* o, float* lse, const void* q, int B, int n_head, const void* kv_cache, int kv_fp8,
+    int64_t n_kv_rows, int page_size, const int32_t* idx, int topk,
+    const int32_t* block_table, int max_blocks, const int32_t* seq_lens, float scale,
+    void* stream) {
+  clear_error();
+  const size_t need = mi355_dsa_sparse_mla_workspace_size(B, n_head, topk);
+  DSA_CHECK(need <= kNoAllocScratchBytes,
+            "sparse_mla_decode_noalloc: B=%d x n_head=%d x topk=%d needs %zu bytes of split "
+            "scratch, more than its %zu-byte maximum; call mi355_dsa_sparse_mla_decode with a "
+            "workspace instead",
+            B, n_head, topk, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = noalloc_scratch(&ws);
+    if (rc != MI355_DSA_OK) return rc;
+  }
+  return mla_decode_impl(o, lse, q, B, n_head, kv_cache, kv_fp8, n_kv_rows, page_size, idx,
+                         topk, block_table, max_blocks, seq_lens, scale, ws, need, stream, false);
 }
 
 extern "C" size_t mi355_dsa_mla_decode_workspace_size(int B, int n_head, int max_kv) {

@@ -247,8 +247,12 @@ int mi355_dsa_persistent_topk(const float* score, int n_rows, int row_stride,
  *   s_j  = fp16(q[b,h,:] * fp16(scale)) . K_j      (576 dims)
  *   o    = sum_j softmax(s)_j V_j                   (V_j = K_j[0:512])
  *   lse  = max_j s_j + ln sum_j exp(s_j - max)      (-inf when no key valid)
- * over the selected keys j = idx[b,i] with 0 <= j < seq_len[b] and a
- * resolved row inside the cache.  q fp16 [B,H,576], o fp16 [B,H,512],
+ * over the selected keys j = idx[b,i] with 0 <= j < seq_len[b].  A selected
+ * key whose row does not resolve inside the cache (negative block, row past
+ * the cache) follows the reference's dispatch (:2511): for B >= 32 and
+ * H <= 16 it is masked and an empty token's lse is -1e30 (its prefill
+ * kernel, :1617-1628, :1789-1793); otherwise it is a zero key with score 0
+ * (its split-decode kernel, :970-992).  q fp16 [B,H,576], o fp16 [B,H,512],
  * lse fp32 [B,H], idx int32 [B,topk] (logical positions, -1 unused),
  * bt int32 [B,max_blocks], seq_lens int32 [B].  kv_fp8 == 0: fp16 rows of
  * 576 halves; kv_fp8 == 1: 656-byte fp8_ds_mla rows.
@@ -263,6 +267,31 @@ int mi355_dsa_sparse_mla_decode(void* o, float* lse, const void* q, int B,
                                 const int32_t* seq_lens, float scale,
                                 void* workspace, size_t workspace_bytes,
                                 void* stream);
+
+/*
+ * mi355_dsa_sparse_mla_decode without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid allocation).  It has no counterpart in the reference.  The
+ * split partials go to a library-owned device array of
+ * mi355_dsa_sparse_mla_noalloc_max_bytes() bytes (32 MiB) per device, held
+ * from the library's load until the process ends; a call needing more
+ * (mi355_dsa_sparse_mla_workspace_size(B, n_head, topk) larger than that,
+ * e.g. B > 31 at 64 heads and topk 2048) returns MI355_DSA_EINVAL and
+ * launches nothing.  Every call on one device shares that device's array:
+ * calls that overlap on one device (different streams) race and must be
+ * serialised by the caller.  Results equal mi355_dsa_sparse_mla_decode's bit
+ * for bit.  Neither entry point calls hipMalloc or hipFree.
+ */
+size_t mi355_dsa_sparse_mla_noalloc_max_bytes(void);
+int mi355_dsa_sparse_mla_decode_noalloc(void* o, float* lse, const void* q,
+                                        int B, int n_head,
+                                        const void* kv_cache, int kv_fp8,
+                                        int64_t n_kv_rows, int page_size,
+                                        const int32_t* idx, int topk,
+                                        const int32_t* block_table,
+                                        int max_blocks,
+                                        const int32_t* seq_lens, float scale,
+                                        void* stream);
 
 /*
  * fp8-e4m3 weight-only GEMV: y[m,n] = sum_k x[m,k] * e4m3(w[n,k]) * s[n/128,k/128]
