@@ -81,6 +81,7 @@ struct MlaParams {
   // 1: a key in range whose row does not resolve is a zero key with score 0
   // (row code -2); 0: such a key is masked (-1)
   int zero_unresolved;
+  int xcd_map;  // 1: decode workgroup order is XCD-aware (grid a multiple of 8)
 };
 
 template <int HW, int KW, int NB>
@@ -560,36 +561,41 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
 // ---------------------------------------------------------------------------
 // fp8_ds_mla split decode with LDS-DMA gathers.
 //
-// Workgroup = (split, 16-head group, token), 8 waves, at most two 64-key
-// chunks (128 keys) per split.  Aimed at the latency chain of a small
-// decode batch:
-//  * Q rows, idx and the token's block-table row are fetched together (the
-//    block table is staged in LDS), so resolving idx -> cache row costs no
-//    second dependent global round trip;
-//  * rows are gathered with global_load_lds_dwordx4 straight into LDS as
-//    raw 656-B rows (no staging registers, no conversion pass), both chunks
-//    in flight; masked keys read a zero row, so they carry finite zeros;
-//  * the e4m3 bytes become exact fp16 at operand load (16-byte reads for QK,
-//    ds_read_b64_tr_b8 transpose reads for the V^T operands of PV);
-//  * both chunks stay resident, so the softmax is exact two-phase:
-//      1. wave w computes S for keys 16(w%4) .. +15 of chunk w/4 (16 heads);
-//      2. split max / sum go through LDS and every wave writes its
-//         exp(S - M) into a [head][key] fp32 table;
-//      3. wave w computes O^T for value dims [64w, 64w+64) over all keys
-//         (v_mfma_f32_16x16x32_f16), so the waves' outputs are disjoint and
-//         need no merge; those dims lie in fp8 scale tile w/2, so P^T takes
-//         one scale per key.
+// Workgroup = (token, split, 16-head group), 8 waves, at most 128 keys per
+// split.  A small decode batch is a latency chain (idx -> block table ->
+// rows -> QK -> softmax -> PV -> partials, then the merge launch), so every
+// step is shortened:
+//  * each wave owns 16 keys of the split end to end: its lanes 0..15 load
+//    their idx entry, then that key's block-table entry (two small dependent
+//    loads; no table row is staged), and the wave gathers its own 16 raw
+//    656-B rows into its LDS region with global_load_lds_dwordx4; masked
+//    keys read a static zero row, so they carry finite zeros;
+//  * Q rows are fetched by LDS-DMA after the block-table loads are issued,
+//    so they overlap the row gathers instead of delaying the table lookup;
+//  * a wave starts its QK as soon as its own rows have landed (no barrier);
+//    the e4m3 bytes become exact fp16 at operand load;
+//  * softmax statistics are per wave (max and sum over its 16 keys); after
+//    the one barrier each wave rescales by exp(m_w - M) inside PV, where
+//    P^T already takes the key's tile scale;
+//  * wave w computes O^T for value dims [64w, 64w+64) over all 128 keys
+//    (ds_read_b64_tr_b8 transpose reads, v_mfma_f32_16x16x32_f16), so the
+//    waves' outputs are disjoint; the loop has no branch (absent keys are
+//    zero rows with P = 0).
+// Splits write fp16 normalised partials plus (m, l) with streaming stores;
+// sparse_mla_merge_kernel combines them.  Launch order is XCD-aware when the
+// grid is a multiple of 8: the head groups of a (token, split) share an XCD
+// and its L2 for the gathered rows, and a token's splits stay on few XCDs so
+// its Q is fetched by few L2s.
 // Barriers that must not wait for in-flight gathers are raw s_barrier with
 // an explicit LDS wait (__syncthreads would also drain the LDS-DMA queue).
 // ---------------------------------------------------------------------------
 constexpr int kDmaWaves = 8;
 constexpr int kDmaThreads = 64 * kDmaWaves;
-constexpr int kDmaKeys = 64;                                            // keys per chunk
-constexpr int kDmaPieces = kDmaKeys * (kDsmlaRowBytes / 16);            // 2624 16-B pieces
-constexpr int kDmaRounds = (kDmaPieces + kDmaThreads - 1) / kDmaThreads;  // 6 per thread
-constexpr int kDmaBufBytes = kDmaRounds * kDmaThreads * 16;             // one chunk buffer
-constexpr int kBtStage = 4096;                                           // block-table entries in LDS
-constexpr int kDmaSplitKeys = 2 * kDmaKeys;                              // keys per split (max)
+constexpr int kDecWaveKeys = 16;                                         // keys per wave
+constexpr int kDmaSplitKeys = kDecWaveKeys * kDmaWaves;                  // keys per split (max)
+constexpr int kDecWavePieces = kDecWaveKeys * (kDsmlaRowBytes / 16);    // 656 16-B pieces
+constexpr int kDecWaveRounds = (kDecWavePieces + 63) / 64;               // 11 LDS-DMA ops
+constexpr int kDecWaveBytes = kDecWaveKeys * kDsmlaRowBytes;            // 10496 B
 constexpr int kQPitchPieces = kLatentDim / 8 + 1;                        // 73 x 16 B: padded Q row
 constexpr int kQRounds = (16 * kQPitchPieces + kDmaThreads - 1) / kDmaThreads;  // 3
 constexpr int kPPitch = kDmaSplitKeys + 4;                               // fp32 P row pitch (floats)
@@ -599,11 +605,9 @@ constexpr int kTilesPerWave = kDimsPerWave / 16;                         // 4
 __device__ __align__(16) const uint8_t kZeroRow[kDsmlaRowBytes] = {};
 
 struct DmaSmem {
-  uint8_t buf[2][kDmaBufBytes];          // raw rows of the split's two chunks
-  int32_t bt[kBtStage];                  // the token's block-table row
+  uint8_t rows[kDmaWaves][kDecWaveBytes];  // raw rows: wave w's keys 16w .. 16w+15
   uint8_t q[kQRounds * kDmaThreads * 16];  // 16 Q rows (fp16, pitch 73 x 16 B)
-  float pt[16 * kPPitch];                // P[head][key] of the whole split
-  int32_t rows[kDmaSplitKeys];
+  float pt[16 * kPPitch];                  // P[head][key] of the split, exp(s - m_wave)
   float m[kDmaWaves * 16];
   float l[kDmaWaves * 16];
 };
@@ -620,43 +624,27 @@ __device__ __forceinline__ f16x4 e4m3x4_to_f16x4(uint32_t w) {
   return __builtin_bit_cast(f16x4, pk);
 }
 
-// Issues the LDS-DMA gather of one 64-key chunk (rows[0..64), -1 = masked)
-// into buf: piece q = 512u + 64*wave + lane lands at buf + 16q, i.e. key
-// q / 41, 16-byte chunk q % 41 of its 656-byte row.  Every thread issues
-// exactly kDmaRounds operations (padding pieces read the zero row).
-__device__ __forceinline__ void dma_chunk(const uint8_t* __restrict__ kv, const int32_t* rows,
-                                          uint8_t* buf) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  int row[kDmaRounds];
-#pragma unroll
-  for (int u = 0; u < kDmaRounds; u++) {  // all row lookups in flight together
-    const int q = kDmaThreads * u + 64 * wave + lane;
-    const int r = q / 41;
-    row[u] = rows[r < kDmaKeys ? r : 0];
-  }
-#pragma unroll
-  for (int u = 0; u < kDmaRounds; u++) {
-    const int q = kDmaThreads * u + 64 * wave + lane;
-    const int r = q / 41, ch = q - r * 41;
-    const bool ok = q < kDmaPieces && row[u] >= 0;
-    const uint8_t* src = ok ? kv + (int64_t)row[u] * kDsmlaRowBytes + 16 * ch
-                            : kZeroRow + 16 * (q < kDmaPieces ? ch : 0);
-    dma16(src, buf + 16 * (kDmaThreads * u + 64 * wave));
-  }
+// Global load of one dword issued as inline asm: the compiler does not count
+// it, so the caller's explicit s_waitcnt (which takes the value as an
+// operand) is the only wait, and LDS-DMA issued after it is not drained.
+__device__ __forceinline__ int load_dword_async(const int32_t* ptr) {
+  int v;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(ptr) : "memory");
+  return v;
 }
 
-// QK of one wave's 16 keys of a chunk of raw fp8_ds_mla rows: returns the
-// masked scores of keys kbase + 4g + r (r = 0..3, accumulator rows) for head
-// c, and in ksc those keys' four tile scales.
-template <bool BATCH_ALL = true>
-__device__ __forceinline__ f32x4 dma_qk(const uint8_t* cb, int kbase, const int32_t* rows,
-                                        const f16x8 (&qf)[18], f32x4 (&ksc)[4]) {
+// QK of one wave's 16 keys of raw fp8_ds_mla rows at cb: returns the scores
+// of keys 4g + r (r = 0..3, accumulator rows) for head c, -inf where
+// valid[r] is false.
+__device__ __forceinline__ f32x4 dma_qk(const uint8_t* cb, const f16x8 (&qf)[18],
+                                        const bool (&valid)[4]) {
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
   // All LDS operands are read first (in-order returns let each MFMA wait only
   // for its own operand).
-  const uint8_t* krow = cb + (kbase + c) * kDsmlaRowBytes;
+  const uint8_t* krow = cb + c * kDsmlaRowBytes;
   u32x4 kraw[8];
   f16x8 krope[2];
+  f32x4 ksc[4];
 #pragma unroll
   for (int s2 = 0; s2 < 8; s2++) kraw[s2] = *reinterpret_cast<const u32x4*>(krow + 64 * s2 + 16 * g);
 #pragma unroll
@@ -664,9 +652,8 @@ __device__ __forceinline__ f32x4 dma_qk(const uint8_t* cb, int kbase, const int3
     krope[s3] = *reinterpret_cast<const f16x8*>(krow + 528 + 64 * s3 + 16 * g);
 #pragma unroll
   for (int r = 0; r < 4; r++)
-    ksc[r] = *reinterpret_cast<const f32x4*>(cb + (kbase + 4 * g + r) * kDsmlaRowBytes + 512);
-  const int4 vr = *reinterpret_cast<const int4*>(rows + kbase + 4 * g);
-  if constexpr (BATCH_ALL) __builtin_amdgcn_sched_barrier(0);
+    ksc[r] = *reinterpret_cast<const f32x4*>(cb + (4 * g + r) * kDsmlaRowBytes + 512);
+  __builtin_amdgcn_sched_barrier(0);
   f32x4 acc[5];
 #pragma unroll
   for (int a = 0; a < 5; a++) acc[a] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -688,12 +675,11 @@ __device__ __forceinline__ f32x4 dma_qk(const uint8_t* cb, int kbase, const int3
     }
   }
   f32x4 sv;
-  const int vv[4] = {vr.x, vr.y, vr.z, vr.w};
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const float v = acc[4][r] + ksc[r][0] * acc[0][r] + ksc[r][1] * acc[1][r] +
                     ksc[r][2] * acc[2][r] + ksc[r][3] * acc[3][r];
-    sv[r] = vv[r] != -1 ? v : -INFINITY;  // -2: zero row, a valid key
+    sv[r] = valid[r] ? v : -INFINITY;
   }
   return sv;
 }
@@ -704,20 +690,39 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const int split = blockIdx.x, h0 = blockIdx.y * 16, b = blockIdx.z;
+  // work item: head group fastest, then split, then token; with the XCD
+  // mapping, consecutive items share an XCD (workgroup i runs on XCD i % 8)
+  const int G = (p.n_head + 15) / 16;
+  const int nwg = (int)gridDim.x;
+  const int item = p.xcd_map ? ((int)blockIdx.x % 8) * (nwg / 8) + (int)blockIdx.x / 8
+                             : (int)blockIdx.x;
+  const int h0 = (item % G) * 16;
+  const int split = (item / G) % p.n_splits;
+  const int b = item / (G * p.n_splits);
   const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
   const int seq_len = p.seq_lens[b];
 
-  // this split's key range: at most kDmaSplitKeys keys (host-guaranteed)
-  const int n_chunks_all = (p.topk + kDmaKeys - 1) / kDmaKeys;
-  const int cps = (n_chunks_all + p.n_splits - 1) / p.n_splits;
-  const int key_lo = min(split * cps * kDmaKeys, p.topk);
-  const int nkeys = min(key_lo + cps * kDmaKeys, p.topk) - key_lo;
-  const int nchunks = (nkeys + kDmaKeys - 1) / kDmaKeys;  // 0, 1 or 2
-  const bool bt_in_lds = p.max_blocks >= 1 && p.max_blocks <= kBtStage;
-  const int32_t* bt_row = p.bt + (int64_t)b * p.max_blocks;
+  // this split's key range: a multiple of 16 keys, at most kDmaSplitKeys
+  // (host-guaranteed), and this wave's 16 of them
+  const int kps = ((p.topk + 15) / 16 + p.n_splits - 1) / p.n_splits * 16;
+  const int key_lo = min(split * kps, p.topk);
+  const int nkeys = min(key_lo + kps, p.topk) - key_lo;
+  const int nk_w = min(max(nkeys - kDecWaveKeys * w, 0), kDecWaveKeys);
 
-  // ---- independent loads: Q rows (LDS-DMA), idx, block-table row ----
+  // ---- idx -> block table -> cache row for this wave's key of lane jl ----
+  const int jl = lane & 15;
+  const bool kval = jl < nk_w;
+  const int32_t* ip = p.idx + (int64_t)b * p.topk + (kval ? key_lo + kDecWaveKeys * w + jl : 0);
+  int pos = load_dword_async(ip);
+  asm volatile("s_waitcnt vmcnt(0)" : "+v"(pos)::"memory");
+  pos = kval ? pos : -1;
+  const bool in_range = pos >= 0 && pos < seq_len;
+  const int pg = in_range ? (p.page_shift >= 0 ? pos >> p.page_shift : pos / p.page_size) : 0;
+  const bool in_table = in_range && pg < p.max_blocks;
+  // a key outside the table re-reads its own idx entry (a valid address)
+  int blk = load_dword_async(in_table ? p.bt + (int64_t)b * p.max_blocks + pg : ip);
+
+  // ---- Q rows (LDS-DMA), issued behind the block-table load ----
   {
     const uint8_t* qb = reinterpret_cast<const uint8_t*>(p.q + (int64_t)b * p.n_head * kLatentDim);
 #pragma unroll
@@ -729,40 +734,35 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
       dma16(qb + (int64_t)hq * kLatentDim * 2 + 16 * chq, sh.q + 16 * (kDmaThreads * u + 64 * w));
     }
   }
-  static_assert(kDmaSplitKeys <= kDmaThreads, "one key per thread");
-  const int jk = threadIdx.x;  // the key this thread resolves
-  const int pos = (jk < nkeys) ? p.idx[(int64_t)b * p.topk + key_lo + jk] : -1;
-  if (bt_in_lds) {
-    constexpr int BTU = kBtStage / kDmaThreads;
-    int btv[BTU];
-#pragma unroll
-    for (int u = 0; u < BTU; u++) {
-      const int i = threadIdx.x + kDmaThreads * u;
-      if (kDmaThreads * u < p.max_blocks) btv[u] = bt_row[i < p.max_blocks ? i : 0];
-    }
-#pragma unroll
-    for (int u = 0; u < BTU; u++)
-      if (kDmaThreads * u < p.max_blocks) sh.bt[threadIdx.x + kDmaThreads * u] = btv[u];
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  lds_barrier();
+  asm volatile("s_waitcnt vmcnt(%1)" : "+v"(blk) : "n"(kQRounds) : "memory");  // table entry landed
+  blk = in_table ? blk : -1;
+  const int64_t row = (int64_t)blk * p.page_size + (pos - pg * p.page_size);
+  const int code = (blk >= 0 && row < p.n_kv_rows) ? (int)row
+                                                   : ((in_table && p.zero_unresolved) ? -2 : -1);
 
-  // ---- resolve idx -> cache row (masked keys and chunk padding: -1) ----
-  if (jk < kDmaSplitKeys) {
-    const int pg = (pos >= 0) ? (p.page_shift >= 0 ? pos >> p.page_shift : pos / p.page_size) : 0;
-    const bool ok = jk < nkeys && pos >= 0 && pos < seq_len && pg < p.max_blocks;
-    const int blk = ok ? (bt_in_lds ? sh.bt[pg] : bt_row[pg]) : -1;
-    const int64_t row = (int64_t)blk * p.page_size + (pos - pg * p.page_size);
-    sh.rows[jk] = (blk < 0 || row >= p.n_kv_rows) ? ((ok && p.zero_unresolved) ? -2 : -1)
-                                                   : (int32_t)row;
+  // ---- this wave's 16 raw rows into its LDS region: piece q = 64u + lane
+  // is key q / 41, 16-byte chunk q % 41 (the last round has 16 pieces) ----
+  uint8_t* reg = sh.rows[w];
+#pragma unroll
+  for (int u = 0; u < kDecWaveRounds; u++) {
+    const int q = 64 * u + lane;
+    const int r = (q < kDecWavePieces ? q : 0) / 41, ch = q - r * 41;
+    const int rc = __shfl(code, r, 64);
+    const uint8_t* src = rc >= 0 ? kv + (int64_t)rc * kDsmlaRowBytes + 16 * ch
+                                 : kZeroRow + 16 * (q < kDecWavePieces ? ch : 0);
+    if (u + 1 < kDecWaveRounds || lane < kDecWavePieces - 64 * (kDecWaveRounds - 1))
+      dma16(src, reg + 1024 * u);
   }
-  lds_barrier();
-  if (nchunks > 0) dma_chunk(kv, sh.rows, sh.buf[0]);
-  if (nchunks > 1) dma_chunk(kv, sh.rows + kDmaKeys, sh.buf[1]);
+  // validity of keys 4g + r (the accumulator rows of this lane)
+  bool valid[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) valid[r] = __shfl(code, 4 * g + r, 64) != -1;
 
   // ---- Q fragments (B operand of S^T = K Q^T), scaled in fp16 ----
   // step 2s'+e2 (s' < 8): lane group g holds dims 64s' + 16g + 8e2 .. +7
   // step 16+s'':          lane group g holds dims 512 + 32s'' + 8g .. +7
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDecWaveRounds) : "memory");  // this wave's Q pieces
+  lds_barrier();                                                          // everyone's
   f16x8 qf[18];
   {
     const f16* qr = reinterpret_cast<const f16*>(sh.q + c * kQPitchPieces * 16);
@@ -778,43 +778,38 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
       qf[16 + s3] = *reinterpret_cast<const f16x8*>(qr + 512 + 32 * s3 + 8 * g) * sc8;
   }
 
-  // ---- S for this wave's 16 keys: chunk w/4, keys 16(w%4) .. +15 ----
-  const int my_chunk = w >> 2, kbase = 16 * (w & 3);
+  // ---- S for this wave's keys, as soon as its own rows have landed ----
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  lds_barrier();
-  f32x4 sv = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  if (my_chunk < nchunks) {
-    f32x4 ksc[4];
-    sv = dma_qk(sh.buf[my_chunk], kbase, sh.rows + my_chunk * kDmaKeys, qf, ksc);
-  }
+  const f32x4 sv = dma_qk(reg, qf, valid);
 
-  // ---- softmax statistics of the split (per head c) ----
+  // ---- per-wave softmax statistics (per head c) ----
   float mt = -1e30f;
 #pragma unroll
   for (int r = 0; r < 4; r++) mt = fmaxf(mt, sv[r]);
   mt = fmaxf(mt, shfl_xor_f(mt, 16));
   mt = fmaxf(mt, shfl_xor_f(mt, 32));
-  if (g == 0) sh.m[w * 16 + c] = mt;
-  lds_barrier();
-  float M = sh.m[c];
-#pragma unroll
-  for (int w2 = 1; w2 < kDmaWaves; w2++) M = fmaxf(M, sh.m[w2 * 16 + c]);
   f32x4 pr;
   float ls = 0.f;
 #pragma unroll
   for (int r = 0; r < 4; r++) {
-    pr[r] = (sv[r] > -INFINITY) ? __expf(sv[r] - M) : 0.f;
+    pr[r] = (sv[r] > -INFINITY) ? __expf(sv[r] - mt) : 0.f;
     ls += pr[r];
   }
   ls += shfl_xor_f(ls, 16);
   ls += shfl_xor_f(ls, 32);
-  if (g == 0) sh.l[w * 16 + c] = ls;
-  // P[head c][key]: keys 64 * my_chunk + kbase + 4g + r
-  *reinterpret_cast<f32x4*>(&sh.pt[c * kPPitch + my_chunk * kDmaKeys + kbase + 4 * g]) = pr;
+  if (g == 0) {
+    sh.m[w * 16 + c] = mt;
+    sh.l[w * 16 + c] = ls;
+  }
+  // P[head c][key]: keys 16w + 4g + r
+  *reinterpret_cast<f32x4*>(&sh.pt[c * kPPitch + kDecWaveKeys * w + 4 * g]) = pr;
   lds_barrier();
+  float M = -1e30f;
+#pragma unroll
+  for (int w2 = 0; w2 < kDmaWaves; w2++) M = fmaxf(M, sh.m[w2 * 16 + c]);
   float L = 0.f;
 #pragma unroll
-  for (int w2 = 0; w2 < kDmaWaves; w2++) L += sh.l[w2 * 16 + c];
+  for (int w2 = 0; w2 < kDmaWaves; w2++) L += __expf(sh.m[w2 * 16 + c] - M) * sh.l[w2 * 16 + c];
 
   // ---- O^T[dims 64w .. +64][head] over the split's keys ----
   const int st = (kDimsPerWave * w) / 128;  // fp8 scale tile of these dims
@@ -823,21 +818,22 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
   for (int t = 0; t < kTilesPerWave; t++) oacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kb = 0; kb < kDmaSplitKeys / 32; kb++) {
-    if (kb * 32 >= nchunks * kDmaKeys) break;  // uniform
-    const uint8_t* cb = sh.buf[kb >> 1];
-    const int k0 = (kb & 1) * 32;  // first key of the block inside its chunk
-    // P^T operand: keys k0 + 8g + e of head c, times the key's scale of tile st
+    // keys 32kb + 8g .. +7 are rows 8(g & 1) .. +7 of wave region 2kb + g/2
+    const int src_w = 2 * kb + (g >> 1);
+    const uint8_t* cb = sh.rows[src_w] + 8 * (g & 1) * kDsmlaRowBytes;
+    // P^T operand: keys 32kb + 8g + e of head c, times the key's scale of
+    // tile st and the source wave's rescale factor
     const f32x4 pa = *reinterpret_cast<const f32x4*>(&sh.pt[c * kPPitch + 32 * kb + 8 * g]);
     const f32x4 pc = *reinterpret_cast<const f32x4*>(&sh.pt[c * kPPitch + 32 * kb + 8 * g + 4]);
+    const float alpha = __expf(sh.m[src_w * 16 + c] - M);  // the source wave's rescale factor
     float ks[8];
 #pragma unroll
     for (int e = 0; e < 8; e++)
-      ks[e] = *reinterpret_cast<const float*>(cb + (k0 + 8 * g + e) * kDsmlaRowBytes + 512 + 4 * st);
-    // V^T transpose reads: lane i of a 16-lane group points at key
-    // k0 + 8g + i/2, dims 64w + 16t + 8(i%2); lane j receives the 8 keys
-    // k0 + 8g .. +7 at dim 64w + 16t + j
-    const uint8_t* vsrc =
-        cb + (k0 + 8 * g + (c >> 1)) * kDsmlaRowBytes + kDimsPerWave * w + 8 * (c & 1);
+      ks[e] = *reinterpret_cast<const float*>(cb + e * kDsmlaRowBytes + 512 + 4 * st) * alpha;
+    // V^T transpose reads: lane i of a 16-lane group points at key 8g + i/2
+    // of the block, dims 64w + 16t + 8(i%2); lane j receives the 8 keys
+    // 8g .. +7 at dim 64w + 16t + j
+    const uint8_t* vsrc = cb + (c >> 1) * kDsmlaRowBytes + kDimsPerWave * w + 8 * (c & 1);
     s32x2 vt[kTilesPerWave];
 #pragma unroll
     for (int t = 0; t < kTilesPerWave; t++)
@@ -1560,20 +1556,20 @@ static bool use_prefill_config(int B, int n_head) {
   return (int64_t)B * ((n_head + 63) / 64) >= kTargetWGs;
 }
 
-// fp8 decode with LDS-DMA gathers: every split holds at most two 64-key
-// chunks, so the split count is raised to ceil(topk / 128) when needed.
+// fp8 decode with LDS-DMA gathers: every split holds at most 128 keys (16
+// per wave), so the split count is raised to ceil(topk / 128) when needed.
 static bool use_dma_decode(int topk) {
   return (topk + kDmaSplitKeys - 1) / kDmaSplitKeys <= kMergeMaxSplits;
 }
 
 static int dma_decode_splits(int B, int n_head, int topk) {
   const int hg = (n_head + 15) / 16;
-  const int chunks = (topk + kDmaKeys - 1) / kDmaKeys;
+  const int units = (topk + kDecWaveKeys - 1) / kDecWaveKeys;  // 16-key units
   int s = kTargetWGs / (B * hg > 0 ? B * hg : 1);
-  if (s >= 8) s = s / 8 * 8;  // a (token, split)'s head groups then share an XCD
-  const int min_s = (chunks + 1) / 2;  // <= 2 chunks per split
+  if (s >= 8) s = s / 8 * 8;
+  const int min_s = (topk + kDmaSplitKeys - 1) / kDmaSplitKeys;  // <= 128 keys per split
   if (s < min_s) s = min_s;
-  if (s > chunks) s = chunks;
+  if (s > units) s = units;
   if (s < 1) s = 1;
   return s;
 }
@@ -1684,6 +1680,7 @@ static int mla_decode_impl(
   // kernel masks it (:1617-1628, :1705), its split-decode and dense kernels
   // read a zero row that keeps score 0 (:970-992, :762-771)
   prm.zero_unresolved = (dense || !(B >= 32 && n_head <= 16)) ? 1 : 0;
+  prm.xcd_map = 0;
   hipStream_t st = as_stream(stream);
 
   if (dense) {
@@ -1733,7 +1730,10 @@ static int mla_decode_impl(
     const int rc2 = reserve_lds(reinterpret_cast<const void*>(sparse_mla_decode_dma_kernel),
                                 sizeof(DmaSmem), "sparse_mla_decode_dma");
     if (rc2) return rc2;
-    sparse_mla_decode_dma_kernel<<<grid, kDmaThreads, sizeof(DmaSmem), st>>>(prm);
+    const int64_t nwg = (int64_t)S * ((n_head + 15) / 16) * B;
+    DSA_CHECK(nwg < ((int64_t)1 << 31), "sparse_mla_decode: grid too large");
+    prm.xcd_map = (nwg % 8 == 0) ? 1 : 0;
+    sparse_mla_decode_dma_kernel<<<dim3((unsigned)nwg), kDmaThreads, sizeof(DmaSmem), st>>>(prm);
     rc = check_launch("sparse_mla_decode");
   } else {
     rc = kv_fp8 ? launch_mla<true, 1, kDecKW, 1>(prm, grid, st)
