@@ -145,6 +145,52 @@ def bench_decode(torch, pkg, dev, ctx, layers, steps, warmup, seed=3):
     return ms, d, idxs, qs
 
 
+def bench_decode_batch(torch, pkg, dev, B, layers, steps, warmup, ctx=184320, seed=11):
+    """C3's decode at batch B (64 heads, topk 2048, 180k context per token,
+    fp8_ds_mla): the tokens' block tables draw pages from one shared pool of
+    at most 8 GB, so every layer's gathered rows come from HBM; `layers`
+    layers with their own q and idx are replayed from one HIP graph."""
+    S = pkg.synthetic
+    ops = pkg._sm70_ops
+    page = 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    bps = ctx // page
+    pool = min(B * bps, (8 << 30) // (656 * page))
+    kv = S.latent_cache(pool * page, True, g, dev)
+    bt = torch.randint(0, pool, (B, bps), generator=g, device=dev, dtype=torch.int32)
+    seq = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    idxs = [S.sorted_unique_positions(B, 2048, ctx, g, dev) for _ in range(layers)]
+    qs = [(torch.randn(B, 64, 576, generator=g, device=dev) / 24.0).to(torch.float16)
+          for _ in range(layers)]
+    o = torch.empty(B, 64, 512, dtype=torch.float16, device=dev)
+    lse = torch.empty(B, 64, device=dev)
+
+    def run():
+        for l in range(layers):
+            ops.sm70_sparse_mla_decode(o, lse, qs[l], kv, idxs[l], bt, seq, 576 ** -0.5)
+
+    graph = capture(torch, run)
+    ms = time_graph(torch, graph, steps, warmup)
+    del graph
+    us = ms * 1000.0 / (steps * layers)
+    nbytes = B * 2048 * 656 + B * 64 * (576 + 512) * 2 + B * 64 * 4 + B * 2048 * 8
+    gbps = nbytes / (us * 1e-6) / 1e9
+    flops = B * 64 * 2048 * (576 + 512) * 2
+    return {"us_per_layer": round(us, 2), "gbps": round(gbps, 1),
+            "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4),
+            "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+            "frac_fp16_peak": round(flops / (us * 1e-6) / 1e12 / FP16_PEAK_TFLOPS, 4),
+            "layers": layers}
+
+
+def decode_splits(pkg, B, H=64, topk=2048):
+    """Split count the library runs for a decode batch (from its workspace
+    size: B * H * splits * (512 fp16 + 2 fp32) bytes; 1 when none)."""
+    ws = pkg._lib.lib().mi355_dsa_sparse_mla_workspace_size(B, H, topk)
+    return max(1, ws // (B * H * 1032))
+
+
 def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
     """Config C4 indexer: packed-Q logits over a causal 64k prefill, in the
     caller's sub-chunks (reference/sparse_attn_indexer.py:764-881)."""
@@ -185,7 +231,7 @@ def bench_indexer_prefill(torch, pkg, dev, T=65536, sub=128, steps=3, warmup=1):
 
 
 SPARSE_PREFILL_T = 65536
-EXTRAS = ("sweep", "indexer_prefill", "sparse_prefill", "indexer_decode", "gemv", "k_store",
+EXTRAS = ("sweep", "batch_sweep", "indexer_prefill", "sparse_prefill", "indexer_decode", "gemv", "k_store",
           "dsa_layer", "dense_decode", "varlen_prefill", "shard_merge", "c1", "prefill_topk",
           "dsa_layer_prefill")
 
@@ -761,6 +807,9 @@ def main():
                          "11520 pages), one step = %d layers replayed from a HIP graph" % L),
             "batch": 4, "heads": 64, "topk": 2048, "ctx": 184320, "kv": "fp8_ds_mla",
             "layers_per_step": L,
+            # the library's split count at this shape (BASELINE C3 names 8; results
+            # are split-invariant, tested); each split is one 128-key workgroup
+            "splits": decode_splits(pkg, 4),
         },
         "hbm_gbps": round(gbps, 1),
         "tflops": round(tflops, 2),
@@ -790,6 +839,15 @@ def main():
         sweep["184320"] = line["value"]
         line["ctx_sweep_us_per_layer"] = sweep
         log(f"ctx sweep: {sweep}")
+    if "batch_sweep" in extras:
+        bs = {}
+        for B, layers in ((4, 78), (16, 40), (64, 12), (128, 6), (256, 4)):
+            r = bench_decode_batch(torch, pkg, dev, B, layers, max(args.steps // 2, 4), 2)
+            r["splits"] = decode_splits(pkg, B)
+            bs[str(B)] = r
+            torch.cuda.empty_cache()
+            log(f"decode batch {B}: {r}")
+        line["decode_batch_sweep"] = bs
     if "indexer_prefill" in extras:
         pms, pflops = bench_indexer_prefill(torch, pkg, dev)
         ptf = pflops / (pms * 1e-3) / 1e12

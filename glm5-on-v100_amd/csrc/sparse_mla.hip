@@ -994,8 +994,14 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
     b = xcd * per + (xcd < rem ? xcd : rem) + j;
   }
   const int hbase = blockIdx.y * 64;
+  const int split = blockIdx.z;
   const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
   const int seq_len = p.seq_lens[b];
+  // this workgroup's keys: split `split` of n_splits, whole 32-key tiles
+  const int kps = ((p.topk + p.n_splits - 1) / p.n_splits + kPfTileKeys - 1) / kPfTileKeys *
+                  kPfTileKeys;
+  const int k_lo = min(split * kps, p.topk);
+  const int k_hi = min(k_lo + kps, p.topk);
 
   // ---- Q of all 64 heads for this wave's QK dims, scaled in fp16 ----
   // NoPE step s: lane (head c of group hg, g) holds dims 128 qd + 32 g + 8 s .. +8
@@ -1139,8 +1145,8 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
     }
   };
 
-  for (int seg_lo = 0; seg_lo < p.topk; seg_lo += kSegKeys) {
-    const int nkeys = min(p.topk - seg_lo, kSegKeys);
+  for (int seg_lo = k_lo; seg_lo < k_hi; seg_lo += kSegKeys) {
+    const int nkeys = min(k_hi - seg_lo, kSegKeys);
     const int ntiles = (nkeys + kPfTileKeys - 1) / kPfTileKeys;
     lds_barrier();  // previous segment done with rows and the ring
     // ---- resolve idx -> block table -> row for the segment, batched ----
@@ -1195,12 +1201,21 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
     }
   }
 
-  // ---- l and lse per head, then o = O / l ----
+  // ---- outputs: o = O / l and lse, or the split's partial ----
+  const bool final_out = (p.n_splits == 1);
   if (sm_k == 0) {
     reinterpret_cast<float*>(&sh.lsum[sm_h & 15])[sm_h >> 4] = l_run;
     const int h = hbase + sm_h;
-    if (h < p.n_head)
-      p.lse[(int64_t)b * p.n_head + h] = (l_run > 0.f) ? (m_run + logf(l_run)) : p.empty_lse;
+    if (h < p.n_head) {
+      const int64_t bh = (int64_t)b * p.n_head + h;
+      if (final_out) {
+        p.lse[bh] = (l_run > 0.f) ? (m_run + logf(l_run)) : p.empty_lse;
+      } else {
+        const int64_t ps = bh * p.n_splits + split;
+        p.part_ml[ps * 2 + 0] = m_run;
+        p.part_ml[ps * 2 + 1] = l_run;
+      }
+    }
   }
   lds_barrier();
   const f32x4 L = sh.lsum[c];
@@ -1208,8 +1223,10 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
   for (int hg = 0; hg < 4; hg++) {
     const int h = hbase + 16 * hg + c;
     if (h >= p.n_head) continue;
+    const int64_t bh = (int64_t)b * p.n_head + h;
     const float inv = (L[hg] > 0.f) ? 1.f / L[hg] : 0.f;
-    f16* orow = p.o + ((int64_t)b * p.n_head + h) * kValueDim + 64 * w;
+    f16* orow = (final_out ? p.o + bh * kValueDim
+                           : p.part_o + (bh * p.n_splits + split) * kValueDim) + 64 * w;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
       f16x4 v;
@@ -1552,9 +1569,8 @@ __global__ void __launch_bounds__(128) sparse_mla_merge_kernel(
 constexpr int kDecKW = 4;        // decode: key-waves per workgroup
 constexpr int kTargetWGs = 256;  // one wave of workgroups over 256 CUs
 
-static bool use_prefill_config(int B, int n_head) {
-  return (int64_t)B * ((n_head + 63) / 64) >= kTargetWGs;
-}
+constexpr int kPipeMinUnits = 8;  // 64-head workgroups from which a batch of > 32 heads
+                                  // takes the pipelined kernels with a key split
 
 // fp8 decode with LDS-DMA gathers: every split holds at most 128 keys (16
 // per wave), so the split count is raised to ceil(topk / 128) when needed.
@@ -1620,16 +1636,41 @@ static int launch_mla(const MlaParams& prm, dim3 grid, hipStream_t st) {
 
 using namespace mi355dsa;
 
-static int splits_for(int B, int n_head, int topk, int kv_fp8) {
-  return (kv_fp8 && use_dma_decode(topk)) ? dma_decode_splits(B, n_head, topk)
-                                          : decode_splits(B, n_head, topk);
+// Which kernel runs a sparse attention call, and over how many key splits:
+//  * kPipelined: the 64-head pipelined kernels (fp8: sparse_mla_prefill_fp8_
+//    kernel, fp16: mla_attn_f16_kernel), workgroup = (token, 64 heads, key
+//    split), tiles streamed through an LDS ring.  Taken from 256 64-head
+//    workgroups up (one split), and for > 32 heads from kPipeMinUnits up
+//    with round(256 / units) splits of at least two 32-key tiles each;
+//  * kSplitDma: fp8 split decode with per-wave LDS-DMA gathers (16 heads per
+//    workgroup, at most 128 keys per split), for small batches;
+//  * kSplitReg: the register-staged split decode (fp16 rows, or fp8 top-k
+//    lists too long for kSplitDma).
+enum DecodeKind { kPipelined, kSplitDma, kSplitReg };
+struct DecodePlan {
+  DecodeKind kind;
+  int S;
+};
+
+static DecodePlan plan_decode(int B, int n_head, int topk, int kv_fp8) {
+  const int64_t units = (int64_t)B * ((n_head + 63) / 64);
+  if (units >= kTargetWGs) return {kPipelined, 1};
+  if (n_head > 32 && units >= kPipeMinUnits) {
+    int s = (int)((kTargetWGs + units / 2) / units);  // nearest: fewer partial second rounds
+    const int max_s = (topk + 2 * kPfTileKeys - 1) / (2 * kPfTileKeys);  // >= 2 tiles per split
+    if (s > max_s) s = max_s;
+    if (s > kMergeMaxSplits) s = kMergeMaxSplits;
+    if (s < 1) s = 1;
+    return {kPipelined, s};
+  }
+  if (kv_fp8 && use_dma_decode(topk)) return {kSplitDma, dma_decode_splits(B, n_head, topk)};
+  return {kSplitReg, decode_splits(B, n_head, topk)};
 }
 
 extern "C" size_t mi355_dsa_sparse_mla_workspace_size(int B, int n_head, int topk) {
   if (B <= 0 || n_head <= 0 || topk <= 0) return 0;
-  if (use_prefill_config(B, n_head)) return 0;
   // the larger of the fp16 and fp8 split counts, so one size serves both
-  const int s16 = splits_for(B, n_head, topk, 0), s8 = splits_for(B, n_head, topk, 1);
+  const int s16 = plan_decode(B, n_head, topk, 0).S, s8 = plan_decode(B, n_head, topk, 1).S;
   const int S = s16 > s8 ? s16 : s8;
   if (S <= 1) return 0;
   return (size_t)B * n_head * S * (kValueDim * sizeof(f16) + 2 * sizeof(float));
@@ -1653,7 +1694,8 @@ static int mla_decode_impl(
   DSA_CHECK(max_blocks == 0 || block_table, "null block_table");
   DSA_CHECK(aligned_to(q, 16) && aligned_to(kv_cache, 16) && aligned_to(o, 8),
             "q / kv_cache / o misaligned");
-  DSA_CHECK(B <= 65535 || use_prefill_config(B, n_head), "B too large");
+  DSA_CHECK(B <= 65535 || dense || plan_decode(B, n_head, topk, kv_fp8).kind == kPipelined,
+            "B too large");
   MlaParams prm;
   prm.q = reinterpret_cast<const f16*>(q);
   prm.kv = kv_cache;
@@ -1701,20 +1743,8 @@ static int mla_decode_impl(
     return check_launch("sparse_mla_merge");
   }
 
-  if (use_prefill_config(B, n_head)) {
-    prm.n_splits = 1;
-    const dim3 grid(B, (n_head + 63) / 64);
-    if (kv_fp8) {
-      const int rc = reserve_lds(reinterpret_cast<const void*>(sparse_mla_prefill_fp8_kernel),
-                                 sizeof(P3Smem), "sparse_mla_prefill_fp8");
-      if (rc) return rc;
-      sparse_mla_prefill_fp8_kernel<<<grid, kPfThreads, sizeof(P3Smem), st>>>(prm);
-      return check_launch("sparse_mla_decode");
-    }
-    return launch_attn_f16(prm, dim3(B, (n_head + 63) / 64, 1), st);
-  }
-  const bool dma = kv_fp8 && !dense && use_dma_decode(topk);
-  const int S = splits_for(B, n_head, topk, kv_fp8);
+  const DecodePlan plan = plan_decode(B, n_head, topk, kv_fp8);
+  const int S = plan.S;
   prm.n_splits = S;
   if (S > 1) {
     const size_t need = mi355_dsa_sparse_mla_workspace_size(B, n_head, topk);
@@ -1726,7 +1756,18 @@ static int mla_decode_impl(
   }
   const dim3 grid(S, (n_head + 15) / 16, B);
   int rc;
-  if (dma) {
+  if (plan.kind == kPipelined) {
+    const dim3 pgrid(B, (n_head + 63) / 64, S);
+    if (kv_fp8) {
+      rc = reserve_lds(reinterpret_cast<const void*>(sparse_mla_prefill_fp8_kernel),
+                       sizeof(P3Smem), "sparse_mla_prefill_fp8");
+      if (rc) return rc;
+      sparse_mla_prefill_fp8_kernel<<<pgrid, kPfThreads, sizeof(P3Smem), st>>>(prm);
+      rc = check_launch("sparse_mla_decode");
+    } else {
+      rc = launch_attn_f16(prm, pgrid, st);
+    }
+  } else if (plan.kind == kSplitDma) {
     const int rc2 = reserve_lds(reinterpret_cast<const void*>(sparse_mla_decode_dma_kernel),
                                 sizeof(DmaSmem), "sparse_mla_decode_dma");
     if (rc2) return rc2;

@@ -276,7 +276,8 @@ int mi355_dsa_sparse_mla_decode(void* o, float* lse, const void* q, int B,
  * mi355_dsa_sparse_mla_noalloc_max_bytes() bytes (32 MiB) per device, held
  * from the library's load until the process ends; a call needing more
  * (mi355_dsa_sparse_mla_workspace_size(B, n_head, topk) larger than that,
- * e.g. B > 31 at 64 heads and topk 2048) returns MI355_DSA_EINVAL and
+ * e.g. B >= 128 at 16 heads and topk 2048; no 64-head shape at topk 2048)
+ * returns MI355_DSA_EINVAL and
  * launches nothing.  Every call on one device shares that device's array:
  * calls that overlap on one device (different streams) race and must be
  * serialised by the caller.  Results equal mi355_dsa_sparse_mla_decode's bit

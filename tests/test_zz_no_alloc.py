@@ -59,8 +59,11 @@ def call(lib, noalloc, q, kv, idx, bt, seq):
 
 @pytest.mark.parametrize("fp8", [True, False], ids=["fp8", "fp16"])
 def test_noalloc_equals_workspace_entry_point(lib, dev, fp8):
-    # first call: C3's shape at a shorter context; second call: smaller
-    for seed, B, H, ctx, topk in ((1, 4, 64, 6000, 2048), (2, 2, 16, 900, 512)):
+    # calls in a row, each needing less scratch than the one before: a 16-token
+    # batch (64-head pipelined kernel, 16 key splits), C3's shape at a shorter
+    # context (split decode), a small 16-head call
+    for seed, B, H, ctx, topk in ((3, 16, 64, 3000, 2048), (1, 4, 64, 6000, 2048),
+                                  (2, 2, 16, 900, 512)):
         ins = inputs(seed, B, H, ctx, topk, fp8, dev)
         o1, l1 = call(lib, True, *ins)
         o2, l2 = call(lib, False, *ins)
@@ -72,7 +75,7 @@ def test_noalloc_equals_workspace_entry_point(lib, dev, fp8):
 def test_noalloc_rejects_oversize(lib, dev):
     cap = lib.mi355_dsa_sparse_mla_noalloc_max_bytes()
     assert cap == 32 << 20
-    B, H, topk = 64, 64, 2048
+    B, H, topk = 128, 16, 2048  # 16 splits of the 16-head split decode: 33.8 MB
     assert lib.mi355_dsa_sparse_mla_workspace_size(B, H, topk) > cap
     rc = lib.mi355_dsa_sparse_mla_decode_noalloc(None, None, None, B, H, None, 1, 0, 64, None,
                                                  topk, None, 1, None, SCALE, None)
