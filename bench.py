@@ -751,6 +751,145 @@ def cpu_baseline(torch, d, idxs, qs, budget_s):
     return el / n * 1e6, n
 
 
+def cpu_threads():
+    """Host threads for the CPU legs: the cores this process may run on
+    (sched_getaffinity), capped by OMP_NUM_THREADS when the box sets it (its
+    CPU share for one GPU)."""
+    aff = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    n = min(aff, int(omp)) if omp and omp.isdigit() and int(omp) > 0 else aff
+    return n, aff
+
+
+def cpu_model():
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed(fn, budget_s, max_n):
+    """Runs fn() until budget_s seconds or max_n calls; returns (s/call, n)."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn(n)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= max_n:
+            return el / n, n
+
+
+def cpu_baselines(torch, pkg, budget_s, gpu):
+    """The oracle's fp32 PyTorch restatement of configs C2, C4 and C5 on the
+    host cores, each on a bounded sample of the GPU workload (stated per
+    record), beside the GPU figure of the same config (`gpu`: the bench's
+    own records, None when that record was not run)."""
+    sys.path.insert(0, ROOT)
+    from oracle import dsa_oracle as O
+
+    S = pkg.synthetic
+    out = {}
+    # C2: indexer logits (+ histogram) and exact top-2048, B=4 x 64k keys
+    d = S.indexer_decode_inputs(device="cpu", seed=20)
+    B, max_kv = 4, d["max_kv"]
+
+    def c2(_):
+        sc, _h = O.indexer_logits(d["q"], d["kc"], d["w"], d["bt"], d["seq"], max_kv,
+                                  dtype=torch.float32, with_hist=True)
+        O.topk_rows(sc, d["seq"], 2048)
+
+    t, n = _timed(c2, budget_s, 20)
+    out["c2_logits_topk"] = {"value": round(t * 1e6, 1), "unit": "us/step", "kind": "port",
+                             "sample": f"{n} whole C2 steps (B=4 x 65536 keys, top-2048)",
+                             "gpu_value": gpu.get("c2")}
+    del d
+    # C4 indexer: rows of the last 1024-row sub-chunk of the 64k causal prefill
+    # (full reach), extrapolated to the causal triangle by FLOP ratio
+    T, page, R = 65536, 64, 1024
+    g = torch.Generator().manual_seed(4)
+    npg = T // page
+    kc = torch.randn(npg, page, 128, generator=g).to(torch.float16)
+    bt = torch.randperm(npg, generator=g).to(torch.int32)[None]
+    q = torch.randn(R, 32, 128, generator=g).to(torch.float16)
+    w = (torch.randn(R, 32, generator=g) / 32 ** 0.5).to(torch.float16)
+    rows_per_call = 8
+    done = [0, 0.0]
+
+    def c4i(i):
+        lo = (i * rows_per_call) % R
+        seq = torch.arange(T - R + lo + 1, T - R + lo + rows_per_call + 1, dtype=torch.int32)
+        O.indexer_logits(q[lo:lo + rows_per_call], kc, w[lo:lo + rows_per_call],
+                         bt.expand(rows_per_call, npg), seq, T, dtype=torch.float32)
+        done[0] += rows_per_call
+        done[1] += 8192.0 * float(seq.double().sum())
+
+    t, n = _timed(c4i, budget_s, R // rows_per_call)
+    rate = done[1] / (t * n)  # FLOP/s
+    total = 8192.0 * T * (T + 1) / 2
+    out["c4_indexer_prefill"] = {
+        "value": round(total / rate * 1e3, 1), "unit": "ms (extrapolated)", "kind": "port",
+        "tflops": round(rate / 1e12, 4),
+        "sample": (f"{done[0]} rows of the last 1024-row sub-chunk (full 64k reach), "
+                   "extrapolated to the 64k causal triangle by FLOP ratio"),
+        "gpu_value": gpu.get("c4_indexer")}
+    del kc, q, w
+    # C4 sparse attention: tokens of the last 1024 of the prefill, 2048 keys each
+    nrow = T
+    kv = S.latent_cache(nrow, True, torch.Generator().manual_seed(6), "cpu")
+    btp = torch.randperm(npg, generator=g).to(torch.int32)[None]
+    qa = (torch.randn(64, 64, 576, generator=g) / 24.0).to(torch.float16)
+    idx = torch.stack([torch.randperm(T - 1024 + i, generator=g)[:2048].sort().values
+                       for i in range(64)]).to(torch.int32)
+    seqa = torch.arange(T - 1024 + 1, T - 1024 + 65, dtype=torch.int32)
+    tok = 4
+
+    def c4s(i):
+        lo = (i * tok) % 64
+        O.sparse_mla(qa[lo:lo + tok], kv, idx[lo:lo + tok], btp.expand(tok, npg),
+                     seqa[lo:lo + tok], 576 ** -0.5, dtype=torch.float32)
+
+    t, n = _timed(c4s, budget_s, 16)
+    flops_tok = 2048 * 64 * (576 + 512) * 2
+    rate = flops_tok * tok / t
+    sp_flops, _ = sparse_prefill_flops()
+    out["c4_sparse_prefill_fp8"] = {
+        "value": round(sp_flops / rate * 1e3, 1), "unit": "ms (extrapolated)", "kind": "port",
+        "tflops": round(rate / 1e12, 4),
+        "sample": (f"{n * tok} tokens of the last 1024 of the 64k prefill (2048 selected keys, "
+                   "64 heads, fp8_ds_mla), extrapolated by FLOP ratio to the selected-key total"),
+        "gpu_value": gpu.get("c4_sparse")}
+    del kv, qa, idx
+    # C5a: fp8 GEMV at M=1 on each shape (dequantise in fp32, then x @ W^T)
+    gemv = {}
+    for (N, K) in ((24576, 6144), (6144, 24576), (2112, 6144)):
+        wq = torch.randint(0, 0x7E, (N, K), generator=g, dtype=torch.int32).to(torch.uint8)
+        sc = torch.rand((N + 127) // 128, (K + 127) // 128, generator=g) * 1e-3
+        x = torch.randn(1, K, generator=g).to(torch.float16)
+
+        def c5(_):
+            deq = O.e4m3_decode(wq) * O.expand_block_scale(sc, N, K)
+            (x.float() @ deq.T).to(torch.float16)
+
+        t, n = _timed(c5, budget_s / 3, 5)
+        gemv[f"{N}x{K}_M1"] = {"us": round(t * 1e6, 1), "calls": n}
+        del wq
+    out["c5a_fp8_gemv"] = {"value": gemv, "unit": "us/call", "kind": "port",
+                           "sample": "1-5 calls per shape at M=1", "gpu_value": gpu.get("c5a")}
+    # C5b: indexer-K scatter of 64k tokens, fp8 rows
+    n_tok = 65536
+    k = torch.randn(n_tok, 128, generator=g).to(torch.float16)
+    slot = torch.randperm(n_tok, generator=g).to(torch.int32)
+    cache = torch.zeros(n_tok // 64, 64, 132, dtype=torch.uint8)
+    t, n = _timed(lambda _: O.indexer_k_store(cache, k, slot), budget_s / 2, 5)
+    out["c5b_k_store_fp8"] = {"value": round(t * 1e6, 1), "unit": "us/call", "kind": "port",
+                              "sample": f"{n} scatters of 65536 tokens into fp8 132-byte rows",
+                              "gpu_value": gpu.get("c5b")}
+    return out
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -923,7 +1062,9 @@ def main():
         torch.cuda.empty_cache()
 
     if not args.no_cpu:
-        cores = torch.get_num_threads()
+        cores, aff = cpu_threads()
+        torch.set_num_threads(cores)
+        model = cpu_model()
         cpu_us, n = cpu_baseline(torch, d, idxs, qs, args.cpu_seconds)
         line["cpu_baseline"] = {
             "value": round(cpu_us, 1),
@@ -932,8 +1073,23 @@ def main():
             "kind": "port",
             "sample": (f"{n} C3 decode layers (B=4, 64 heads, topk 2048, fp8_ds_mla) "
                        "through the oracle's fp32 PyTorch restatement on the host CPU"),
+            "cpu_model": model,
+            "affinity_cores": aff,
         }
-        log(f"cpu baseline: {cpu_us:.0f} us/layer on {cores} threads ({n} layers)")
+        log(f"cpu baseline: {cpu_us:.0f} us/layer on {cores} threads ({n} layers), {model}")
+        if not args.no_extra:
+            gpu = {
+                "c2": line.get("indexer_decode_topk", {}).get("logits_plus_topk_us"),
+                "c4_indexer": line.get("indexer_prefill", {}).get("ms"),
+                "c4_sparse": line.get("sparse_prefill_fp8", {}).get("ms"),
+                "c5a": {k: v["us"] for k, v in line.get("fp8_gemv", {}).items()
+                        if isinstance(v, dict) and k.endswith("_M1")} or None,
+                "c5b": line.get("k_store", {}).get("fp8", {}).get("us"),
+            }
+            line["cpu_baselines"] = cpu_baselines(torch, pkg, args.cpu_seconds / 2, gpu)
+            for k2, v2 in line["cpu_baselines"].items():
+                v2["cores"] = cores
+            log(f"cpu baselines: {line['cpu_baselines']}")
 
     print(json.dumps(line), flush=True)
 
