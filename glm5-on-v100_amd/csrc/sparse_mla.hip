@@ -71,7 +71,11 @@ struct MlaParams {
   const int32_t* seq_lens;
   f16* o;
   float* lse;
-  f16* part_o;     // [B, H, S, 512] per-split normalised outputs o_s (S > 1)
+  // [B, H, S, 512] per-split normalised outputs o_s (S > 1); inside each 512,
+  // dim d = 64 w + 16 t + 4 g + r (w, t, g, r: 8, 4, 4, 4) is stored at
+  // 64 w + 16 g + 4 t + r, so the lane holding the four MFMA tiles of a wave's
+  // dims writes 32 contiguous bytes
+  f16* part_o;
   float* part_ml;  // [B, H, S, 2]   per-split (m_s, l_s)
   int B, n_head, topk, max_blocks, page_size, n_splits;
   int page_shift;  // log2(page_size) when it is a power of two, else -1
@@ -541,7 +545,8 @@ __global__ void __launch_bounds__(HW * KW * 64) sparse_mla_kernel(MlaParams p) {
             f16x4 o4;
 #pragma unroll
             for (int r = 0; r < 4; r++) o4[r] = (f16)(v[r] * inv);
-            *reinterpret_cast<f16x4*>(p.part_o + ps * kValueDim + 16 * t + 4 * g) = o4;
+            *reinterpret_cast<f16x4*>(p.part_o + ps * kValueDim + 64 * (t / 4) + 16 * g +
+                                      4 * (t % 4)) = o4;
           }
         }
       }
@@ -859,15 +864,26 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
   const int64_t bh = (int64_t)b * p.n_head + h;
   const float inv = (L > 0.f) ? 1.f / L : 0.f;
   if (h < p.n_head) {
-    f16* dst = final_out ? p.o + bh * kValueDim : p.part_o + (bh * p.n_splits + split) * kValueDim;
+    if (final_out) {
 #pragma unroll
-    for (int t = 0; t < kTilesPerWave; t++) {
-      f16x4 o4;
+      for (int t = 0; t < kTilesPerWave; t++) {
+        f16x4 o4;
 #pragma unroll
-      for (int r = 0; r < 4; r++) o4[r] = (f16)(oacc[t][r] * inv);
-      // streaming store: the partials are read once, by the merge kernel
-      __builtin_nontemporal_store(__builtin_bit_cast(u32x2, o4),
-                                  reinterpret_cast<u32x2*>(dst + kDimsPerWave * w + 16 * t + 4 * g));
+        for (int r = 0; r < 4; r++) o4[r] = (f16)(oacc[t][r] * inv);
+        *reinterpret_cast<f16x4*>(p.o + bh * kValueDim + kDimsPerWave * w + 16 * t + 4 * g) = o4;
+      }
+    } else {
+      // the lane's 16 values are contiguous in the partial layout: two 16-byte
+      // streaming stores (the partials are read once, by the merge kernel)
+      f16x8 o8[2];
+#pragma unroll
+      for (int t = 0; t < kTilesPerWave; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) o8[t >> 1][4 * (t & 1) + r] = (f16)(oacc[t][r] * inv);
+      u32x4* dst = reinterpret_cast<u32x4*>(p.part_o + (bh * p.n_splits + split) * kValueDim +
+                                            kDimsPerWave * w + 16 * g);
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o8[0]), dst);
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o8[1]), dst + 1);
     }
     if (w == 0 && g == 0) {
       if (final_out) {
@@ -1225,14 +1241,25 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
     if (h >= p.n_head) continue;
     const int64_t bh = (int64_t)b * p.n_head + h;
     const float inv = (L[hg] > 0.f) ? 1.f / L[hg] : 0.f;
-    f16* orow = (final_out ? p.o + bh * kValueDim
-                           : p.part_o + (bh * p.n_splits + split) * kValueDim) + 64 * w;
+    if (final_out) {
+      f16* orow = p.o + bh * kValueDim + 64 * w;
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      f16x4 v;
+      for (int t = 0; t < 4; t++) {
+        f16x4 v;
 #pragma unroll
-      for (int r = 0; r < 4; r++) v[r] = (f16)(oacc[t][hg][r] * inv);
-      *reinterpret_cast<f16x4*>(orow + 16 * t + 4 * g) = v;
+        for (int r = 0; r < 4; r++) v[r] = (f16)(oacc[t][hg][r] * inv);
+        *reinterpret_cast<f16x4*>(orow + 16 * t + 4 * g) = v;
+      }
+    } else {
+      f16x8 o8[2];
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) o8[t >> 1][4 * (t & 1) + r] = (f16)(oacc[t][hg][r] * inv);
+      u32x4* dst = reinterpret_cast<u32x4*>(p.part_o + (bh * p.n_splits + split) * kValueDim +
+                                            64 * w + 16 * g);
+      dst[0] = __builtin_bit_cast(u32x4, o8[0]);
+      dst[1] = __builtin_bit_cast(u32x4, o8[1]);
     }
   }
 }
@@ -1498,14 +1525,25 @@ __global__ void __launch_bounds__(kPfThreads) mla_attn_f16_kernel(MlaParams p) {
     if (h >= p.n_head) continue;
     const int64_t bh = (int64_t)b * p.n_head + h;
     const float inv = (L[hg] > 0.f) ? 1.f / L[hg] : 0.f;
-    f16* orow = (final_out ? p.o + bh * kValueDim
-                           : p.part_o + (bh * p.n_splits + split) * kValueDim) + 64 * w;
+    if (final_out) {
+      f16* orow = p.o + bh * kValueDim + 64 * w;
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      f16x4 v;
+      for (int t = 0; t < 4; t++) {
+        f16x4 v;
 #pragma unroll
-      for (int r = 0; r < 4; r++) v[r] = (f16)(oacc[t][hg][r] * inv);
-      *reinterpret_cast<f16x4*>(orow + 16 * t + 4 * g) = v;
+        for (int r = 0; r < 4; r++) v[r] = (f16)(oacc[t][hg][r] * inv);
+        *reinterpret_cast<f16x4*>(orow + 16 * t + 4 * g) = v;
+      }
+    } else {
+      f16x8 o8[2];
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) o8[t >> 1][4 * (t & 1) + r] = (f16)(oacc[t][hg][r] * inv);
+      u32x4* dst = reinterpret_cast<u32x4*>(p.part_o + (bh * p.n_splits + split) * kValueDim +
+                                            64 * w + 16 * g);
+      dst[0] = __builtin_bit_cast(u32x4, o8[0]);
+      dst[1] = __builtin_bit_cast(u32x4, o8[1]);
     }
   }
 }
@@ -1523,9 +1561,12 @@ __global__ void __launch_bounds__(128) sparse_mla_merge_kernel(
     const f16* __restrict__ part_o, const float* __restrict__ part_ml,
     f16* __restrict__ O, float* __restrict__ LSE, int n_splits, float empty_lse) {
   const int64_t bh = blockIdx.x;
-  const int d = 4 * threadIdx.x;
+  // this thread's 4 dims: position 4i of the partial layout holds natural
+  // dims 64 w + 16 t + 4 g .. +3 with i = 16 w + 4 g + t
+  const int i = threadIdx.x;
+  const int d = 64 * (i >> 4) + 16 * (i & 3) + 4 * ((i >> 2) & 3);
   const f32x2* ml = reinterpret_cast<const f32x2*>(part_ml + bh * n_splits * 2);
-  const f16* po = part_o + bh * n_splits * kValueDim + d;
+  const f16* po = part_o + bh * n_splits * kValueDim + 4 * i;
   float m = -1e30f, l = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
