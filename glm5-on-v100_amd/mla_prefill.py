@@ -12,8 +12,14 @@ entry points, `run_prefill_new_tokens` (:229-244) and
 
 The reference computes in fp32 from fp16/bf16 inputs; the kernel multiplies
 fp16 (bf16) inputs exactly into fp32 accumulators and rounds P to fp16 (bf16
-P is kept as a hi + lo pair) for the PV product.  fp32 inputs are not
-supported by the kernel and raise.
+P is kept as a hi + lo pair) for the PV product.  The reference backend also
+lists fp32 (sm70_triton.py:193), where it computes in fp32 throughout.  This
+build takes fp32 inputs by rounding q, k and v to fp16 (one conversion pass
+each) and running the fp16 kernel; the output is returned in fp32 and the LSE
+is fp32 as for the other dtypes.  The results differ from fp32 arithmetic by
+that rounding (2^-11 relative per input element, so |x| must stay below
+fp16's 65504; larger values become inf and show in the output); the GPU test
+bounds the difference against the fp64 oracle.
 """
 from __future__ import annotations
 
@@ -31,14 +37,22 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
                      softmax_scale: float, causal: bool, return_softmax_lse: bool,
                      max_seqlen_q: int | None = None):
-    """q [total_q, H, Dq], k [total_k, H, Dq], v [total_k, H, Dv] (fp16 or
-    bf16, last dim contiguous); cu_seqlens_* int [num_seqs + 1].  Returns out
-    [total_q, H, Dv] (q.dtype) and, if asked, lse [H, total_q] fp32.
+    """q [total_q, H, Dq], k [total_k, H, Dq], v [total_k, H, Dv] (fp16, bf16
+    or fp32, last dim contiguous); cu_seqlens_* int [num_seqs + 1].  Returns
+    out [total_q, H, Dv] (q.dtype) and, if asked, lse [H, total_q] fp32.
+    fp32 inputs are rounded to fp16 for the kernel (see the module note).
     max_seqlen_q saves the host read of the longest query run."""
     _check(q.is_cuda and k.is_cuda and v.is_cuda, "q, k and v must be on the GPU")
-    _check(q.dtype in (torch.float16, torch.bfloat16),
-           "varlen_attention: fp16 or bf16 inputs (the kernel has no fp32 path)")
+    _check(q.dtype in (torch.float16, torch.bfloat16, torch.float32),
+           "varlen_attention: fp16, bf16 or fp32 inputs")
     _check(k.dtype == q.dtype and v.dtype == q.dtype, "q, k and v must share one dtype")
+    if q.dtype == torch.float32:
+        res = varlen_attention(q.to(torch.float16), k.to(torch.float16), v.to(torch.float16),
+                               cu_seqlens_q, cu_seqlens_k, softmax_scale, causal,
+                               return_softmax_lse, max_seqlen_q)
+        if return_softmax_lse:
+            return res[0].to(torch.float32), res[1]
+        return res.to(torch.float32)
     _check(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "q, k, v must be [tokens, heads, dim]")
     total_q, H, d_qk = q.shape
     total_k = k.shape[0]

@@ -108,3 +108,32 @@ def test_equal_scores_closed_form(pkg, dev):
         assert (lse[:, t] - math.log(n)).abs().max() <= 1e-4
         ks = cu_k[seq]
         torch.testing.assert_close(out[t], v[ks:ks + n].float().mean(0), rtol=2e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"c{c[0]}" for c in CASES])
+def test_varlen_attention_fp32_inputs(pkg, dev, case):
+    """fp32 q, k, v (the reference backend's third dtype, sm70_triton.py:193)
+    are rounded to fp16 for the kernel and the output comes back in fp32.
+    Against the fp64 oracle of the unrounded fp32 inputs the input rounding
+    alone moves lse by up to 1e-3 and o by up to 1.05x the fp16 bar on these
+    cases (computed on the CPU), so the bars are twice the fp16 ones:
+    o 4e-3 relative / 2e-3 absolute, lse 2e-3."""
+    seed, cu_q, cu_k, H, dqk, dv, causal = case
+    cu_k = cu_k or cu_q
+    q, k, v = make(seed, cu_q, cu_k, H, dqk, dv, torch.float32)
+    scale = dqk ** -0.5
+    cq = torch.tensor(cu_q, dtype=torch.int32, device=dev)
+    ck = torch.tensor(cu_k, dtype=torch.int32, device=dev)
+    out, lse = pkg.mla_prefill.varlen_attention(q.to(dev), k.to(dev), v.to(dev), cq, ck, scale,
+                                                causal, True)
+    assert out.dtype == torch.float32 and lse.dtype == torch.float32
+    out2 = pkg.mla_prefill.varlen_attention(q.to(dev), k.to(dev), v.to(dev), cq, ck, scale,
+                                            causal, False)
+    assert torch.equal(out, out2)
+    ro, rl = O.varlen_attention(q, k, v, cu_q, cu_k, scale, causal)
+    lse, out = lse.cpu(), out.cpu()
+    assert torch.equal(torch.isinf(lse), torch.isinf(rl))
+    fin = torch.isfinite(rl)
+    if fin.any():
+        assert (lse[fin].double() - rl[fin]).abs().max().item() <= 2e-3
+    torch.testing.assert_close(out.double(), ro, rtol=4e-3, atol=2e-3)
