@@ -94,6 +94,8 @@ UNRESOLVED = [
     # B, H, fp8, topk: kernel path -> rule for a position below seq_len on a bad block
     (4, 64, True, 2048),    # fp8 split decode (LDS-DMA kernel): zero key
     (2, 64, False, 1024),   # fp16 split decode (register-staged kernel): zero key
+    (16, 64, True, 2048),   # fp8 pipelined kernel with 16 key splits: zero key
+    (16, 64, False, 2048),  # fp16 pipelined kernel with 16 key splits: zero key
     (300, 64, True, 256),   # fp8 prefill configuration: zero key (64 heads)
     (300, 64, False, 256),  # fp16 prefill configuration: zero key
     (40, 16, True, 256),    # B >= 32, H <= 16 (the reference's prefill kernel): masked
@@ -183,6 +185,35 @@ def test_prefill_config_segments_partial_heads(ops, dev, fp8):
     o, lse = run(ops, dev, q, kv, idx, bt, seq)
     ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
     check(o, lse, ro, rl)
+
+
+PIPE_SPLIT = [
+    # seed, B, H, fp8, topk, seqs: batches of 8..255 tokens at > 32 heads run the
+    # 64-head pipelined kernels with round(256 / (B * ceil(H / 64))) key splits
+    # (at least two 32-key tiles each), then the merge
+    (40, 16, 64, True, 2048, [3000 - 37 * i for i in range(15)] + [1]),   # 16 splits
+    (41, 16, 64, False, 2048, [3000 - 37 * i for i in range(15)] + [100]),
+    (42, 10, 80, True, 2304, [2900 - 11 * i for i in range(10)]),  # 13 splits, last one empty
+    (43, 10, 80, False, 2304, [2900 - 11 * i for i in range(10)]),
+    (44, 64, 64, True, 1024, [1500 + 7 * i for i in range(64)]),   # 4 splits
+    (45, 8, 64, False, 200, [150, 200, 260, 20, 199, 201, 64, 3]),  # 32 -> 4 splits, short lists
+]
+
+
+@pytest.mark.parametrize("case", PIPE_SPLIT, ids=[f"B{c[1]}H{c[2]}{'fp8' if c[3] else 'fp16'}"
+                                                  for c in PIPE_SPLIT])
+def test_decode_pipelined_key_split(ops, dev, case):
+    """The pipelined kernels with a key split and the merge, against the
+    oracle: ragged top-k lists (-1 padding, splits with no valid key, one
+    split past the list's end), a partial second 64-head group, invalid
+    entries, and one token with no valid key (o = 0, lse = -inf)."""
+    seed, B, H, fp8, topk, seqs = case
+    q, kv, idx, bt, seq = make(seed, B, H, 60, 64, fp8, topk, seqs, invalid_frac=0.03)
+    idx[B // 2] = -1
+    o, lse = run(ops, dev, q, kv, idx, bt, seq)
+    ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
+    check(o, lse, ro, rl)
+    assert torch.all(o[B // 2] == 0) and torch.all(torch.isinf(lse[B // 2]))
 
 
 def test_prefill_equals_decode_config(ops, dev):
