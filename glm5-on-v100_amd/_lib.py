@@ -40,6 +40,11 @@ SIGNATURES = {
                                      _c_int, _c_int, _c_int, _p]),
     "mi355_dsa_concat_and_cache_mla": (_c_int, [_p, _c_int, _c_i64, _p, _c_i64, _p, _c_i64,
                                                 _c_int, _c_i64, _p, _c_int, _p]),
+    "mi355_dsa_decode_layer_prologue": (_c_int, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p,
+                                                 _c_int, _c_int, _c_int, _c_int, _c_int,
+                                                 _p, _c_int, _c_i64, _p, _c_i64, _p, _c_i64,
+                                                 _c_int, _p, _c_int, _p, _c_int, _c_i64, _p, _p,
+                                                 _p, _c_i64, _p]),
     "mi355_dsa_indexer_logits": (_c_int, [_p, _c_int, _c_int, _p, _c_int, _c_int, _p, _c_int,
                                           _c_i64, _c_int, _p, _p, _c_int, _p, _p, _p]),
     "mi355_dsa_indexer_logits_packed": (_c_int, [_p, _c_int, _c_int, _p, _p, _c_int, _c_i64,

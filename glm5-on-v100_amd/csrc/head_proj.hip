@@ -28,94 +28,14 @@
 
 #include "capi_internal.h"
 #include "dsa_common.h"
+#include "head_proj.h"
 
 namespace mi355dsa {
 namespace {
 
-constexpr int kHpMaxKb = 8;  // 32-wide k blocks per wave (K / KW <= 256)
-
-struct HpArgs {
-  const f16* x;
-  int64_t x_st, x_sh;  // element strides of a token and of a head
-  const f16* wt;       // [H, N, K]
-  f16* out;
-  int64_t o_st, o_sh;
-  int T, H, N, K, tail;
-  int n_blocks;  // workgroups per head along n
-  int t_chunk;   // tokens per workgroup along grid y (multiple of 16)
-  int out8;      // out rows take 8-byte stores (aligned base and strides)
-};
-
 template <int NW, int KW>
 __global__ __launch_bounds__(256) void head_proj_kernel(HpArgs a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int g = lane >> 4, c = lane & 15;
-  const int h = blockIdx.x / a.n_blocks, nb = blockIdx.x % a.n_blocks;
-  const int wn = wave % NW, wk = wave / NW;
-  const int n0 = (nb * NW + wn) * 16;  // the wave's 16 output columns
-  const int n = n0 + c;                 // weight row this lane loads
-  const int kp = a.K / KW;
-  const int nkb = kp / 32;
-  const int k0 = wk * kp + 8 * g;
-
-  f16x8 b[kHpMaxKb];
-  const f16* wrow = a.wt + ((int64_t)h * a.N + n) * a.K + k0;
-#pragma unroll
-  for (int i = 0; i < kHpMaxKb; ++i)
-    if (i < nkb) b[i] = *reinterpret_cast<const f16x8*>(wrow + 32 * i);
-
-  __shared__ f32x4 red[KW > 1 ? (KW - 1) * NW * 64 : 1];
-  const int t_begin = blockIdx.y * a.t_chunk;
-  const int t_end = min(a.T, t_begin + a.t_chunk);
-  const f16x8 zero = {};
-  for (int t0 = t_begin; t0 < t_end; t0 += 16) {
-    const int ta = t0 + c;  // A row of this lane
-    const bool live = ta < t_end;
-    const f16* xrow = a.x + (int64_t)(live ? ta : t_begin) * a.x_st + (int64_t)h * a.x_sh + k0;
-    f16x8 av[kHpMaxKb];
-#pragma unroll
-    for (int i = 0; i < kHpMaxKb; ++i)
-      if (i < nkb) av[i] = live ? *reinterpret_cast<const f16x8*>(xrow + 32 * i) : zero;
-    // D^T = W^T X^T: the weight fragment is the A operand, the tokens' the
-    // B operand, so a lane's D column is one token and its four rows are
-    // consecutive output columns (one 8-byte store)
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < kHpMaxKb; ++i)
-      if (i < nkb) acc = mfma16x16x32(b[i], av[i], acc);
-    if constexpr (KW > 1) {
-      if (wk > 0) red[((wk - 1) * NW + wn) * 64 + lane] = acc;
-      __syncthreads();
-      if (wk == 0) {
-#pragma unroll
-        for (int j = 0; j < KW - 1; ++j) acc += red[(j * NW + wn) * 64 + lane];
-      }
-      __syncthreads();
-    }
-    if (wk == 0 && live) {
-      // lane: token ta, columns n0 + 4g .. +3
-      f16* op = a.out + (int64_t)ta * a.o_st + (int64_t)h * a.o_sh + n0 + 4 * g;
-      if (a.out8) {
-        const f16x4 o = {(f16)acc[0], (f16)acc[1], (f16)acc[2], (f16)acc[3]};
-        *reinterpret_cast<f16x4*>(op) = o;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) op[j] = (f16)acc[j];
-      }
-    }
-  }
-
-  // carried columns (q's RoPE part): the n-block-0 workgroup of each head
-  if (a.tail > 0 && nb == 0) {
-    const int per_tok = a.tail / 8;
-    const int n_items = (t_end - t_begin) * per_tok;
-    for (int it = threadIdx.x; it < n_items; it += 256) {
-      const int t = t_begin + it / per_tok, v = (it % per_tok) * 8;
-      const f16x8 val = *reinterpret_cast<const f16x8*>(
-          a.x + (int64_t)t * a.x_st + (int64_t)h * a.x_sh + a.K + v);
-      *reinterpret_cast<f16x8*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + a.N + v) = val;
-    }
-  }
+  head_proj_block<NW, KW>(a, blockIdx.x, blockIdx.y);
 }
 
 // Prefill shapes (many tokens): a workgroup covers all N columns of a head

@@ -155,13 +155,16 @@ class DsaLayer:
 
     # -- decode -------------------------------------------------------------
     def decode_topk(self, idx_q: torch.Tensor, idx_w: torch.Tensor,
-                    block_table: torch.Tensor, seq_lens: torch.Tensor) -> torch.Tensor:
-        """Indexer logits + fused histogram + decode top-k: idx [B, topk]."""
+                    block_table: torch.Tensor, seq_lens: torch.Tensor,
+                    hist: torch.Tensor | None = None) -> torch.Tensor:
+        """Indexer logits + fused histogram + decode top-k: idx [B, topk].
+        hist, if given, is an already cleared int32 [B, 4096]."""
         B = idx_q.shape[0]
         page = self.idx_k_cache.shape[1]
         max_kv = block_table.shape[1] * page
         score = torch.empty(B, max_kv, dtype=torch.float32, device=idx_q.device)
-        hist = torch.zeros(B, 4096, dtype=torch.int32, device=idx_q.device)
+        if hist is None:
+            hist = torch.zeros(B, 4096, dtype=torch.int32, device=idx_q.device)
         idx = torch.empty(B, self.topk, dtype=torch.int32, device=idx_q.device)
         _sm70_ops.sm70_indexer_logits(score, idx_q.contiguous(), self.idx_k_cache,
                                       idx_w.contiguous(), block_table, seq_lens, hist)
@@ -187,16 +190,67 @@ class DsaLayer:
             offs = torch.arange(n, device=q.device, dtype=torch.int32)
             sl = (sl.unsqueeze(1) - (n - 1) + offs).reshape(-1).contiguous()
             bt = bt.repeat_interleave(n, dim=0).contiguous()
-        if kv_c is not None:
-            self.store(kv_c, k_pe, idx_k, slot_mapping)
-        idx = self.decode_topk(idx_q, idx_w, bt, sl)
-        ql = q_latent(q, self.w)
+        hist = None
+        if kv_c is not None and self._fusable(q, kv_c, k_pe, idx_k, slot_mapping):
+            # one launch: q_latent, both cache writes and the histogram clear
+            ql, hist = self._prologue(q, kv_c, k_pe, idx_k, slot_mapping)
+        else:
+            if kv_c is not None:
+                self.store(kv_c, k_pe, idx_k, slot_mapping)
+            ql = q_latent(q, self.w)
+        idx = self.decode_topk(idx_q, idx_w, bt, sl, hist)
         o = torch.empty(B, self.w.n_heads, 512, dtype=torch.float16, device=q.device)
         lse = torch.empty(B, self.w.n_heads, dtype=torch.float32, device=q.device)
         _sm70_ops.sm70_sparse_mla_decode(o, lse, ql, self.latent_cache, idx, bt, sl,
                                          self.w.scale)
         self.last_idx, self.last_o, self.last_lse = idx, o, lse
         return v_up(o, self.w)
+
+    def _fusable(self, q, kv_c, k_pe, idx_k, slot_mapping) -> bool:
+        """The fused decode prologue covers the layer's usual shapes: one
+        slot per token, 16-bit latent inputs of one dtype (fp16 for an fp16
+        cache), fp16-castable indexer keys of 128 dims."""
+        B = q.shape[0]
+        fp8 = self.kv_dtype == "fp8_ds_mla"
+        return (slot_mapping.numel() == B and slot_mapping.dtype in (torch.int32, torch.int64)
+                and kv_c.dim() == 2 and k_pe.dim() == 2 and kv_c.shape[0] >= B
+                and k_pe.shape[0] >= B and kv_c.shape[1] == 512 and k_pe.shape[1] == 64
+                and kv_c.dtype == k_pe.dtype
+                and (kv_c.dtype == torch.float16 or (fp8 and kv_c.dtype == torch.bfloat16))
+                and idx_k.dim() == 2 and idx_k.shape[0] >= B and idx_k.shape[1] == 128
+                and q.dim() == 3 and q.shape[2] == self.w.nope_dim + 64)
+
+    def _prologue(self, q, kv_c, k_pe, idx_k, slot_mapping):
+        """mi355_dsa_decode_layer_prologue: q_latent (returned), the latent
+        and indexer-K cache writes, and a cleared histogram (returned)."""
+        B, H = q.shape[0], q.shape[1]
+        q = _rows8(q)
+        ql = torch.empty(B, H, 576, dtype=torch.float16, device=q.device)
+        hist = torch.empty(B, 4096, dtype=torch.int32, device=q.device)
+
+        def rows16(x):
+            ok = x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
+            return x if ok else x.contiguous()
+
+        kv_c, k_pe = rows16(kv_c[:B]), rows16(k_pe[:B])
+        ik = idx_k[:B].to(torch.float16).contiguous()
+        slot = slot_mapping.contiguous()
+        islot = slot.to(torch.int32)
+        lat, ikc = self.latent_cache, self.idx_k_cache
+        fp8 = self.kv_dtype == "fp8_ds_mla"
+        ik_fp8 = ikc.dtype == torch.uint8
+        kv_rows = lat.numel() // (656 if fp8 else 576)
+        ik_rows = ikc.numel() // (132 if ik_fp8 else 128)
+        uk = self.w.uk_t
+        with torch.cuda.device(q.device):
+            _lib.call("mi355_dsa_decode_layer_prologue", ql.data_ptr(), ql.stride(0), ql.stride(1),
+                      q.data_ptr(), q.stride(0), q.stride(1), uk.data_ptr(), B, H, uk.shape[1],
+                      uk.shape[2], 64, lat.data_ptr(), int(fp8), kv_rows, kv_c.data_ptr(),
+                      kv_c.stride(0), k_pe.data_ptr(), k_pe.stride(0),
+                      int(kv_c.dtype == torch.bfloat16), slot.data_ptr(),
+                      int(slot.dtype == torch.int64), ikc.data_ptr(), int(ik_fp8), ik_rows,
+                      ik.data_ptr(), islot.data_ptr(), hist.data_ptr(), hist.numel(), _stream(q))
+        return ql, hist
 
     # -- prefill ------------------------------------------------------------
     def prefill_topk(self, idx_q: torch.Tensor, idx_w: torch.Tensor, bounds: list[int],

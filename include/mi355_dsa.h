@@ -177,6 +177,32 @@ int mi355_dsa_head_proj(void* out, int64_t out_tok_stride, int64_t out_head_stri
                         void* stream);
 
 /*
+ * Fused prologue of one DSA decode layer step: the work before the indexer
+ * that depends only on the step's inputs, as one launch.  Equal, bit for
+ * bit, to the four calls
+ *   mi355_dsa_head_proj(q_lat, ..., q, ..., wt_uk, T, H, N, K, tail)
+ *   mi355_dsa_concat_and_cache_mla(kv_cache, kv_fp8, kv_rows, kv_c, kv_c_stride,
+ *                                  k_pe, k_pe_stride, in_bf16, T, slot_mapping, slot_i64)
+ *   mi355_dsa_indexer_k_store(idx_cache, idx_fp8, idx_rows, idx_k, T, 128, idx_slot)
+ *   a clear of hist (hist_words int32, a multiple of 4, 16-byte aligned)
+ * with the argument rules of each (the projection always takes the
+ * decode-shaped kernel; idx_k is fp16 [T, 128], 16-byte aligned).  T is the
+ * step's token count for all four.  It has no single counterpart in the
+ * reference: it replaces, for the layer harness, the indexer-K store and
+ * zeroed histogram of reference/sparse_attn_indexer.py:553-555 and :601 and
+ * the latent write and q_nope @ W_UK_T of vLLM's MLA layer (the projection
+ * restated at reference/triton_mla.py:406-418).
+ */
+int mi355_dsa_decode_layer_prologue(
+    void* q_lat, int64_t ql_tok_stride, int64_t ql_head_stride, const void* q,
+    int64_t q_tok_stride, int64_t q_head_stride, const void* wt_uk, int T, int H, int N, int K,
+    int tail, void* kv_cache, int kv_fp8, int64_t kv_rows, const void* kv_c,
+    int64_t kv_c_stride, const void* k_pe, int64_t k_pe_stride, int in_bf16,
+    const void* slot_mapping, int slot_i64, void* idx_cache, int idx_fp8, int64_t idx_rows,
+    const void* idx_k, const int32_t* idx_slot, int32_t* hist, int64_t hist_words,
+    void* stream);
+
+/*
  * Indexer logits (decode and generic path):
  *   score[b,p] = sum_h relu(q[b,h,:] . K[row(b,p),:]) * w[b,h]   (p < seq_len[b])
  *   score[b,p] = -inf                                          (seq_len[b] <= p < max_kv)
