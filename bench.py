@@ -305,9 +305,12 @@ def graph_time_per_call(torch, fn, n_calls, steps=10, warmup=2):
 
 def bench_indexer_decode(torch, pkg, dev, copies=5):
     """Config C2: indexer logits (fused histogram) + decode top-k, B=4 x 64k
-    keys, fp16 indexer-K cache; `copies` distinct caches (> 256 MB MALL)."""
+    keys, fp16 indexer-K cache; `copies` distinct caches (> 256 MB MALL).
+    Also the logits alone on the 132-byte fp8 indexer-K cache the reference
+    offers beside fp16 rows (glue.patch:2952-2966)."""
     ops = pkg._sm70_ops
-    ins = [pkg.synthetic.indexer_decode_inputs(device=dev, seed=20 + i) for i in range(copies)]
+    ins = [pkg.synthetic.indexer_decode_inputs(device=dev, seed=20 + i, fp8=True)
+           for i in range(copies)]
     B, max_kv = 4, ins[0]["max_kv"]
     score = torch.empty(B, max_kv, device=dev)
     hist = torch.zeros(B, 4096, dtype=torch.int32, device=dev)
@@ -323,14 +326,22 @@ def bench_indexer_decode(torch, pkg, dev, copies=5):
             ops.sm70_indexer_logits(score, d["q"], d["kc"], d["w"], d["bt"], d["seq"], hist)
             ops.sm70_decode_topk(idx, score, d["seq"], hist, 2048)
 
+    def logits_fp8():
+        for d in ins:
+            ops.sm70_indexer_logits(score, d["q"], d["kc8"], d["w"], d["bt"], d["seq"], None)
+
     us_logits = graph_time_per_call(torch, logits_only, copies)
     us_full = graph_time_per_call(torch, full, copies)
+    us_fp8 = graph_time_per_call(torch, logits_fp8, copies)
     nbytes = 4 * 65536 * 256 + 4 * 65536 * 4 + 4 * 4096 * 4 + 4 * (32 * 128 + 32) * 2
+    nbytes8 = nbytes - 4 * 65536 * (256 - 132)
     return {
         "logits_us": round(us_logits, 2),
         "logits_gbps": round(nbytes / (us_logits * 1e-6) / 1e9, 1),
         "logits_frac_hbm": round(nbytes / (us_logits * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
         "logits_plus_topk_us": round(us_full, 2),
+        "logits_fp8_index_k_us": round(us_fp8, 2),
+        "logits_fp8_index_k_gbps": round(nbytes8 / (us_fp8 * 1e-6) / 1e9, 1),
         "workload": "C2: B=4, 65536 keys each, 32 heads x 128, fp16 indexer-K, top-2048",
     }
 
@@ -413,7 +424,7 @@ def bench_k_store(torch, pkg, dev, n_tok=65536, copies=8):
     return out
 
 
-def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128):
+def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128, idx_fp8=False):
     """One whole DSA decode layer step at the C3 shape (B=4 tokens at ctx,
     64 heads, top-2048): the step's cache writes (latent + indexer-K), the
     indexer logits with the fused histogram over the full context, decode
@@ -421,14 +432,19 @@ def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128):
     bmm.  `copies` layers with their own caches and weights (> 256 MB MALL)
     are captured in one graph.  Also reports the indexer + top-k, the
     attention (with both projections) and the two projections alone, from
-    graphs of their own."""
+    graphs of their own.  idx_fp8 runs the layer on the 132-byte fp8
+    indexer-K cache instead of fp16 rows (the reference offers both,
+    glue.patch:2952-2966)."""
     m = pkg.dsa_layer
     B, H, page = 4, 64, 64
     layers, steps = [], []
     for i in range(copies):
         d = pkg.synthetic.decode_inputs(B=B, H=H, ctx=ctx, device=dev, seed=60 + i)
         ix = pkg.synthetic.indexer_decode_inputs(B=B, ctx=ctx, dup_frac=0.0, device=dev,
-                                                 seed=70 + i)
+                                                 seed=70 + i, fp8=idx_fp8)
+        if idx_fp8:
+            ix["kc"] = ix.pop("kc8")
+        del ix["k"]
         g = torch.Generator(device=dev)
         g.manual_seed(80 + i)
         w = m.DsaLayerWeights(
@@ -492,7 +508,8 @@ def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128):
         "projections_us": round(us_proj, 2),
         "projections_gbps": round(proj_bytes / (us_proj * 1e-6) / 1e9, 1),
         "workload": (f"one DSA decode layer: B=4 tokens at {ctx} ctx, 64 heads (q_nope {P}, "
-                     f"v {V}), cache writes + indexer 32x128 fp16 K over the full context + "
+                     f"v {V}), cache writes + indexer 32x128 {'fp8' if idx_fp8 else 'fp16'} K "
+                     "over the full context + "
                      "top-2048 + q_latent bmm + sparse MLA (fp8_ds_mla) + W_UV bmm; "
                      f"{copies} layers per graph"),
     }
@@ -1059,6 +1076,8 @@ def main():
     if "dsa_layer" in extras:
         line["dsa_layer_decode"] = bench_dsa_layer(torch, pkg, dev)
         log(f"dsa layer decode: {line['dsa_layer_decode']}")
+        line["dsa_layer_decode_fp8_index_k"] = bench_dsa_layer(torch, pkg, dev, idx_fp8=True)
+        log(f"dsa layer decode, fp8 indexer K: {line['dsa_layer_decode_fp8_index_k']}")
         torch.cuda.empty_cache()
 
     if not args.no_cpu:

@@ -85,7 +85,9 @@ def decode_inputs(B=4, H=64, ctx=184320, topk=2048, fp8=True, page=64, pool_fact
 
 def indexer_decode_inputs(B=4, ctx=65536, page=64, dup_frac=0.01, seed=2, device="cuda",
                           fp8=False):
-    """Config C2: indexer logits + top-k at decode, with ~1% duplicated keys."""
+    """Config C2: indexer logits + top-k at decode, with ~1% duplicated keys.
+    fp8=True also returns the keys quantised into 132-byte fp8 rows
+    (`kc8`, written by the indexer-K store op) in the same paged layout."""
     g = _gen(seed, device)
     bps = (ctx + page - 1) // page
     pool = B * bps
@@ -99,4 +101,11 @@ def indexer_decode_inputs(B=4, ctx=65536, page=64, dup_frac=0.01, seed=2, device
     w = (torch.randn(B, 32, generator=g, device=device) / 32 ** 0.5).to(torch.float16)
     seq = torch.full((B,), ctx, dtype=torch.int32, device=device)
     kc = k.view(pool, page, 128)
-    return dict(q=q, k=k, kc=kc, w=w, bt=bt, seq=seq, max_kv=bps * page)
+    out = dict(q=q, k=k, kc=kc, w=w, bt=bt, seq=seq, max_kv=bps * page)
+    if fp8:
+        from . import _sm70_ops
+        kc8 = torch.empty(pool, page, 132, dtype=torch.uint8, device=device)
+        slots = torch.arange(pool * page, dtype=torch.int32, device=device)
+        _sm70_ops.sm70_indexer_k_store(kc8, k, slots)
+        out["kc8"] = kc8
+    return out
