@@ -66,6 +66,16 @@ __device__ __forceinline__ uint32_t mono_key(float f) {
 // OCP e4m3 (e4m3fn: bias 7, no inf, max 448) codec, exact, integer based.
 // ---------------------------------------------------------------------------
 
+// 4 e4m3 bytes -> 4 exact fp16 values (every e4m3 value, denormals included,
+// is an fp16 value), with the gfx950 conversion at scale 1: two values per
+// instruction
+__device__ __forceinline__ f16x4 e4m3x4_to_f16x4(uint32_t w) {
+  const f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, false);
+  const f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, true);
+  const u32x2 pk = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+  return __builtin_bit_cast(f16x4, pk);
+}
+
 // e4m3 byte -> fp16 bit pattern of value/256.  Exact for every finite byte,
 // including denormals (they land on fp16 denormals): the 4-bit exponent
 // field moves into the low bits of fp16's 5-bit field, i.e. the bias grows

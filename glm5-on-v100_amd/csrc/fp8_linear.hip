@@ -6,10 +6,11 @@
 // GEMV design for gfx950: the HBM-bound stream of W is fed straight into
 // v_mfma_f32_16x16x32_f16.  Each wave owns NB column blocks of 16 weight
 // rows; x (M <= 8 rows, zero padded to 16) is the A operand, the dequantised
-// weights the B operand.  e4m3 bytes become exact fp16 (value/256) with the
-// bit-level decode, so the fp16 products are exact and accumulate in fp32;
-// the block scale (x256) is applied once per 128-wide k block.  Waves of a
-// workgroup split K and are reduced through LDS.
+// weights the B operand.  e4m3 bytes become exact fp16 with the hardware
+// conversion (v_cvt_scalef32_pk_f16_fp8 at scale 1, two per instruction), so
+// the fp16 products are exact and accumulate in fp32; the block scale is
+// applied once per 128-wide k block.  Waves of a workgroup split K and are
+// reduced through LDS.
 #include "capi_internal.h"
 #include "dsa_common.h"
 
@@ -26,16 +27,15 @@ __global__ void __launch_bounds__(256) fp8_dequant_kernel(
   const int k0 = chunk * 16;
   if (k0 >= K) return;
   const int64_t off = (int64_t)n * K + k0;
-  const float sc = s[(int64_t)(n >> 7) * KB + (k0 >> 7)] * 256.0f;
+  const float sc = s[(int64_t)(n >> 7) * KB + (k0 >> 7)];
   const u32x4 raw = *reinterpret_cast<const u32x4*>(w + off);
   f16x8 o0, o1;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    float v[4];
-    e4m3x4_to_f32_div256(raw[i], v);
+    const f16x4 v = e4m3x4_to_f16x4(raw[i]);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const f16 h = (f16)(v[j] * sc);
+      const f16 h = (f16)((float)v[j] * sc);
       if (i < 2)
         o0[4 * i + j] = h;
       else
@@ -63,7 +63,7 @@ template <int NB>
 struct GemvFrag {
   f16x8 a[4];  // x, A operand
   u32x4 b0[NB], b1[NB];
-  float sc[NB];  // block scale x 256 (0 past the end)
+  float sc[NB];  // block scale (0 past the end)
 };
 
 template <int NB, int WAVES>
@@ -110,7 +110,7 @@ __global__ void __launch_bounds__(WAVES * 64) fp8_gemv_kernel(
       if (32 * g < kvalid) f.b0[j] = *reinterpret_cast<const u32x4*>(p);
       if (32 * g + 16 < kvalid) f.b1[j] = *reinterpret_cast<const u32x4*>(p + 16);
       // every row of a 16-row column block shares one 128x128 scale block
-      f.sc[j] = (ok && n_base + 16 * j < N) ? sr[j][kb] * 256.0f : 0.f;
+      f.sc[j] = (ok && n_base + 16 * j < N) ? sr[j][kb] : 0.f;
     }
   };
 
@@ -125,12 +125,9 @@ __global__ void __launch_bounds__(WAVES * 64) fp8_gemv_kernel(
       for (int q = 0; q < 4; q++) {
         const uint32_t d0 = (q < 2) ? f.b0[j][2 * q] : f.b1[j][2 * (q - 2)];
         const uint32_t d1 = (q < 2) ? f.b0[j][2 * q + 1] : f.b1[j][2 * (q - 2) + 1];
-        u32x4 h;
-        h[0] = e4m3x2_to_f16x2_div256(spread_lo(d0));
-        h[1] = e4m3x2_to_f16x2_div256(spread_hi(d0));
-        h[2] = e4m3x2_to_f16x2_div256(spread_lo(d1));
-        h[3] = e4m3x2_to_f16x2_div256(spread_hi(d1));
-        t = mfma16x16x32(f.a[q], __builtin_bit_cast(f16x8, h), t);
+        const f16x4 h0 = e4m3x4_to_f16x4(d0), h1 = e4m3x4_to_f16x4(d1);
+        const f16x8 h = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+        t = mfma16x16x32(f.a[q], h, t);
       }
 #pragma unroll
       for (int r = 0; r < 4; r++) acc[j][r] += f.sc[j] * t[r];

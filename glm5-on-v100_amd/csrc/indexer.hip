@@ -43,7 +43,7 @@ constexpr int kIdxGroup = 2;              // 16-key blocks per pipeline stage
 // [32g, 32g+32), 32 bytes.
 struct KeyFrag {
   u32x4 v[4];
-  float scale;  // fp8: row scale * 256; fp16: 1
+  float scale;  // fp8: row scale; fp16: 1
 };
 
 template <bool KFP8>
@@ -62,7 +62,7 @@ __device__ __forceinline__ void load_key_frag(KeyFrag& f, const void* kv,
     const u32x4_a4* p = reinterpret_cast<const u32x4_a4*>(rp + 32 * g);
     f.v[0] = p[0];
     f.v[1] = p[1];
-    f.scale = *reinterpret_cast<const float*>(rp + 128) * 256.0f;
+    f.scale = *reinterpret_cast<const float*>(rp + 128);
   } else {
     const u32x4* p = reinterpret_cast<const u32x4*>(
         reinterpret_cast<const f16*>(kv) + row * kIdxHeadDim + 8 * g);
@@ -87,7 +87,7 @@ __device__ __forceinline__ void load_key_frag_nb(KeyFrag& f, const void* kv, int
     const u32x4_a4* p = reinterpret_cast<const u32x4_a4*>(rp + 32 * g);
     f.v[0] = p[0];
     f.v[1] = p[1];
-    f.scale = *reinterpret_cast<const float*>(rp + 128) * 256.0f;
+    f.scale = *reinterpret_cast<const float*>(rp + 128);
   } else {
     const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const f16*>(kv) +
                                                     r * kIdxHeadDim + 8 * g);
@@ -102,14 +102,9 @@ __device__ __forceinline__ void load_key_frag_nb(KeyFrag& f, const void* kv, int
 template <bool KFP8>
 __device__ __forceinline__ f16x8 key_operand(const KeyFrag& f, int s) {
   if constexpr (KFP8) {
-    const uint32_t d0 = f.v[s >> 1][2 * (s & 1)];
-    const uint32_t d1 = f.v[s >> 1][2 * (s & 1) + 1];
-    u32x4 h;
-    h[0] = e4m3x2_to_f16x2_div256(spread_lo(d0));
-    h[1] = e4m3x2_to_f16x2_div256(spread_hi(d0));
-    h[2] = e4m3x2_to_f16x2_div256(spread_lo(d1));
-    h[3] = e4m3x2_to_f16x2_div256(spread_hi(d1));
-    return __builtin_bit_cast(f16x8, h);
+    const f16x4 a = e4m3x4_to_f16x4(f.v[s >> 1][2 * (s & 1)]);
+    const f16x4 b = e4m3x4_to_f16x4(f.v[s >> 1][2 * (s & 1) + 1]);
+    return (f16x8){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   } else {
     return __builtin_bit_cast(f16x8, f.v[s]);
   }
@@ -500,12 +495,11 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, SM& sh, int q_base, int
           const u32x2 raw =
               *reinterpret_cast<const u32x2*>(rp + 32 * s + 8 * g);  // 4-B aligned
           const float sc = *reinterpret_cast<const float*>(rp + 128);
-          float v[8];
-          e4m3x4_to_f32_div256(raw[0], v);
-          e4m3x4_to_f32_div256(raw[1], v + 4);
+          const f16x4 k0 = e4m3x4_to_f16x4(raw[0]), k1 = e4m3x4_to_f16x4(raw[1]);
+          const f16x8 k8 = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
           f16x8 h;
 #pragma unroll
-          for (int e = 0; e < 8; e++) h[e] = (f16)(v[e] * (sc * 256.0f));
+          for (int e = 0; e < 8; e++) h[e] = (f16)((float)k8[e] * sc);
           ka[kb][s] = h;
         }
       }

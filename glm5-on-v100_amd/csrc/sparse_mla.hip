@@ -621,14 +621,6 @@ typedef int s32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) s32x2 lds_s32x2;
 typedef __attribute__((address_space(3))) void lds_void;
 
-// 4 e4m3 bytes -> 4 exact fp16 values
-__device__ __forceinline__ f16x4 e4m3x4_to_f16x4(uint32_t w) {
-  const f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, false);
-  const f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, true);
-  const u32x2 pk = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
-  return __builtin_bit_cast(f16x4, pk);
-}
-
 // Global load of one dword issued as inline asm: the compiler does not count
 // it, so the caller's explicit s_waitcnt (which takes the value as an
 // operand) is the only wait, and LDS-DMA issued after it is not drained.
