@@ -1636,11 +1636,13 @@ static int decode_splits(int B, int n_head, int topk) {
 }
 
 // dense decode: splits of the context so that ~256 workgroups run, at least
-// one 32-key tile each
+// four 32-key tiles each (at short contexts the split partials, 1032 B per
+// split, token and head, would otherwise rival the rows read: at 4k context,
+// B = 4 x 64 heads, 32 splits measured 24.8 us against 27.5 us for 64)
 static int dense_splits(int B, int n_head, int max_kv) {
   const int hg = (n_head + 63) / 64;
   int s = kTargetWGs / (B * hg > 0 ? B * hg : 1);
-  const int max_s = (max_kv + kPfTileKeys - 1) / kPfTileKeys;
+  const int max_s = (max_kv + 4 * kPfTileKeys - 1) / (4 * kPfTileKeys);
   if (s > max_s) s = max_s;
   if (s > kMergeMaxSplits) s = kMergeMaxSplits;
   if (s < 1) s = 1;
