@@ -967,32 +967,46 @@ __global__ void __launch_bounds__(kTkThreads) topk_select_kernel(
   uint32_t above2;
   sel_threshold(sh, sh.u.c.hist, kSelBins, need1, &T2, &above2);
   const uint32_t need2 = need1 - above2;
-  for (int i = threadIdx.x; i < kSelBins; i += kTkThreads) sh.u.c.hist[i] = 0u;
-  __syncthreads();
   const uint32_t pre2 = ((uint32_t)T1 << 10) | (uint32_t)T2;  // top 22 bits
-  for (int i = threadIdx.x; i < total_c; i += kTkThreads) {
-    const uint32_t k = sh.u.c.ckey[i];
-    if ((k >> 10) == pre2) atomicAdd(&sh.u.c.hist[k & 1023], 1u);
+  // The T1 keys (a few hundred) spread over 1024 second-level bins, so bin T2
+  // is usually taken whole: then the threshold is pre2 at 22-bit precision,
+  // every key of that bin is taken and the third level is skipped.
+  const bool whole = sh.u.c.hist[T2] == need2;
+  uint32_t tau, take_eq;
+  int sh_bits;  // keys compare as k >> sh_bits against tau
+  if (whole) {
+    tau = pre2;
+    take_eq = need2;
+    sh_bits = 10;
+  } else {
+    __syncthreads();  // every thread has read hist[T2]
+    for (int i = threadIdx.x; i < kSelBins; i += kTkThreads) sh.u.c.hist[i] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < total_c; i += kTkThreads) {
+      const uint32_t k = sh.u.c.ckey[i];
+      if ((k >> 10) == pre2) atomicAdd(&sh.u.c.hist[k & 1023], 1u);
+    }
+    __syncthreads();
+    int T3;
+    uint32_t above3;
+    sel_threshold(sh, sh.u.c.hist, kSelBins, need2, &T3, &above3);
+    tau = (pre2 << 10) | (uint32_t)T3;
+    take_eq = need2 - above3;  // keys equal to tau to take, lowest positions
+    sh_bits = 0;
   }
-  __syncthreads();
-  int T3;
-  uint32_t above3;
-  sel_threshold(sh, sh.u.c.hist, kSelBins, need2, &T3, &above3);
-  const uint32_t tau = (pre2 << 10) | (uint32_t)T3;
-  const uint32_t take_eq = need2 - above3;  // keys equal to tau to take, lowest positions
   // ---- ordered compaction over the candidates: packed (gt | eq << 16) scan ----
   const int per = (total_c + kTkThreads - 1) / kTkThreads;
   const int i0 = threadIdx.x * per, i1 = min(i0 + per, total_c);
   uint32_t packed = 0;
   for (int i = i0; i < i1; i++) {
-    const uint32_t k = sh.u.c.ckey[i];
+    const uint32_t k = sh.u.c.ckey[i] >> sh_bits;
     packed += (k > tau ? 1u : 0u) + (k == tau ? (1u << 16) : 0u);
   }
   uint32_t tot;
   const uint32_t ex = block_excl_scan_n<kTkThreads>(packed, sh.wsum, &tot);
   uint32_t gt = ex & 0xFFFFu, eq = ex >> 16;
   for (int i = i0; i < i1; i++) {
-    const uint32_t k = sh.u.c.ckey[i];
+    const uint32_t k = sh.u.c.ckey[i] >> sh_bits;
     if (k > tau) {
       const uint32_t o = gt + (eq < take_eq ? eq : take_eq);
       if (o < (uint32_t)K) out[o] = sh.u.c.cpos[i];
