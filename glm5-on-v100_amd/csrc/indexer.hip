@@ -116,7 +116,7 @@ __global__ void __launch_bounds__(kIdxWaves * 64) indexer_logits_kernel(
     const f16* __restrict__ W, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ seq_lens, float* __restrict__ score,
     uint32_t* __restrict__ hist, int64_t n_kv_rows, int max_blocks,
-    int page_shift, int max_kv) {
+    int page_shift, int max_kv, int hist8) {
   const int b = blockIdx.y;
   const int p_lo = blockIdx.x * kIdxPPB;
   const int p_hi = min(p_lo + kIdxPPB, max_kv);
@@ -280,10 +280,24 @@ __global__ void __launch_bounds__(kIdxWaves * 64) indexer_logits_kernel(
 
   if (hist != nullptr) {
     __syncthreads();
-    uint32_t* hrow = hist + (int64_t)b * kTopkBins;
-    for (int i = threadIdx.x; i < kTopkBins; i += blockDim.x) {
-      const uint32_t n = s_hist[i];
-      if (n) atomicAdd(&hrow[i], n);
+    // Flush: the workgroups of a row all add into the same few hot bins at
+    // the end, so the device-scope atomics queue on those addresses.  Two
+    // adjacent bins go in one 64-bit atomic (half the atomics); no carry
+    // crosses from the low count into the high one, since a row's counts
+    // stay below 2^32.
+    if (hist8) {
+      unsigned long long* hrow2 =
+          reinterpret_cast<unsigned long long*>(hist + (int64_t)b * kTopkBins);
+      for (int i = threadIdx.x; i < kTopkBins / 2; i += blockDim.x) {
+        const unsigned long long lo = s_hist[2 * i], hi = s_hist[2 * i + 1];
+        if (lo | hi) atomicAdd(hrow2 + i, lo | (hi << 32));
+      }
+    } else {  // a hist base that is not 8-byte aligned: one bin per atomic
+      uint32_t* hrow = hist + (int64_t)b * kTopkBins;
+      for (int i = threadIdx.x; i < kTopkBins; i += blockDim.x) {
+        const uint32_t n = s_hist[i];
+        if (n) atomicAdd(&hrow[i], n);
+      }
     }
   }
 }
@@ -753,14 +767,15 @@ extern "C" int mi355_dsa_indexer_logits(
   const int shift = ilog2_pow2(page_size);
   hipStream_t st = as_stream(stream);
   uint32_t* h = reinterpret_cast<uint32_t*>(hist);
+  const int hist8 = aligned_to(hist, 8) ? 1 : 0;
   if (k_fp8)
     indexer_logits_kernel<true><<<grid, kIdxWaves * 64, 0, st>>>(
         reinterpret_cast<const f16*>(q), k_cache, reinterpret_cast<const f16*>(weights),
-        block_table, seq_lens, score, h, n_kv_rows, max_blocks, shift, max_kv);
+        block_table, seq_lens, score, h, n_kv_rows, max_blocks, shift, max_kv, hist8);
   else
     indexer_logits_kernel<false><<<grid, kIdxWaves * 64, 0, st>>>(
         reinterpret_cast<const f16*>(q), k_cache, reinterpret_cast<const f16*>(weights),
-        block_table, seq_lens, score, h, n_kv_rows, max_blocks, shift, max_kv);
+        block_table, seq_lens, score, h, n_kv_rows, max_blocks, shift, max_kv, hist8);
   DSA_LAUNCH_CHECK("indexer_logits");
   return MI355_DSA_OK;
 }

@@ -66,6 +66,24 @@ def test_logits_and_hist(ops, dev, case):
         assert torch.equal(hist[b].cpu().long(), ref)
 
 
+@pytest.mark.parametrize("offset", [0, 1], ids=["aligned", "word-offset"])
+def test_hist_flush_alignment(ops, dev, offset):
+    """The histogram flush adds two adjacent bins per 64-bit atomic when the
+    hist rows are 8-byte aligned, one bin per atomic otherwise (a hist view
+    one int32 into its buffer); both give the exact bincount."""
+    q, kc, w, bt, seq = make_case(12, 4, 140, 64, False, False, 8192, [8192, 8000, 5000, 8191])
+    buf = torch.full((4 * 4096 + offset,), 0, dtype=torch.int32, device=dev)
+    hist = buf[offset:].view(4, 4096)
+    assert (hist.data_ptr() % 8 == 0) == (offset == 0)
+    score = torch.empty(4, 8192, device=dev)
+    ops.sm70_indexer_logits(score, q.to(dev), kc.to(dev), w.to(dev), bt.to(dev), seq.to(dev), hist)
+    got = score.cpu()
+    for b in range(4):
+        ref = torch.bincount((O.mono_key(got[b, :int(seq[b])]) >> 20).long(), minlength=4096)
+        assert torch.equal(hist[b].cpu().long(), ref)
+    assert int(hist.sum()) == int(seq.sum())
+
+
 @pytest.mark.parametrize("fp8", [False, True], ids=["fp16", "fp8"])
 def test_unmapped_pages_in_full_workgroups(ops, dev, fp8):
     """Block-table entries that are -1 or point past the cache, inside
