@@ -431,8 +431,10 @@ def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128, idx_fp8
     top-k, the q_nope -> latent bmm, sparse MLA decode + merge and the W_UV
     bmm.  `copies` layers with their own caches and weights (> 256 MB MALL)
     are captured in one graph.  Also reports the indexer + top-k, the
-    attention (with both projections) and the two projections alone, from
-    graphs of their own.  idx_fp8 runs the layer on the 132-byte fp8
+    attention with both projections (the layer's fused merge + W_UV
+    launch, and the same work as sparse MLA decode + merge then a separate
+    W_UV projection) and the two projections alone, from graphs of their
+    own.  idx_fp8 runs the layer on the 132-byte fp8
     indexer-K cache instead of fp16 rows (the reference offers both,
     glue.patch:2952-2966)."""
     m = pkg.dsa_layer
@@ -478,6 +480,12 @@ def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128, idx_fp8
             s["layer"].decode_topk(s["idx_q"], s["idx_w"], s["bt"], s["seq"])
 
     def attn_only():
+        for s in steps:
+            L = s["layer"]
+            ql = m.q_latent(s["q"], L.w)
+            L._attention(ql, L.last_idx, s["bt"], s["seq"])
+
+    def attn_two_calls():
         ops = pkg._sm70_ops
         for s in steps:
             L = s["layer"]
@@ -497,6 +505,7 @@ def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128, idx_fp8
     us = graph_time_per_call(torch, full, copies)
     us_topk = graph_time_per_call(torch, topk_only, copies)
     us_attn = graph_time_per_call(torch, attn_only, copies)
+    us_attn2 = graph_time_per_call(torch, attn_two_calls, copies)
     us_proj = graph_time_per_call(torch, proj_only, copies)
     # weight bytes of the two projections (each read once per call)
     proj_bytes = 2 * H * 512 * (P + V)
@@ -505,6 +514,7 @@ def bench_dsa_layer(torch, pkg, dev, ctx=184320, copies=3, P=128, V=128, idx_fp8
         "us_per_layer": round(us, 2),
         "indexer_topk_us": round(us_topk, 2),
         "attention_us": round(us_attn, 2),
+        "attention_two_calls_us": round(us_attn2, 2),
         "projections_us": round(us_proj, 2),
         "projections_gbps": round(proj_bytes / (us_proj * 1e-6) / 1e9, 1),
         "workload": (f"one DSA decode layer: B=4 tokens at {ctx} ctx, 64 heads (q_nope {P}, "

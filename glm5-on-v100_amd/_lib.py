@@ -40,6 +40,9 @@ SIGNATURES = {
                                      _c_int, _c_int, _c_int, _p]),
     "mi355_dsa_concat_and_cache_mla": (_c_int, [_p, _c_int, _c_i64, _p, _c_i64, _p, _c_i64,
                                                 _c_int, _c_i64, _p, _c_int, _p]),
+    "mi355_dsa_decode_layer_attention": (_c_int, [_p, _c_i64, _p, _p, _p, _c_int, _c_int, _p,
+                                                  _c_int, _c_i64, _c_int, _p, _c_int, _p, _c_int,
+                                                  _p, _c_f32, _p, _c_int, _p, _c_size, _p]),
     "mi355_dsa_decode_layer_prologue": (_c_int, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _p,
                                                  _c_int, _c_int, _c_int, _c_int, _c_int,
                                                  _p, _c_int, _c_i64, _p, _c_i64, _p, _c_i64,

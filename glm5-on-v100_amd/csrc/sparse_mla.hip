@@ -1549,51 +1549,184 @@ __global__ void __launch_bounds__(kPfThreads) mla_attn_f16_kernel(MlaParams p) {
 constexpr int kMergeMaxSplits = 128;
 constexpr int kMergeBatch = 16;
 
+// Merged outputs of NU (token, head, position) units: unit j is (bh[j], i[j]),
+// the 4 natural dims held by partial-layout position 4 i (i = 16 w + 4 g + t
+// holds dims 64 w + 16 t + 4 g .. +3).  Returns them normalised in o4[j] and
+// (m[j], l[j]) for the lse.  The loads of all NU units in a batch of splits
+// are issued before any of them is combined; each unit's arithmetic is the
+// same whatever NU is.
+template <int NU>
+__device__ __forceinline__ void merge_units(const f16* __restrict__ part_o,
+                                            const float* __restrict__ part_ml,
+                                            const int64_t (&bh)[NU], int n_splits,
+                                            const int (&i)[NU], f16x4 (&o4)[NU], float (&m)[NU],
+                                            float (&l)[NU]) {
+  const f32x2* ml[NU];
+  const f16* po[NU];
+  f32x4 acc[NU];
+#pragma unroll
+  for (int j = 0; j < NU; j++) {
+    ml[j] = reinterpret_cast<const f32x2*>(part_ml + bh[j] * n_splits * 2);
+    po[j] = part_o + bh[j] * n_splits * kValueDim + 4 * i[j];
+    m[j] = -1e30f;
+    l[j] = 0.f;
+    acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  }
+  for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
+    f32x2 mlv[NU][kMergeBatch];
+    f16x4 hv[NU][kMergeBatch];
+#pragma unroll
+    for (int j = 0; j < NU; j++) {
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; u++) {
+        const int s = s0 + u;
+        mlv[j][u] = (s < n_splits) ? ml[j][s] : (f32x2){-1e30f, 0.f};
+        hv[j][u] = (s < n_splits) ? *reinterpret_cast<const f16x4*>(po[j] + (int64_t)s * kValueDim)
+                                  : (f16x4){0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NU; j++) {
+      f32x4 v[kMergeBatch];
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; u++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) v[u][r] = (float)hv[j][u][r];
+      float mb = m[j];
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; u++)
+        if (mlv[j][u][1] > 0.f) mb = fmaxf(mb, mlv[j][u][0]);
+      const float resc = (l[j] > 0.f) ? expf(m[j] - mb) : 0.f;
+      l[j] *= resc;
+      acc[j] *= resc;
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; u++) {
+        const float w = (mlv[j][u][1] > 0.f) ? expf(mlv[j][u][0] - mb) * mlv[j][u][1] : 0.f;
+        l[j] += w;
+        acc[j] += v[u] * w;
+      }
+      m[j] = mb;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NU; j++) {
+    const float inv = (l[j] > 0.f) ? 1.f / l[j] : 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) o4[j][r] = (f16)(acc[j][r] * inv);
+  }
+}
+
+__device__ __forceinline__ int merge_dim(int i) {
+  return 64 * (i >> 4) + 16 * (i & 3) + 4 * ((i >> 2) & 3);
+}
+
 __global__ void __launch_bounds__(128) sparse_mla_merge_kernel(
     const f16* __restrict__ part_o, const float* __restrict__ part_ml,
     f16* __restrict__ O, float* __restrict__ LSE, int n_splits, float empty_lse) {
-  const int64_t bh = blockIdx.x;
-  // this thread's 4 dims: position 4i of the partial layout holds natural
-  // dims 64 w + 16 t + 4 g .. +3 with i = 16 w + 4 g + t
-  const int i = threadIdx.x;
-  const int d = 64 * (i >> 4) + 16 * (i & 3) + 4 * ((i >> 2) & 3);
-  const f32x2* ml = reinterpret_cast<const f32x2*>(part_ml + bh * n_splits * 2);
-  const f16* po = part_o + bh * n_splits * kValueDim + 4 * i;
-  float m = -1e30f, l = 0.f;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < n_splits; s0 += kMergeBatch) {
-    f32x2 mlv[kMergeBatch];
-    f32x4 v[kMergeBatch];
+  const int64_t bh[1] = {blockIdx.x};
+  const int i[1] = {(int)threadIdx.x};
+  f16x4 o4[1];
+  float m[1], l[1];
+  merge_units<1>(part_o, part_ml, bh, n_splits, i, o4, m, l);
+  *reinterpret_cast<f16x4*>(O + bh[0] * kValueDim + merge_dim(i[0])) = o4[0];
+  if (threadIdx.x == 0) LSE[bh[0]] = (l[0] > 0.f) ? (m[0] + logf(l[0])) : empty_lse;
+}
+
+// Fused epilogue of a decode layer step: the split merge and the o @ W_UV
+// projection in one launch.  Workgroup = (head h, 32 output columns), 8
+// waves: wave w holds the k quarter [128 (w % 4), +128) of column tile w / 4
+// (16 columns).  It loads its 32 KB slice of W_UV^T first, merges all B
+// (<= 16) tokens of head h into LDS with merge_units (the merge kernel's
+// arithmetic; NU units per thread, their loads issued together), then
+// computes each column tile as head_proj_block<1, 4> does (four 16x16x32
+// MFMAs per k quarter, the quarters' partial sums added in quarter order
+// through LDS), so o, lse and out are bit-identical to
+// sparse_mla_merge_kernel followed by mi355_dsa_head_proj.  The workgroups
+// with cb == 0 also write o and lse.  Every workgroup of a head reads the
+// same partials: with xcd_map the grid is numbered so that a head's
+// workgroups share one XCD (dispatch goes round-robin over the 8 XCDs), and
+// its partials one L2.
+constexpr int kEpiMaxTok = 16;
+constexpr int kEpiCols = 32;
+constexpr int kEpiThreads = 512;
+
+struct EpiArgs {
+  const f16* part_o;
+  const float* part_ml;
+  int n_splits;
+  int B, H, V;
+  float empty_lse;
+  const f16* uv_t;  // [H, V, 512]
+  f16* out;         // out[b * out_st + h * V + n]
+  int64_t out_st;
+  f16* o;           // [B, H, 512]
+  float* lse;       // [B, H]
+  int xcd_map;      // grid size is a multiple of 8: group a head's workgroups per XCD
+};
+
+template <int NU>
+__global__ void __launch_bounds__(kEpiThreads) decode_epilogue_kernel(EpiArgs a) {
+  __shared__ __align__(16) f16 so[kEpiMaxTok][kValueDim + 8];
+  __shared__ f32x4 red[3][2][64];
+  const int n_cb = a.V / kEpiCols;
+  const int bid = a.xcd_map ? (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8)
+                            : (int)blockIdx.x;
+  const int h = bid / n_cb, cb = bid % n_cb;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = wave >> 2, kq = wave & 3;
+  const int g = lane >> 4, c = lane & 15;
+  const int k0 = kq * 128 + 8 * g;
+  // weight fragments: column n = 32 cb + 16 t + c, dims k0 + 32 i .. +8
+  f16x8 bw[4];
+  const f16* wrow = a.uv_t + ((int64_t)h * a.V + kEpiCols * cb + 16 * t + c) * kValueDim + k0;
 #pragma unroll
-    for (int u = 0; u < kMergeBatch; u++) {
-      const int s = s0 + u;
-      mlv[u] = (s < n_splits) ? ml[s] : (f32x2){-1e30f, 0.f};
-      const f16x4 h = (s < n_splits) ? *reinterpret_cast<const f16x4*>(po + (int64_t)s * kValueDim)
-                                     : (f16x4){0, 0, 0, 0};
+  for (int i = 0; i < 4; i++) bw[i] = *reinterpret_cast<const f16x8*>(wrow + 32 * i);
+  // merge: unit u = (token u / 128, position 4 (u % 128)); a thread takes
+  // units u + 512 j, j < NU, together (those past the end repeat u and are
+  // not stored)
+  const int n_units = a.B * 128;
+  for (int u = threadIdx.x; u < n_units; u += kEpiThreads * NU) {
+    int uu[NU];
+    int64_t bh[NU];
+    int i[NU];
 #pragma unroll
-      for (int r = 0; r < 4; r++) v[u][r] = (float)h[r];
+    for (int j = 0; j < NU; j++) {
+      uu[j] = u + kEpiThreads * j < n_units ? u + kEpiThreads * j : u;
+      bh[j] = (int64_t)(uu[j] >> 7) * a.H + h;
+      i[j] = uu[j] & 127;
     }
-    float mb = m;
+    f16x4 o4[NU];
+    float m[NU], l[NU];
+    merge_units<NU>(a.part_o, a.part_ml, bh, a.n_splits, i, o4, m, l);
 #pragma unroll
-    for (int u = 0; u < kMergeBatch; u++)
-      if (mlv[u][1] > 0.f) mb = fmaxf(mb, mlv[u][0]);
-    const float resc = (l > 0.f) ? expf(m - mb) : 0.f;
-    l *= resc;
-    acc *= resc;
-#pragma unroll
-    for (int u = 0; u < kMergeBatch; u++) {
-      const float w = (mlv[u][1] > 0.f) ? expf(mlv[u][0] - mb) * mlv[u][1] : 0.f;
-      l += w;
-      acc += v[u] * w;
+    for (int j = 0; j < NU; j++) {
+      if (j > 0 && u + kEpiThreads * j >= n_units) break;
+      const int d = merge_dim(i[j]);
+      *reinterpret_cast<f16x4*>(&so[uu[j] >> 7][d]) = o4[j];
+      if (cb == 0) {
+        *reinterpret_cast<f16x4*>(a.o + bh[j] * kValueDim + d) = o4[j];
+        if (i[j] == 0) a.lse[bh[j]] = (l[j] > 0.f) ? (m[j] + logf(l[j])) : a.empty_lse;
+      }
     }
-    m = mb;
   }
-  const float inv = (l > 0.f) ? 1.f / l : 0.f;
-  f16x4 o4;
+  __syncthreads();
+  // projection: D^T = W^T X^T, lane (c, g): token c, columns 4 g + r of the tile
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const f16x8 zero = {};
 #pragma unroll
-  for (int r = 0; r < 4; r++) o4[r] = (f16)(acc[r] * inv);
-  *reinterpret_cast<f16x4*>(O + bh * kValueDim + d) = o4;
-  if (threadIdx.x == 0) LSE[bh] = (l > 0.f) ? (m + logf(l)) : empty_lse;
+  for (int i = 0; i < 4; i++) {
+    const f16x8 av = c < a.B ? *reinterpret_cast<const f16x8*>(&so[c][k0 + 32 * i]) : zero;
+    acc = mfma16x16x32(bw[i], av, acc);
+  }
+  if (kq > 0) red[kq - 1][t][lane] = acc;
+  __syncthreads();
+  if (kq == 0 && c < a.B) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) acc += red[j][t][lane];
+    f16* op = a.out + (int64_t)c * a.out_st + (int64_t)h * a.V + kEpiCols * cb + 16 * t + 4 * g;
+    const f16x4 ov = {(f16)acc[0], (f16)acc[1], (f16)acc[2], (f16)acc[3]};
+    *reinterpret_cast<f16x4*>(op) = ov;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1718,7 +1851,8 @@ static int mla_decode_impl(
     void* o, float* lse, const void* q, int B, int n_head, const void* kv_cache,
     int kv_fp8, int64_t n_kv_rows, int page_size, const int32_t* idx, int topk,
     const int32_t* block_table, int max_blocks, const int32_t* seq_lens,
-    float scale, void* workspace, size_t workspace_bytes, void* stream, bool dense) {
+    float scale, void* workspace, size_t workspace_bytes, void* stream, bool dense,
+    EpiArgs* epi = nullptr) {
   DSA_CHECK(B >= 0 && n_head > 0, "n_head must be > 0");
   DSA_CHECK(topk >= 0 && max_blocks >= 0 && n_kv_rows >= 0, "bad sizes");
   DSA_CHECK(page_size > 0, "page size must be > 0");
@@ -1816,6 +1950,19 @@ static int mla_decode_impl(
                 : launch_mla<false, 1, kDecKW, 1>(prm, grid, st);
   }
   if (rc != MI355_DSA_OK || S == 1) return rc;
+  if (epi) {  // the fused merge + W_UV epilogue of a layer step
+    epi->part_o = prm.part_o;
+    epi->part_ml = prm.part_ml;
+    epi->n_splits = S;
+    epi->empty_lse = prm.empty_lse;
+    const int nwg = n_head * (epi->V / kEpiCols);
+    epi->xcd_map = (nwg % 8 == 0) ? 1 : 0;
+    if (B * 128 <= kEpiThreads)
+      decode_epilogue_kernel<1><<<dim3((unsigned)nwg), kEpiThreads, 0, st>>>(*epi);
+    else
+      decode_epilogue_kernel<2><<<dim3((unsigned)nwg), kEpiThreads, 0, st>>>(*epi);
+    return check_launch("decode_epilogue");
+  }
   sparse_mla_merge_kernel<<<dim3((unsigned)((int64_t)B * n_head)), 128, 0, st>>>(
       prm.part_o, prm.part_ml, prm.o, prm.lse, S, prm.empty_lse);
   return check_launch("sparse_mla_merge");
@@ -1830,6 +1977,50 @@ extern "C" int mi355_dsa_sparse_mla_decode(
   return mla_decode_impl(o, lse, q, B, n_head, kv_cache, kv_fp8, n_kv_rows, page_size, idx,
                          topk, block_table, max_blocks, seq_lens, scale, workspace,
                          workspace_bytes, stream, false);
+}
+
+// Attention of one DSA decode layer step with its W_UV projection:
+// mi355_dsa_sparse_mla_decode into o / lse, then out = o @ W_UV per head
+// (mi355_dsa_head_proj with wt = uv_t [H, V, 512], K = 512, N = V).  When
+// the decode splits the keys (workspace needed), B <= 16 and V is a multiple
+// of 32, the merge and the projection run as one launch
+// (decode_epilogue_kernel); the results are bit-identical either way.
+extern "C" int mi355_dsa_decode_layer_attention(
+    void* out, int64_t out_tok_stride, void* o, float* lse, const void* q, int B, int n_head,
+    const void* kv_cache, int kv_fp8, int64_t n_kv_rows, int page_size, const int32_t* idx,
+    int topk, const int32_t* block_table, int max_blocks, const int32_t* seq_lens, float scale,
+    const void* uv_t, int V, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  DSA_CHECK(V > 0 && B >= 0 && n_head > 0, "decode_layer_attention: bad sizes");
+  if (B == 0) return MI355_DSA_OK;
+  DSA_CHECK(out && uv_t, "decode_layer_attention: null pointer argument");
+  DSA_CHECK(out_tok_stride >= (int64_t)n_head * V,
+            "decode_layer_attention: out rows must hold n_head * V values");
+  DSA_CHECK(topk >= 0, "bad sizes");
+  const DecodePlan plan = plan_decode(B, n_head, topk, kv_fp8);
+  const bool fused = plan.S > 1 && B <= kEpiMaxTok && V % kEpiCols == 0 &&
+                     (int64_t)n_head * (V / kEpiCols) < ((int64_t)1 << 31) &&
+                     aligned_to(uv_t, 16) && aligned_to(out, 8) && out_tok_stride % 4 == 0;
+  if (!fused) {
+    int rc = mla_decode_impl(o, lse, q, B, n_head, kv_cache, kv_fp8, n_kv_rows, page_size, idx,
+                             topk, block_table, max_blocks, seq_lens, scale, workspace,
+                             workspace_bytes, stream, false);
+    if (rc != MI355_DSA_OK) return rc;
+    return mi355_dsa_head_proj(out, out_tok_stride, V, o, (int64_t)n_head * kValueDim, kValueDim,
+                               uv_t, B, n_head, V, kValueDim, 0, stream);
+  }
+  EpiArgs epi{};
+  epi.B = B;
+  epi.H = n_head;
+  epi.V = V;
+  epi.uv_t = reinterpret_cast<const f16*>(uv_t);
+  epi.out = reinterpret_cast<f16*>(out);
+  epi.out_st = out_tok_stride;
+  epi.o = reinterpret_cast<f16*>(o);
+  epi.lse = lse;
+  return mla_decode_impl(o, lse, q, B, n_head, kv_cache, kv_fp8, n_kv_rows, page_size, idx, topk,
+                         block_table, max_blocks, seq_lens, scale, workspace, workspace_bytes,
+                         stream, false, &epi);
 }
 
 // ---------------------------------------------------------------------------

@@ -199,12 +199,35 @@ class DsaLayer:
                 self.store(kv_c, k_pe, idx_k, slot_mapping)
             ql = q_latent(q, self.w)
         idx = self.decode_topk(idx_q, idx_w, bt, sl, hist)
-        o = torch.empty(B, self.w.n_heads, 512, dtype=torch.float16, device=q.device)
-        lse = torch.empty(B, self.w.n_heads, dtype=torch.float32, device=q.device)
-        _sm70_ops.sm70_sparse_mla_decode(o, lse, ql, self.latent_cache, idx, bt, sl,
-                                         self.w.scale)
+        o, lse, out = self._attention(ql, idx, bt, sl)
         self.last_idx, self.last_o, self.last_lse = idx, o, lse
-        return v_up(o, self.w)
+        return out
+
+    def _attention(self, ql, idx, bt, sl):
+        """Sparse MLA decode over the top-k rows and the W_UV projection
+        (mi355_dsa_decode_layer_attention: the split merge and the projection
+        in one launch where the decode splits the keys).  Returns o [B, H,
+        512], lse [B, H] and out [B, H * V]."""
+        B, H = ql.shape[0], ql.shape[1]
+        lat = self.latent_cache
+        kv_fp8 = lat.dtype == torch.uint8
+        o = torch.empty(B, H, 512, dtype=torch.float16, device=ql.device)
+        lse = torch.empty(B, H, dtype=torch.float32, device=ql.device)
+        out = torch.empty(B, H * self.w.v_dim, dtype=torch.float16, device=ql.device)
+        _check(lat.is_contiguous(), "latent cache must be contiguous")
+        idx, bt, sl = idx.contiguous(), bt.contiguous(), sl.contiguous()
+        topk = idx.shape[1]
+        L = _lib.lib()
+        ws_bytes = L.mi355_dsa_sparse_mla_workspace_size(B, H, topk)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=ql.device)
+        uv = self.w.uv_t
+        with torch.cuda.device(ql.device):
+            _lib.call("mi355_dsa_decode_layer_attention", out.data_ptr(), out.stride(0),
+                      o.data_ptr(), lse.data_ptr(), ql.data_ptr(), B, H, lat.data_ptr(),
+                      int(kv_fp8), lat.numel() // lat.shape[-1], lat.shape[-2], idx.data_ptr(),
+                      topk, bt.data_ptr(), bt.shape[1], sl.data_ptr(), float(self.w.scale),
+                      uv.data_ptr(), uv.shape[1], ws.data_ptr(), ws_bytes, _stream(ql))
+        return o, lse, out
 
     def _fusable(self, q, kv_c, k_pe, idx_k, slot_mapping) -> bool:
         """The fused decode prologue covers the layer's usual shapes: one

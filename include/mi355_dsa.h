@@ -177,6 +177,23 @@ int mi355_dsa_head_proj(void* out, int64_t out_tok_stride, int64_t out_head_stri
                         void* stream);
 
 /*
+ * Attention of one DSA decode layer step with its W_UV projection: o and lse
+ * as mi355_dsa_sparse_mla_decode (same arguments, same workspace size), then
+ * out[b, h*V + n] = sum_k o[b,h,k] * uv_t[h,n,k] as mi355_dsa_head_proj
+ * (x = o, K = 512, N = V, tail 0; out rows out_tok_stride apart).  When the
+ * decode splits the keys, B <= 16 and V is a multiple of 32, the split
+ * merge and the projection run as one launch; o, lse and out are
+ * bit-identical either way.  Replaces, for the layer harness, the caller's
+ * sparse attention plus W_UV bmm (reference/triton_mla.py:292-301, :486-492);
+ * it has no single counterpart in the reference.
+ */
+int mi355_dsa_decode_layer_attention(
+    void* out, int64_t out_tok_stride, void* o, float* lse, const void* q, int B, int n_head,
+    const void* kv_cache, int kv_fp8, int64_t n_kv_rows, int page_size, const int32_t* idx,
+    int topk, const int32_t* block_table, int max_blocks, const int32_t* seq_lens, float scale,
+    const void* uv_t, int V, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Fused prologue of one DSA decode layer step: the work before the indexer
  * that depends only on the step's inputs, as one launch.  Equal, bit for
  * bit, to the four calls
