@@ -48,12 +48,19 @@ SIGNATURES = {
                                                  _p, _c_int, _c_i64, _p, _c_i64, _p, _c_i64,
                                                  _c_int, _p, _c_int, _p, _c_int, _c_i64, _p, _p,
                                                  _p, _c_i64, _p]),
+    "mi355_dsa_decode_layer_indexer": (_c_int, [_c_int, _p, _c_int, _c_i64, _p, _c_i64, _p,
+                                                _c_i64, _c_int, _p, _c_int, _p, _c_int, _c_i64,
+                                                _p, _p, _p, _c_int, _c_int, _p, _p, _c_int, _p,
+                                                _c_int, _p, _p, _p]),
     "mi355_dsa_indexer_logits": (_c_int, [_p, _c_int, _c_int, _p, _c_int, _c_int, _p, _c_int,
                                           _c_i64, _c_int, _p, _p, _c_int, _p, _p, _p]),
     "mi355_dsa_indexer_logits_packed": (_c_int, [_p, _c_int, _c_int, _p, _p, _c_int, _c_i64,
                                                  _c_int, _p, _p, _c_int, _p, _p]),
     "mi355_dsa_decode_topk_workspace_size": (_c_size, [_c_int, _c_int, _c_int]),
     "mi355_dsa_decode_topk": (_c_int, [_p, _p, _p, _p, _c_int, _c_int, _c_int, _p, _c_size, _p]),
+    "mi355_dsa_decode_layer_topk": (_c_int, [_p, _p, _p, _p, _c_int, _c_int, _c_int, _p,
+                                             _c_size, _p, _c_i64, _c_i64, _p, _c_i64, _c_i64,
+                                             _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p]),
     "mi355_dsa_persistent_topk_workspace_size": (_c_size, [_c_int, _c_int, _c_int]),
     "mi355_dsa_persistent_topk": (_c_int, [_p, _c_int, _c_int, _p, _p, _c_int, _c_int, _p,
                                            _c_size, _p]),

@@ -32,8 +32,32 @@ __device__ __forceinline__ void k_store_f16_vec_block(
   for (int c = c0 + cx; c < chunks; c += cx) dst[c] = src[c];
 }
 
-// fp8 132-byte rows: scale = max(amax/448, FLT_MIN); byte = e4m3(v/scale).
-// 16 tokens per 256-thread block; lanes (16j .. 16j+15) own token j.
+// One fp8 132-byte row: scale = max(amax/448, FLT_MIN); byte = e4m3(v/scale).
+// The 16 lanes of one DPP row (sub = 0..15, all active) hold the fp16 key,
+// lane sub dims 8 sub .. +8 in raw.  rp null: the lanes take part in the
+// row maximum and store nothing.
+__device__ __forceinline__ void k_fp8_row_store(const u32x4 raw, uint8_t* rp, int sub) {
+  // Whole-vector bit_cast: hipcc (ROCm 7.2) lowers a bit_cast of a single
+  // vector element inside an unrolled loop to a load of element 0 only.
+  const f16x8 h8 = __builtin_bit_cast(f16x8, raw);
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) v[i] = (float)h8[i];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+  amax = max16(amax);  // the 16 lanes of this row
+  if (rp == nullptr) return;
+  const float scale = fmaxf(amax / 448.0f, FLT_MIN);
+  const u32x2 q = e4m3_quant8(v, amax, scale);
+  uint32_t* dw = reinterpret_cast<uint32_t*>(rp + 8 * sub);  // 4-B aligned
+  dw[0] = q[0];
+  dw[1] = q[1];
+  if (sub == 0) *reinterpret_cast<float*>(rp + 128) = scale;
+}
+
+// fp8 132-byte rows, 16 tokens per 256-thread block; lanes (16j .. 16j+15)
+// own token j.
 __device__ __forceinline__ void k_store_fp8_block(
     const u32x4* __restrict__ k, const int32_t* __restrict__ slot,
     uint8_t* __restrict__ kv, int64_t n_tok, int64_t n_rows, int bx) {
@@ -45,24 +69,8 @@ __device__ __forceinline__ void k_store_fp8_block(
     row = slot[t];
     raw = k[t * 16 + sub];
   }
-  // Whole-vector bit_cast: hipcc (ROCm 7.2) lowers a bit_cast of a single
-  // vector element inside an unrolled loop to a load of element 0 only.
-  const f16x8 h8 = __builtin_bit_cast(f16x8, raw);
-  float v[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) v[i] = (float)h8[i];
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
-  amax = max16(amax);  // the 16 lanes of this token
-  if (t >= n_tok || row < 0 || row >= n_rows) return;
-  const float scale = fmaxf(amax / 448.0f, FLT_MIN);
-  const u32x2 q = e4m3_quant8(v, amax, scale);
-  uint8_t* rp = kv + row * (int64_t)kIdxkFp8RowBytes;
-  uint32_t* dw = reinterpret_cast<uint32_t*>(rp + 8 * sub);  // 4-B aligned
-  dw[0] = q[0];
-  dw[1] = q[1];
-  if (sub == 0) *reinterpret_cast<float*>(rp + 128) = scale;
+  const bool store = t < n_tok && row >= 0 && row < n_rows;
+  k_fp8_row_store(raw, store ? kv + row * (int64_t)kIdxkFp8RowBytes : nullptr, sub);
 }
 
 // MLA latent rows.  One wave per token: lane l holds latent dims 8l .. 8l+7

@@ -3,6 +3,9 @@
 // prologue (dsa_layer.hip).
 #pragma once
 
+#include <algorithm>
+
+#include "capi_internal.h"
 #include "dsa_common.h"
 
 namespace mi355dsa {
@@ -23,9 +26,12 @@ struct HpArgs {
 
 // Body of one 256-thread workgroup (bx, by) of the decode-shaped grid; also
 // run by the fused decode-layer prologue (dsa_layer.hip).
+// tid: the thread's index among the workgroup's 256 (a 1024-thread launch
+// runs four of these blocks side by side when KW == 1, which has no barrier).
 template <int NW, int KW>
-__device__ __forceinline__ void head_proj_block(const HpArgs& a, int bx, int by) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+__device__ __forceinline__ void head_proj_block(const HpArgs& a, int bx, int by,
+                                                int tid = threadIdx.x) {
+  const int wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, c = lane & 15;
   const int h = bx / a.n_blocks, nb = bx % a.n_blocks;
   const int wn = wave % NW, wk = wave / NW;
@@ -86,13 +92,60 @@ __device__ __forceinline__ void head_proj_block(const HpArgs& a, int bx, int by)
   if (a.tail > 0 && nb == 0) {
     const int per_tok = a.tail / 8;
     const int n_items = (t_end - t_begin) * per_tok;
-    for (int it = threadIdx.x; it < n_items; it += 256) {
+    for (int it = tid; it < n_items; it += 256) {
       const int t = t_begin + it / per_tok, v = (it % per_tok) * 8;
       const f16x8 val = *reinterpret_cast<const f16x8*>(
           a.x + (int64_t)t * a.x_st + (int64_t)h * a.x_sh + a.K + v);
       *reinterpret_cast<f16x8*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + a.N + v) = val;
     }
   }
+}
+
+// Host side: arguments and grid of the decode-shaped projection, with the
+// checks mi355_dsa_head_proj makes for it.  kw: the k split of the waves;
+// gx: workgroups per token chunk; wgs: all workgroups.
+inline int hp_decode_setup(HpArgs& a, int& kw, int& gx, int64_t& wgs, const char* who,
+                           void* out, int64_t o_st, int64_t o_sh, const void* x, int64_t x_st,
+                           int64_t x_sh, const void* wt, int T, int H, int N, int K, int tail) {
+  DSA_CHECK(T >= 1 && H > 0 && N > 0 && K > 0 && tail >= 0, "%s: bad projection sizes", who);
+  DSA_CHECK(out && x && wt, "%s: null pointer argument", who);
+  const int KW = K >= 512 ? 4 : (K >= 256 ? 2 : 1);
+  const int NW = 4 / KW;
+  DSA_CHECK(K % (32 * KW) == 0 && K / KW <= 32 * kHpMaxKb,
+            "%s: K = %d must be a multiple of %d and at most %d", who, K, 32 * KW,
+            32 * kHpMaxKb * 4);
+  DSA_CHECK(N % (16 * NW) == 0, "%s: N = %d must be a multiple of %d", who, N, 16 * NW);
+  DSA_CHECK(tail % 8 == 0, "%s: tail must be a multiple of 8", who);
+  DSA_CHECK(aligned_to(x, 16) && aligned_to(wt, 16) && x_st % 8 == 0 && x_sh % 8 == 0,
+            "%s: q and wt must be 16-byte aligned with strides multiple of 8", who);
+  DSA_CHECK(x_sh >= K + tail && x_st >= (int64_t)H * x_sh,
+            "%s: q strides too small for K + tail per head", who);
+  DSA_CHECK(o_sh >= N + tail && o_st >= (int64_t)H * o_sh,
+            "%s: q_lat strides too small for N + tail per head", who);
+  DSA_CHECK(tail == 0 || (aligned_to(out, 16) && o_st % 8 == 0 && o_sh % 8 == 0 && N % 8 == 0),
+            "%s: q_lat must be 16-byte aligned with strides multiple of 8", who);
+  a = HpArgs{};
+  a.x = reinterpret_cast<const f16*>(x);
+  a.x_st = x_st;
+  a.x_sh = x_sh;
+  a.wt = reinterpret_cast<const f16*>(wt);
+  a.out = reinterpret_cast<f16*>(out);
+  a.o_st = o_st;
+  a.o_sh = o_sh;
+  a.T = T;
+  a.H = H;
+  a.N = N;
+  a.K = K;
+  a.tail = tail;
+  a.out8 = aligned_to(out, 8) && o_st % 4 == 0 && o_sh % 4 == 0;
+  a.n_blocks = N / (16 * NW);
+  kw = KW;
+  gx = H * a.n_blocks;
+  const int tiles = (T + 15) / 16;
+  const int n_chunks = std::max(1, std::min(tiles, 2048 / std::max(gx, 1)));
+  a.t_chunk = (tiles + n_chunks - 1) / n_chunks * 16;
+  wgs = (int64_t)gx * ((T + a.t_chunk - 1) / a.t_chunk);
+  return MI355_DSA_OK;
 }
 
 }  // namespace mi355dsa

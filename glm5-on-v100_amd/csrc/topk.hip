@@ -24,6 +24,7 @@
 // already built.  Every path is deterministic.
 #include "capi_internal.h"
 #include "dsa_common.h"
+#include "head_proj.h"
 
 namespace mi355dsa {
 
@@ -876,13 +877,11 @@ __device__ void sel_threshold(SelShared& sh, const uint32_t* hist, int nbins, ui
   __syncthreads();
 }
 
-__global__ void __launch_bounds__(kTkThreads) topk_select_kernel(
-    const float* __restrict__ score, int max_kv, const int32_t* __restrict__ seq_lens,
-    const uint32_t* __restrict__ hist, int32_t* __restrict__ idx, int K, int n_tiles,
-    TopkWs ws) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  SelShared& sh = *reinterpret_cast<SelShared*>(smem_raw);
-  const int b = blockIdx.x;
+// Row b of the select (every return is workgroup-uniform).
+__device__ __forceinline__ void topk_select_row(
+    SelShared& sh, const float* __restrict__ score, int max_kv,
+    const int32_t* __restrict__ seq_lens, const uint32_t* hist,
+    int32_t* __restrict__ idx, int K, int n_tiles, const TopkWs& ws, int b) {
   int32_t* out = idx + (int64_t)b * K;
   // The row's length, its scan metadata and thread t's tile count (this
   // path has n_tiles <= 1024) do not depend on each other: they are loaded
@@ -1021,6 +1020,48 @@ __global__ void __launch_bounds__(kTkThreads) topk_select_kernel(
   }
 }
 
+
+__global__ void __launch_bounds__(256) zero_u32x4_kernel(u32x4* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = (u32x4){0u, 0u, 0u, 0u};
+}
+
+// A decode layer step's q_nope -> latent projection, run beside the select:
+// workgroups n_rows.. of the launch each take four 256-thread blocks of the
+// decode-shaped projection (head_proj_block<4, 1>, which has no barrier).
+// The select's B workgroups leave the rest of the chip idle.
+struct SelProj {
+  HpArgs hp;
+  int gx;   // projection blocks per token chunk
+  int wgs;  // projection blocks
+};
+
+// clear_hist (null or the histogram itself): the consuming variant, which
+// leaves the row's histogram zero for the next step's logits launch once the
+// row is selected.  PROJ: workgroups from n_rows on run the projection.
+template <bool PROJ>
+__global__ void __launch_bounds__(kTkThreads) topk_select_kernel(
+    const float* __restrict__ score, int max_kv, const int32_t* __restrict__ seq_lens,
+    const uint32_t* hist, int32_t* __restrict__ idx, int K, int n_tiles, TopkWs ws,
+    uint32_t* clear_hist, int n_rows, SelProj proj) {
+  if constexpr (PROJ) {
+    if ((int)blockIdx.x >= n_rows) {
+      const int vb = ((int)blockIdx.x - n_rows) * 4 + (int)(threadIdx.x >> 8);
+      if (vb < proj.wgs) head_proj_block<4, 1>(proj.hp, vb % proj.gx, vb / proj.gx, threadIdx.x & 255);
+      return;
+    }
+  }
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  SelShared& sh = *reinterpret_cast<SelShared*>(smem_raw);
+  const int b = blockIdx.x;
+  topk_select_row(sh, score, max_kv, seq_lens, hist, idx, K, n_tiles, ws, b);
+  if (clear_hist != nullptr) {
+    __syncthreads();  // every read of the row's histogram is done
+    u32x4* h = reinterpret_cast<u32x4*>(clear_hist + (int64_t)b * kTopkBins);
+    for (int i = threadIdx.x; i < kTopkBins / 4; i += kTkThreads) h[i] = (u32x4){0u, 0u, 0u, 0u};
+  }
+}
+
 }  // namespace mi355dsa
 
 using namespace mi355dsa;
@@ -1038,19 +1079,22 @@ extern "C" size_t mi355_dsa_decode_topk_workspace_size(int B, int max_kv, int k)
   return topk_ws_bytes(B, (max_kv + kScanTile - 1) / kScanTile);
 }
 
-extern "C" int mi355_dsa_decode_topk(int32_t* idx, const float* score,
-                                     const int32_t* seq_lens, const int32_t* hist,
-                                     int B, int max_kv, int k, void* workspace,
-                                     size_t workspace_bytes, void* stream) {
-  clear_error();
-  (void)workspace;
-  (void)workspace_bytes;
+// Shared by mi355_dsa_decode_topk and the layer step's variant.  clear: the
+// histogram is left zero.  proj (non-null): the projection runs inside the
+// select launch when the two-kernel path is taken (*proj_done set).
+static int decode_topk_impl(int32_t* idx, const float* score, const int32_t* seq_lens,
+                            int32_t* hist, int B, int max_kv, int k, void* workspace,
+                            size_t workspace_bytes, bool clear, const SelProj* proj,
+                            bool* proj_done, void* stream) {
+  if (proj_done) *proj_done = false;
   DSA_CHECK(k >= 1, "k must be >= 1");
   DSA_CHECK(B >= 0 && max_kv >= 0, "B and max_kv must be >= 0");
   DSA_CHECK(k <= (1 << 16) - 1, "k too large");
   if (B == 0) return MI355_DSA_OK;
   DSA_CHECK(idx && score && seq_lens && hist, "null pointer argument");
+  DSA_CHECK(!clear || aligned_to(hist, 16), "hist must be 16-byte aligned");
   hipStream_t st = as_stream(stream);
+  uint32_t* h = reinterpret_cast<uint32_t*>(hist);
   if (two_kernel_topk(B, max_kv, k)) {
     const int n_tiles = (max_kv + kScanTile - 1) / kScanTile;
     const size_t need = topk_ws_bytes(B, n_tiles);
@@ -1058,19 +1102,66 @@ extern "C" int mi355_dsa_decode_topk(int32_t* idx, const float* score,
               "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     DSA_CHECK(aligned_to(workspace, 16), "workspace must be 16-byte aligned");
     const TopkWs ws = topk_ws(workspace, B, n_tiles);
-    const uint32_t* h = reinterpret_cast<const uint32_t*>(hist);
     topk_scan_kernel<<<dim3(n_tiles, B), kScanThreads, 0, st>>>(score, max_kv, seq_lens, h, k, ws);
     int rc = check_launch("decode_topk scan");
     if (rc) return rc;
-    rc = reserve_lds(reinterpret_cast<const void*>(topk_select_kernel), sizeof(SelShared),
-                     "decode_topk");
-    if (rc) return rc;
-    topk_select_kernel<<<B, kTkThreads, sizeof(SelShared), st>>>(score, max_kv, seq_lens, h, idx,
-                                                                 k, n_tiles, ws);
+    uint32_t* ch = clear ? h : nullptr;
+    if (proj != nullptr) {
+      rc = reserve_lds(reinterpret_cast<const void*>(topk_select_kernel<true>), sizeof(SelShared),
+                       "decode_topk");
+      if (rc) return rc;
+      const int grid = B + (proj->wgs + 3) / 4;
+      topk_select_kernel<true><<<grid, kTkThreads, sizeof(SelShared), st>>>(
+          score, max_kv, seq_lens, h, idx, k, n_tiles, ws, ch, B, *proj);
+      if (proj_done) *proj_done = true;
+    } else {
+      rc = reserve_lds(reinterpret_cast<const void*>(topk_select_kernel<false>), sizeof(SelShared),
+                       "decode_topk");
+      if (rc) return rc;
+      topk_select_kernel<false><<<B, kTkThreads, sizeof(SelShared), st>>>(
+          score, max_kv, seq_lens, h, idx, k, n_tiles, ws, ch, B, SelProj{});
+    }
     return check_launch("decode_topk select");
   }
-  return launch_topk_row2<true>(score, B, max_kv, seq_lens,
-                                reinterpret_cast<const uint32_t*>(hist), idx, k, st);
+  int rc = launch_topk_row2<true>(score, B, max_kv, seq_lens, h, idx, k, st);
+  if (rc || !clear) return rc;
+  const int64_t n_vec = (int64_t)B * kTopkBins / 4;
+  zero_u32x4_kernel<<<dim3((unsigned)((n_vec + 255) / 256)), 256, 0, st>>>(
+      reinterpret_cast<u32x4*>(hist), n_vec);
+  return check_launch("decode_topk clear");
+}
+
+extern "C" int mi355_dsa_decode_topk(int32_t* idx, const float* score,
+                                     const int32_t* seq_lens, const int32_t* hist,
+                                     int B, int max_kv, int k, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  clear_error();
+  return decode_topk_impl(idx, score, seq_lens, const_cast<int32_t*>(hist), B, max_kv, k,
+                          workspace, workspace_bytes, false, nullptr, nullptr, stream);
+}
+
+extern "C" int mi355_dsa_decode_layer_topk(
+    int32_t* idx, const float* score, const int32_t* seq_lens, int32_t* hist, int B, int max_kv,
+    int k, void* workspace, size_t workspace_bytes, void* q_lat, int64_t ql_tok_stride,
+    int64_t ql_head_stride, const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+    const void* wt_uk, int T, int H, int N, int K, int tail, void* stream) {
+  clear_error();
+  SelProj proj{};
+  int kw = 0;
+  int64_t wgs = 0;
+  int rc = hp_decode_setup(proj.hp, kw, proj.gx, wgs, "decode_layer_topk", q_lat, ql_tok_stride,
+                           ql_head_stride, q, q_tok_stride, q_head_stride, wt_uk, T, H, N, K,
+                           tail);
+  if (rc) return rc;
+  DSA_CHECK(wgs < ((int64_t)1 << 30), "decode_layer_topk: projection grid too large");
+  proj.wgs = (int)wgs;
+  bool done = false;
+  rc = decode_topk_impl(idx, score, seq_lens, hist, B, max_kv, k, workspace, workspace_bytes,
+                        true, kw == 1 ? &proj : nullptr, &done, stream);
+  if (rc || done) return rc;
+  // the projection as its own launch (whole-row top-k path, or K >= 256)
+  return mi355_dsa_head_proj(q_lat, ql_tok_stride, ql_head_stride, q, q_tok_stride,
+                             q_head_stride, wt_uk, T, H, N, K, tail, stream);
 }
 
 extern "C" size_t mi355_dsa_persistent_topk_workspace_size(int n_rows, int row_stride,

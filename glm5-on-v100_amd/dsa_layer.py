@@ -136,6 +136,7 @@ class DsaLayer:
         self.kv_dtype = "fp8_ds_mla" if latent_cache.dtype == torch.uint8 else "auto"
         # the writer's (unused) scale argument, made once: a fill per step costs a launch
         self._one = torch.ones((), device=latent_cache.device)
+        self._hists: dict = {}
 
     # -- cache writes -------------------------------------------------------
     def store(self, kv_c: torch.Tensor, k_pe: torch.Tensor, idx_k: torch.Tensor,
@@ -191,14 +192,21 @@ class DsaLayer:
             sl = (sl.unsqueeze(1) - (n - 1) + offs).reshape(-1).contiguous()
             bt = bt.repeat_interleave(n, dim=0).contiguous()
         hist = None
-        if kv_c is not None and self._fusable(q, kv_c, k_pe, idx_k, slot_mapping):
-            # one launch: q_latent, both cache writes and the histogram clear
-            ql, hist = self._prologue(q, kv_c, k_pe, idx_k, slot_mapping)
+        fusable = kv_c is not None and self._fusable(q, kv_c, k_pe, idx_k, slot_mapping)
+        if fusable and self._indexer_fusable(q, idx_q, idx_w):
+            # one launch: both cache writes and the indexer logits; then the
+            # top-k (leaving the layer's histogram zero) with q_latent beside it
+            ql, idx = self._indexer_step(q, idx_q, idx_w, bt, sl, kv_c, k_pe, idx_k,
+                                         slot_mapping)
         else:
-            if kv_c is not None:
-                self.store(kv_c, k_pe, idx_k, slot_mapping)
-            ql = q_latent(q, self.w)
-        idx = self.decode_topk(idx_q, idx_w, bt, sl, hist)
+            if fusable:
+                # one launch: q_latent, both cache writes and the histogram clear
+                ql, hist = self._prologue(q, kv_c, k_pe, idx_k, slot_mapping)
+            else:
+                if kv_c is not None:
+                    self.store(kv_c, k_pe, idx_k, slot_mapping)
+                ql = q_latent(q, self.w)
+            idx = self.decode_topk(idx_q, idx_w, bt, sl, hist)
         o, lse, out = self._attention(ql, idx, bt, sl)
         self.last_idx, self.last_o, self.last_lse = idx, o, lse
         return out
@@ -242,6 +250,74 @@ class DsaLayer:
                 and (kv_c.dtype == torch.float16 or (fp8 and kv_c.dtype == torch.bfloat16))
                 and idx_k.dim() == 2 and idx_k.shape[0] >= B and idx_k.shape[1] == 128
                 and q.dim() == 3 and q.shape[2] == self.w.nope_dim + 64)
+
+    def _indexer_fusable(self, q, idx_q, idx_w) -> bool:
+        """The fused prologue + logits launch takes at most 64 new tokens and
+        the logits op's own operand forms."""
+        B = q.shape[0]
+        return (B <= 64 and idx_q.dtype == torch.float16 and idx_q.dim() == 3
+                and tuple(idx_q.shape) == (B, 32, 128) and idx_w.dtype == torch.float16
+                and idx_w.numel() == B * 32)
+
+    def _zero_hist(self, B: int, device) -> torch.Tensor:
+        """The layer's own [B, 4096] top-k histogram, zero between steps: the
+        fused logits launch adds into it and the consuming top-k clears it."""
+        key = (B, str(device))
+        h = self._hists.get(key)
+        if h is None:
+            h = torch.zeros(B, 4096, dtype=torch.int32, device=device)
+            self._hists[key] = h
+        return h
+
+    def _indexer_step(self, q, idx_q, idx_w, bt, sl, kv_c, k_pe, idx_k, slot_mapping):
+        """mi355_dsa_decode_layer_indexer (the latent and indexer-K writes and
+        the indexer logits with the histogram, one launch), then
+        mi355_dsa_decode_layer_topk (the top-k, which leaves the histogram
+        zero, with q_latent run beside its select).  Returns (q_latent, idx)."""
+        B, H = q.shape[0], q.shape[1]
+        q = _rows8(q)
+        ql = torch.empty(B, H, 576, dtype=torch.float16, device=q.device)
+
+        def rows16(x):
+            ok = x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
+            return x if ok else x.contiguous()
+
+        kv_c, k_pe = rows16(kv_c[:B]), rows16(k_pe[:B])
+        ik = idx_k[:B].to(torch.float16).contiguous()
+        slot = slot_mapping.contiguous()
+        islot = slot.to(torch.int32)
+        lat, ikc = self.latent_cache, self.idx_k_cache
+        fp8 = self.kv_dtype == "fp8_ds_mla"
+        ik_fp8 = ikc.dtype == torch.uint8
+        kv_rows = lat.numel() // (656 if fp8 else 576)
+        ik_rows = ikc.numel() // (132 if ik_fp8 else 128)
+        page = ikc.shape[1]
+        max_kv = bt.shape[1] * page
+        score = torch.empty(B, max_kv, dtype=torch.float32, device=q.device)
+        hist = self._zero_hist(B, q.device)
+        iq, iw = idx_q.contiguous(), idx_w.contiguous()
+        bt, sl = bt.contiguous(), sl.contiguous()
+        idx = torch.empty(B, self.topk, dtype=torch.int32, device=q.device)
+        L = _lib.lib()
+        ws_bytes = L.mi355_dsa_decode_topk_workspace_size(B, max_kv, self.topk)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+        uk = self.w.uk_t
+        st = _stream(q)
+        with torch.cuda.device(q.device):
+            _lib.call("mi355_dsa_decode_layer_indexer", B, lat.data_ptr(), int(fp8), kv_rows,
+                      kv_c.data_ptr(), kv_c.stride(0), k_pe.data_ptr(), k_pe.stride(0),
+                      int(kv_c.dtype == torch.bfloat16), slot.data_ptr(),
+                      int(slot.dtype == torch.int64), ikc.data_ptr(), int(ik_fp8), ik_rows,
+                      ik.data_ptr(), islot.data_ptr(), score.data_ptr(), B, max_kv,
+                      iq.data_ptr(), iw.data_ptr(), page, bt.data_ptr(), bt.shape[1],
+                      sl.data_ptr(), hist.data_ptr(), st)
+            self.last_score = score
+            _lib.call("mi355_dsa_decode_layer_topk", idx.data_ptr(), score.data_ptr(),
+                      sl.data_ptr(), hist.data_ptr(), B, max_kv, self.topk, ws.data_ptr(),
+                      ws_bytes, ql.data_ptr(), ql.stride(0), ql.stride(1), q.data_ptr(),
+                      q.stride(0), q.stride(1), uk.data_ptr(), B, H, uk.shape[1], uk.shape[2],
+                      64, st)
+        return ql, idx
 
     def _prologue(self, q, kv_c, k_pe, idx_k, slot_mapping):
         """mi355_dsa_decode_layer_prologue: q_latent (returned), the latent

@@ -220,6 +220,26 @@ int mi355_dsa_decode_layer_prologue(
     void* stream);
 
 /*
+ * The cache writes and the indexer logits of one DSA decode layer step as one
+ * launch: the latent-cache and indexer-K writes of the step's T tokens (the
+ * arguments of mi355_dsa_decode_layer_prologue from kv_cache to idx_slot)
+ * and the logits with the level-1 histogram as mi355_dsa_indexer_logits
+ * over idx_cache (32 heads x 128 dims; score [B, max_kv], idx_q [B, 32, 128],
+ * idx_w [B, 32], the cache's page size, block_table [B, max_blocks],
+ * seq_lens [B]).  hist [B, 4096] must be zero on entry
+ * (mi355_dsa_decode_layer_topk leaves it so); T <= 64.  Results equal, bit
+ * for bit, the separate calls (the reference's indexer-K store,
+ * sparse_attn_indexer.py:553-555, then its logits, :586-590).
+ */
+int mi355_dsa_decode_layer_indexer(
+    int T, void* kv_cache, int kv_fp8, int64_t kv_rows, const void* kv_c, int64_t kv_c_stride,
+    const void* k_pe, int64_t k_pe_stride, int in_bf16, const void* slot_mapping, int slot_i64,
+    void* idx_cache, int idx_fp8, int64_t idx_rows, const void* idx_k, const int32_t* idx_slot,
+    float* score, int B, int max_kv, const void* idx_q, const void* idx_w, int idx_page_size,
+    const int32_t* block_table, int max_blocks, const int32_t* seq_lens, int32_t* hist,
+    void* stream);
+
+/*
  * Indexer logits (decode and generic path):
  *   score[b,p] = sum_h relu(q[b,h,:] . K[row(b,p),:]) * w[b,h]   (p < seq_len[b])
  *   score[b,p] = -inf                                          (seq_len[b] <= p < max_kv)
@@ -268,6 +288,24 @@ int mi355_dsa_decode_topk(int32_t* idx, const float* score,
                           const int32_t* seq_lens, const int32_t* hist, int B,
                           int max_kv, int k, void* workspace,
                           size_t workspace_bytes, void* stream);
+
+/*
+ * The top-k phase of one DSA decode layer step (the layer harness): the
+ * decode top-k as mi355_dsa_decode_topk (same first nine arguments), which
+ * also leaves hist zero (16-byte aligned) for the next step's
+ * mi355_dsa_decode_layer_indexer, and the q_nope -> latent projection as
+ * mi355_dsa_head_proj (x = q, wt = W_UK_T^T [H, N, K], carried tail
+ * columns).  On the two-kernel top-k path with K < 256 the projection runs
+ * in the select launch, on the CUs the select leaves idle.  Results are
+ * bit-identical to the two calls.  The reference zeroes a fresh histogram
+ * each step (reference/sparse_attn_indexer.py:601) and projects q in the MLA
+ * layer (triton_mla.py:413-418).
+ */
+int mi355_dsa_decode_layer_topk(
+    int32_t* idx, const float* score, const int32_t* seq_lens, int32_t* hist, int B, int max_kv,
+    int k, void* workspace, size_t workspace_bytes, void* q_lat, int64_t ql_tok_stride,
+    int64_t ql_head_stride, const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+    const void* wt_uk, int T, int H, int N, int K, int tail, void* stream);
 
 /*
  * Row-wise top-k for prefill: same selection contract as decode_topk, per
