@@ -180,32 +180,39 @@ __device__ __forceinline__ void indexer_logits_body(
     // position p = (page of s in the table) + (s mod page) when p lies in
     // [p_lo, min(p_hi, seq_len)).
     const int lim = min(p_hi, seq_len);
+    int found = 0;
     for (int i = threadIdx.x; i < nk.T * npg; i += blockDim.x) {
       const int t = i / npg, j = i - t * npg;
       const int32_t s = s_new[t];
       if (s >= 0 && s < n_kv_rows && s_bt[j] == (s >> page_shift)) {
         const int p = ((pg0 + j) << page_shift) | (s & ((1 << page_shift) - 1));
-        if (p >= p_lo && p < lim) s_new[kIdxMaxNew + t] = 1;
+        if (p >= p_lo && p < lim) {
+          s_new[kIdxMaxNew + t] = 1;
+          found = 1;
+        }
       }
     }
-    __syncthreads();
-    // 16 lanes per key, 16 keys per pass; a 16-lane group is wholly active
-    // or wholly idle
-    for (int t0 = 0; t0 < nk.T; t0 += 16) {
-      const int t = t0 + (int)(threadIdx.x >> 4);
-      if (t < nk.T && s_new[kIdxMaxNew + t]) {
-        const int sub = threadIdx.x & 15;
-        const int64_t row = s_new[t];
-        void* dst = KFP8 ? (void*)(reinterpret_cast<uint8_t*>(const_cast<void*>(Kv)) +
-                                   row * (int64_t)kIdxkFp8RowBytes)
-                         : (void*)(reinterpret_cast<f16*>(const_cast<void*>(Kv)) +
-                                   row * kIdxHeadDim);
-        idx_key_row_store<KFP8>(nk.ik[(int64_t)t * 16 + sub], dst, sub);
+    // Most workgroups read none of the new rows: for them this one barrier
+    // is the whole cost.
+    if (__syncthreads_or(found)) {
+      // 16 lanes per key, 16 keys per pass; a 16-lane group is wholly active
+      // or wholly idle
+      for (int t0 = 0; t0 < nk.T; t0 += 16) {
+        const int t = t0 + (int)(threadIdx.x >> 4);
+        if (t < nk.T && s_new[kIdxMaxNew + t]) {
+          const int sub = threadIdx.x & 15;
+          const int64_t row = s_new[t];
+          void* dst = KFP8 ? (void*)(reinterpret_cast<uint8_t*>(const_cast<void*>(Kv)) +
+                                     row * (int64_t)kIdxkFp8RowBytes)
+                           : (void*)(reinterpret_cast<f16*>(const_cast<void*>(Kv)) +
+                                     row * kIdxHeadDim);
+          idx_key_row_store<KFP8>(nk.ik[(int64_t)t * 16 + sub], dst, sub);
+        }
       }
+      // the rows written above are read by every wave of this workgroup: the
+      // barrier's workgroup-scope fence orders the stores before those loads
+      __syncthreads();
     }
-    // the rows written above are read by every wave of this workgroup: the
-    // barrier's workgroup-scope fence orders the stores before those loads
-    __syncthreads();
   }
 
   const int lane = threadIdx.x & 63;
@@ -315,6 +322,7 @@ __device__ __forceinline__ void indexer_logits_body(
     // the row's last workgroup: blocks past p_hi are skipped
 #pragma unroll
     for (int j = 0; j < kIdxGroup; j++) load_key_frag<KFP8>(cur[j], Kv, key_row(blk_of(0, j)));
+#pragma unroll
     for (int st = 0; st < n_groups; st++) {
       if (16 * blk_of(st, 0) + p_lo >= p_hi) break;
       if (st + 1 < n_groups) {
