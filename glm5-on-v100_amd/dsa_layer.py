@@ -10,12 +10,18 @@ v_up projection):
   3. q_nope -> latent through W_UK_T (bmm over heads), concatenated with q_pe;
   4. sparse MLA attention over the top-k rows;
   5. o -> values through W_UV (bmm over heads).
-Steps 3 and 5 run the per-head projection kernel (mi355_dsa_head_proj): one
-launch each instead of the reference's transposes, bmm and concatenation.
-Everything runs in order on the caller's stream: a second stream for the
-latent write and step 3 (which do not feed the indexer) made a captured
-decode layer slower (106.7 vs 96.0 us at 180k context), the cross-stream
-join costing more than the overlap hides.
+Steps 3 and 5 run the per-head projection kernel (mi355_dsa_head_proj)
+instead of the reference's transposes, bmm and concatenation.  With the
+step's tokens given (the usual decode shapes) the step is five launches:
+the cache writes fused into the indexer logits launch
+(mi355_dsa_decode_layer_indexer), the top-k scan and select with step 3 run
+in the select launch (mi355_dsa_decode_layer_topk, which also leaves the
+layer's histogram zero for the next step), the attention, and the split merge
+fused with step 5 (mi355_dsa_decode_layer_attention).  All are bit-identical
+to the separate ops.  Everything runs in order on the caller's stream: a
+second stream for the latent write and step 3 (which do not feed the
+indexer) made a captured decode layer slower (106.7 vs 96.0 us at 180k
+context), the cross-stream join costing more than the overlap hides.
 Speculative decode rows (B tokens over B / next_n requests) are expanded per
 token as the reference does (triton_mla.py:267-279).
 
