@@ -10,7 +10,9 @@
 // conversion (v_cvt_scalef32_pk_f16_fp8 at scale 1, two per instruction), so
 // the fp16 products are exact and accumulate in fp32; the block scale is
 // applied once per 128-wide k block.  Waves of a workgroup split K and are
-// reduced through LDS.
+// reduced through LDS.  Long-K shapes stream the weights through a per-wave
+// LDS ring filled by LDS-DMA (fp8_gemv_dma_kernel), several k blocks in
+// flight per wave without holding them in registers.
 #include "capi_internal.h"
 #include "dsa_common.h"
 
@@ -155,6 +157,125 @@ __global__ void __launch_bounds__(WAVES * 64) fp8_gemv_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// GEMV with the weights streamed through a per-wave LDS ring by LDS-DMA
+// (K a multiple of 128, M <= 4).  The register kernel above keeps one k block
+// per wave in flight, so a wave's k blocks form a chain of dependent memory
+// round trips; deeper prefetch in registers cost more occupancy than it hid
+// (measured).  Here each wave keeps D k blocks in flight in LDS without
+// holding them in VGPRs.  A workgroup owns R (16 or 8) weight rows; per slot
+// the R rows x 128 B are stored as [16-byte piece hq][row], so that lane
+// (c, g) reads pieces 2g and 2g + 1 of row c with conflict-free 16-byte
+// reads (lanes c >= R, and x rows >= M, read a zero line), and the 4 x rows
+// of the block take 256 B each, chunk k of row r at chunk k ^ 4r (the rows'
+// reads then fall in different banks).  A wave waits with an explicit vmcnt for its
+// oldest slot only, reads it, then reuses the slot for the block D steps
+// ahead (past its last block it reloads the block it just read, so the count
+// in flight stays uniform).  The MFMA arithmetic per k block is the register
+// kernel's.
+// ---------------------------------------------------------------------------
+constexpr int kGdSlotX = 4 * 256;  // 4 x rows x 128 halves
+
+template <int R>
+struct GdShape {
+  static constexpr int kSlotW = R * 128;          // weight rows x 128 B
+  static constexpr int kSlot = kSlotW + kGdSlotX;
+  static constexpr int kPer = R / 8 + 1;          // DMA instructions per slot
+};
+
+template <int R, int WAVES, int D>
+__global__ void __launch_bounds__(WAVES * 64) fp8_gemv_dma_kernel(
+    const f16* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ s,
+    f16* __restrict__ y, int M, int N, int K, int KB) {
+  using G = GdShape<R>;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int n_base = blockIdx.x * R;
+  uint8_t* ring = smem + wave * D * G::kSlot;
+  uint8_t* zero = smem + WAVES * D * G::kSlot;                       // 64 B of zeros
+  float* s_sc = reinterpret_cast<float*>(zero + 64);                 // this row block's KB scales
+
+  // the R rows share one 128-row scale block
+  const float* srow = s + (int64_t)(n_base >> 7) * KB;
+  for (int i = threadIdx.x; i < KB; i += WAVES * 64) s_sc[i] = srow[i];
+  if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zero)[threadIdx.x] = 0u;
+  __syncthreads();
+
+  // DMA sources of this lane.  Weights, instruction j: slot position
+  // 64 j + lane = hq R + r, i.e. row r = lane % R (clamped into the matrix),
+  // piece hq = (64 j + lane) / R.  x: row min(g, M - 1), 16-byte chunk
+  // c ^ 4g of the block's 256 bytes, landing at chunk c of LDS row g.
+  const uint8_t* wsrc = w + (int64_t)min(n_base + lane % R, N - 1) * K;
+  const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(x) +
+                        (int64_t)min(g, M - 1) * K * 2 + 16 * (c ^ (4 * g));
+  auto issue = [&](int kb, int slot) {
+    uint8_t* sl = ring + slot * G::kSlot;
+#pragma unroll
+    for (int j = 0; j < R / 8; j++)
+      dma16(wsrc + (int64_t)kb * 128 + 16 * ((64 * j + lane) / R), sl + 1024 * j);
+    dma16(xsrc + (int64_t)kb * 256, sl + G::kSlotW);
+  };
+
+  const int nk = (KB + WAVES - 1) / WAVES;  // uniform trip count
+#pragma unroll
+  for (int d = 0; d < D; d++) issue(min(wave + WAVES * d, KB - 1), d);
+
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const bool wrow = c < R, xrow = c < M;
+  for (int i = 0; i < nk; i++) {
+    const int slot = i % D;
+    const int kb = wave + WAVES * i;
+    // the oldest slot's DMAs are done once at most (D - 1) * kPer newer ones
+    // remain in flight
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((D - 1) * G::kPer) : "memory");
+    const uint8_t* sl = ring + slot * G::kSlot;
+    const uint8_t* w0 = wrow ? sl + ((2 * g) * R + c) * 16 : zero;
+    const uint8_t* w1 = wrow ? sl + ((2 * g + 1) * R + c) * 16 : zero;
+    const u32x4 b0 = *reinterpret_cast<const u32x4*>(w0);
+    const u32x4 b1 = *reinterpret_cast<const u32x4*>(w1);
+    const uint8_t* xa = xrow ? sl + G::kSlotW + c * 256 + 64 * (g ^ c) : zero;
+    const int xs = xrow ? 16 : 0;
+    f16x8 a[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) a[q] = *reinterpret_cast<const f16x8*>(xa + xs * q);
+    const float sc = kb < KB ? s_sc[kb] : 0.f;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot is read: reuse it
+    const int nxt = kb + WAVES * D;
+    issue(nxt < KB ? nxt : min(kb, KB - 1), slot);
+    f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t d0 = (q < 2) ? b0[2 * q] : b1[2 * (q - 2)];
+      const uint32_t d1 = (q < 2) ? b0[2 * q + 1] : b1[2 * (q - 2) + 1];
+      const f16x4 h0 = e4m3x4_to_f16x4(d0), h1 = e4m3x4_to_f16x4(d1);
+      const f16x8 h = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+      t = mfma16x16x32(a[q], h, t);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[r] += sc * t[r];
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring's last reloads
+  __syncthreads();
+
+  // reduce the WAVES partial sums through LDS (the ring is free now)
+  float* red = reinterpret_cast<float*>(smem);  // [WAVES][4][64]
+#pragma unroll
+  for (int r = 0; r < 4; r++) red[(wave * 4 + r) * 64 + lane] = acc[r];
+  __syncthreads();
+  for (int e = threadIdx.x; e < 4 * 64; e += WAVES * 64) {
+    const int r = e >> 6, l = e & 63;
+    const int m = 4 * (l >> 4) + r;
+    const int n = n_base + (l & 15);
+    if (m >= M || (l & 15) >= R || n >= N) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < WAVES; wv++) v += red[(wv * 4 + r) * 64 + l];
+    y[(int64_t)m * N + n] = (f16)v;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Load-time quantizer (reference _sm70_attn_fp8_quantize, glue.patch:
 // 1515-1532): per 128x128 block scale = max(amax / 448, 1e-12) and
 // q = e4m3_rne(clamp(w / scale, +-448)); partial edge blocks take the amax
@@ -222,6 +343,18 @@ static void launch_gemv(const f16* x, const uint8_t* w, const float* s, f16* y,
   fp8_gemv_kernel<NB, WAVES><<<blocks, WAVES * 64, 0, st>>>(x, w, s, y, M, N, K, KB);
 }
 
+template <int R, int WAVES, int D>
+static int launch_gemv_dma(const f16* x, const uint8_t* w, const float* s, f16* y, int M,
+                           int N, int K, int KB, hipStream_t st) {
+  const size_t lds = (size_t)WAVES * D * GdShape<R>::kSlot + 64 + 4 * (size_t)KB;
+  const int rc = reserve_lds(reinterpret_cast<const void*>(fp8_gemv_dma_kernel<R, WAVES, D>), lds,
+                             "attn_fp8_gemv");
+  if (rc) return rc;
+  fp8_gemv_dma_kernel<R, WAVES, D><<<(N + R - 1) / R, WAVES * 64, lds, st>>>(x, w, s, y, M, N,
+                                                                              K, KB);
+  return MI355_DSA_OK;
+}
+
 }  // namespace mi355dsa
 
 using namespace mi355dsa;
@@ -240,12 +373,20 @@ extern "C" int mi355_dsa_attn_fp8_gemv(void* y, const void* x, const uint8_t* w,
   const f16* xp = reinterpret_cast<const f16*>(x);
   f16* yp = reinterpret_cast<f16*>(y);
   // Large N: 32 rows x 8 waves per workgroup (768 workgroups at N = 24576,
-  // three resident per CU).  Smaller N: 16 rows x 16 waves, so that K is
-  // spread over enough waves to keep the matrix streaming.
-  if (N >= 16384)
+  // three resident per CU).  Smaller N with a long K (at least 64 k blocks,
+  // M <= 4): the LDS-ring kernel, 8 rows x 4 waves x 4 blocks in flight per
+  // wave (768 workgroups at N = 6144: 44.4 -> 30.7 us at M = 1).  Otherwise
+  // 16 rows x 16 waves, so that K is spread over enough waves to keep the
+  // matrix streaming (at K = 6144 a wave has only 3 k blocks, and the ring
+  // gains nothing).
+  if (N >= 16384) {
     launch_gemv<2, 8>(xp, w, s, yp, M, N, K, KB, st);
-  else
+  } else if (K % 128 == 0 && K >= 8192 && M <= 4) {
+    const int rc = launch_gemv_dma<8, 4, 4>(xp, w, s, yp, M, N, K, KB, st);
+    if (rc) return rc;
+  } else {
     launch_gemv<1, 16>(xp, w, s, yp, M, N, K, KB, st);
+  }
   DSA_LAUNCH_CHECK("attn_fp8_gemv");
   return MI355_DSA_OK;
 }

@@ -104,6 +104,23 @@ def test_gemv_small(ops, dev, M, N, K):
     assert (err <= ref.abs() * 2.0 ** -10 + 1e-3 * ref.abs().max()).all(), err.max()
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("N,K", [(1032, 8192), (8, 16384), (2056, 12288)])
+def test_gemv_long_k(ops, dev, M, N, K):
+    """Long-K shapes (the LDS-ring kernel for M <= 4): a row count that is a
+    multiple of 8 but not of 16, a single 8-row workgroup, and more k blocks
+    than the ring's waves x depth; M = 5 takes the register kernel."""
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.float16)
+    q8, s = O.attn_fp8_quantize(w)
+    x = torch.randn(M, K, generator=g).to(torch.float16)
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    ops.sm70_attn_fp8_gemv(y, x.to(dev), q8.to(dev), s.to(dev))
+    ref = O.attn_fp8_gemv(x, q8, s)
+    err = (y.cpu().double() - ref).abs()
+    assert (err <= ref.abs() * 2.0 ** -10 + 1e-3 * ref.abs().max()).all(), err.max()
+
+
 def _decode_table(dev):
     return O.e4m3_decode(torch.arange(256, dtype=torch.int32).to(torch.uint8)).to(dev)
 
