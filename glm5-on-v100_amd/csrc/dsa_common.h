@@ -216,6 +216,77 @@ __host__ __device__ __forceinline__ int ilog2_pow2(int v) {
   return s;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (all lanes active):
+// row_shr DPP steps within each 16-lane row, then the row totals read with
+// v_readlane.  No LDS traffic.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true);  // row_shr:2
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, true);  // row_shr:4
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, true);  // row_shr:8
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)x, 15);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)x, 31);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)x, 47);
+  const int row = (int)(threadIdx.x & 63) >> 4;
+  return x + (row >= 1 ? r0 : 0u) + (row >= 2 ? r1 : 0u) + (row >= 3 ? r2 : 0u);
+}
+
+// Block-wide exclusive prefix sum over NT threads; *total gets the full sum.
+// wsum needs NT/64 + 1 words.
+template <int NT>
+__device__ uint32_t block_excl_scan_n(uint32_t v, uint32_t* wsum, uint32_t* total) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t x = wave_incl_scan(v);
+  if (lane == 63) wsum[wave] = x;
+  __syncthreads();
+  if (wave == 0) {  // exclusive scan of the NW wave sums, in wave 0's lanes
+    const uint32_t t = lane < NW ? wsum[lane] : 0u;
+    const uint32_t y = wave_incl_scan(t);
+    if (lane < NW) wsum[lane] = y - t;
+    if (lane == NW - 1) wsum[NW] = y;
+  }
+  __syncthreads();
+  const uint32_t res = wsum[wave] + x - v;
+  *total = wsum[NW];
+  __syncthreads();
+  return res;
+}
+
+// Reductions over the 64 lanes of a wave (all lanes active), the same value
+// in every lane: DPP steps within each 16-lane row, then the four row results
+// read with v_readlane (no LDS traffic, unlike a shuffle).
+template <typename Op>
+__device__ __forceinline__ int wave_reduce_i32(int x, Op op) {
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0x140, 0xf, 0xf, false));  // row_mirror
+  return op(op(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+            op(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+__device__ __forceinline__ int wave_min_i32(int x) {
+  return wave_reduce_i32(x, [](int a, int b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ int wave_max_i32(int x) {
+  return wave_reduce_i32(x, [](int a, int b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  return (uint32_t)wave_reduce_i32((int)x, [](int a, int b) {
+    return (uint32_t)a < (uint32_t)b ? a : b;
+  });
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  return (uint32_t)wave_reduce_i32((int)x, [](int a, int b) {
+    return (uint32_t)a > (uint32_t)b ? a : b;
+  });
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t x) {
+  return (uint32_t)wave_reduce_i32((int)x, [](int a, int b) {
+    return (int)((uint32_t)a + (uint32_t)b);
+  });
+}
+
 // Workgroup barrier that waits only for this wave's LDS operations (not for
 // vector-memory loads in flight, which __syncthreads would drain).
 __device__ __forceinline__ void lds_barrier() {

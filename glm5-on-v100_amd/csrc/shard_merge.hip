@@ -13,11 +13,13 @@
 // 2055-2182, host :2411-2436.)
 //
 // One 512-thread workgroup per row.  Each thread holds tp*K/512 (<= 16)
-// candidates' monotone keys in registers (column tid + 512 i for its i-th).  A 12+12+8
-// bit radix select on LDS histograms finds the K-th largest score key T and
-// how many candidates equal to T are taken; those are the lowest columns
-// among the equal ones, ranked by block scans in column order (only when
-// that choice can change the output).  The selected positions are collected
+// candidates' monotone keys and positions in registers (column tid + 512 i
+// for its i-th).  A radix select on LDS histograms (a first digit of at most
+// 12 bits starting below the bits that all of the row's keys share, then
+// digits of 8) finds the K-th largest score key T and how many candidates
+// equal to T are taken; those are the lowest columns among the equal ones,
+// ranked by block scans in column order (only when that choice can change
+// the output).  The selected positions are collected
 // in LDS and put in ascending order by a bitmap over their span (distinct
 // positions spanning fewer than 131072 values: one block scan) or, failing
 // that, a bitonic sort.
@@ -37,36 +39,15 @@ struct SmShared {
   uint32_t wsum[kSmWaves + 1];
   int T;
   uint32_t above;
-  uint32_t cnt, eq_cnt, n_neg;
+  uint32_t cnt, n_neg;
   int pmin, pmax;
+  uint32_t kmin, kmax;
 };
 constexpr int kSmBitmapBits = kTopkBins * 32;  // 131072 positions
 
-// exclusive prefix sum over the block; *total gets the sum
-__device__ uint32_t sm_scan(uint32_t v, SmShared& sh, uint32_t* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  if (lane == 63) sh.wsum[wave] = x;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t run = 0;
-    for (int w = 0; w < kSmWaves; w++) {
-      const uint32_t t = sh.wsum[w];
-      sh.wsum[w] = run;
-      run += t;
-    }
-    sh.wsum[kSmWaves] = run;
-  }
-  __syncthreads();
-  const uint32_t res = sh.wsum[wave] + x - v;
-  *total = sh.wsum[kSmWaves];
-  __syncthreads();
-  return res;
+// exclusive prefix sum over the block (DPP wave scans); *total gets the sum
+__device__ __forceinline__ uint32_t sm_scan(uint32_t v, SmShared& sh, uint32_t* total) {
+  return block_excl_scan_n<kSmThreads>(v, sh.wsum, total);
 }
 
 // bin T of an nbins histogram with above(T) < need <= above(T) + hist[T]
@@ -105,7 +86,11 @@ __device__ __forceinline__ uint32_t mono_of(float v) {
 
 constexpr int kSmMaxPer = 16;  // candidates per thread (tp*K <= 8192)
 
-__global__ void __launch_bounds__(kSmThreads) shard_merge_kernel(
+// VEC: tp*K a multiple of 2048 and a 16-byte aligned payload; a thread's
+// i-th candidate is column 2048 (i / 4) + 4 tid + i % 4, four of them per
+// 16-byte load.  Otherwise column tid + 512 i, one per load.
+template <bool VEC>
+__global__ void __launch_bounds__(kSmThreads, 8) shard_merge_kernel(
     const float* __restrict__ allf, const int32_t* __restrict__ dst_rows,
     int32_t* __restrict__ out, int64_t out_stride, int64_t out_rows, int R, int K,
     int nper, int dst_base) {
@@ -113,76 +98,119 @@ __global__ void __launch_bounds__(kSmThreads) shard_merge_kernel(
   const int r = blockIdx.x;
   const int tid = threadIdx.x;
 
-  // ---- candidates: column col = tid + 512 i = s K + c ----
+  // ---- candidates (column col = s K + c) ----
   // The loops over i skip (continue) rather than stop at nper, so they
   // unroll with fixed registers; the loads are unconditional (steps past
-  // nper re-read column tid, whose value is never used), so all of a
+  // nper re-read the first ones, whose values are never used), so all of a
   // thread's loads are in flight together.  A break made a runtime loop:
-  // one load, then one wait, per step.
+  // one load, then one wait, per step.  Positions are loaded with the
+  // scores: about a quarter of the candidates are selected, spread over the
+  // row, so reading only theirs later would touch the same cache lines
+  // after a second round trip.
   uint32_t key[kSmMaxPer];
+  int32_t pos[kSmMaxPer];
+  if constexpr (VEC) {
 #pragma unroll
-  for (int i = 0; i < kSmMaxPer; i++) {
-    const int col = tid + (i < nper ? i : 0) * kSmThreads;
-    const int s = col / K, c = col - s * K;
-    key[i] = mono_of(allf[((int64_t)s * R + r) * (2 * K) + c]);
+    for (int j = 0; j < kSmMaxPer / 4; j++) {
+      const int col = 2048 * (4 * j < nper ? j : 0) + 4 * tid;
+      const int s = col / K, c = col - s * K;  // c % 4 == 0: a group stays in one shard
+      const float* rowp = allf + ((int64_t)s * R + r) * (2 * K);
+      const u32x4 sv = *reinterpret_cast<const u32x4*>(rowp + c);
+      const u32x4 pv = *reinterpret_cast<const u32x4*>(rowp + K + c);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        key[4 * j + e] = mono_of(__uint_as_float(sv[e]));
+        pos[4 * j + e] = (int32_t)pv[e];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kSmMaxPer; i++) {
+      const int col = tid + (i < nper ? i : 0) * kSmThreads;
+      const int s = col / K, c = col - s * K;
+      const float* rowp = allf + ((int64_t)s * R + r) * (2 * K);
+      key[i] = mono_of(rowp[c]);
+      pos[i] = __float_as_int(rowp[K + c]);
+    }
   }
 
-  // ---- radix select of the K-th largest score key ----
-  for (int i = tid; i < kTopkBins; i += kSmThreads) sh.hist[i] = 0u;
-  __syncthreads();
+  // ---- the bits the row's keys share: the first digit starts below them ----
+  // (normally distributed scores share their sign and most exponent bits; a
+  // digit over those bits would put every key in a few bins, whose LDS
+  // atomics then serialise)
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
 #pragma unroll
   for (int i = 0; i < kSmMaxPer; i++) {
     if (i >= nper) continue;
-    atomicAdd(&sh.hist[key[i] >> 20], 1u);
+    kmin = min(kmin, key[i]);
+    kmax = max(kmax, key[i]);
+  }
+  kmin = wave_min_u32(kmin);
+  kmax = wave_max_u32(kmax);
+  if (tid == 0) {
+    sh.kmin = 0xFFFFFFFFu;
+    sh.kmax = 0u;
+  }
+  for (int i = tid; i < kTopkBins; i += kSmThreads) sh.hist[i] = 0u;
+  __syncthreads();
+  if ((tid & 63) == 0) {
+    atomicMin(&sh.kmin, kmin);
+    atomicMax(&sh.kmax, kmax);
+  }
+  __syncthreads();
+  const uint32_t diff = sh.kmin ^ sh.kmax;
+  // highest differing bit hb; the keys agree on every bit above it
+  const int hb = diff ? 31 - __clz(diff) : 0;
+
+  // ---- radix select of the K-th largest key: a digit of at most 12 bits
+  // from bit hb down, then digits of 8; prefix = key >> shift of the K-th key ----
+  int lo = hb >= 11 ? hb - 11 : 0;
+  int nb = hb - lo + 1;
+#pragma unroll
+  for (int i = 0; i < kSmMaxPer; i++) {
+    if (i >= nper) continue;
+    atomicAdd(&sh.hist[(key[i] >> lo) & ((1u << nb) - 1u)], 1u);
   }
   __syncthreads();
   int T;
   uint32_t above;
   sm_threshold(sh, kTopkBins, (uint32_t)K, &T, &above);
   uint32_t need = (uint32_t)K - above;
-  uint32_t prefix = (uint32_t)T;
-  int shift = 20;
-  if (sh.hist[T] > need) {
+  int shift = lo;
+  // every key agrees with kmin above bit hb: the K-th key's prefix
+  uint32_t prefix = ((hb == 31 ? 0u : (sh.kmin >> (hb + 1)) << nb)) | (uint32_t)T;
+  const int lane = tid & 63;
+  uint32_t n_at = sh.hist[T];  // candidates with (key >> shift) == prefix
+  // further digits of 8 bits: a threshold bin holds a few hundred keys, and
+  // a 256-bin histogram is cleared and scanned in one step per thread
+  while (n_at > need && shift > 0) {  // uniform
+    const int lo2 = shift >= 8 ? shift - 8 : 0;
+    const int nb2 = shift - lo2;
     __syncthreads();
-    for (int i = tid; i < kTopkBins; i += kSmThreads) sh.hist[i] = 0u;
+    for (int i = tid; i < (1 << nb2); i += kSmThreads) sh.hist[i] = 0u;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kSmMaxPer; i++) {
       if (i >= nper) continue;
-      if ((key[i] >> 20) == prefix) atomicAdd(&sh.hist[(key[i] >> 8) & 0xFFFu], 1u);
+      if ((key[i] >> shift) == prefix) atomicAdd(&sh.hist[(key[i] >> lo2) & ((1u << nb2) - 1u)], 1u);
     }
     __syncthreads();
-    sm_threshold(sh, kTopkBins, need, &T, &above);
+    sm_threshold(sh, 1 << nb2, need, &T, &above);
     need -= above;
-    prefix = (prefix << 12) | (uint32_t)T;
-    shift = 8;
-    if (sh.hist[T] > need) {
-      __syncthreads();
-      for (int i = tid; i < 256; i += kSmThreads) sh.hist[i] = 0u;
-      __syncthreads();
-#pragma unroll
-      for (int i = 0; i < kSmMaxPer; i++) {
-        if (i >= nper) continue;
-        if ((key[i] >> 8) == prefix) atomicAdd(&sh.hist[key[i] & 0xFFu], 1u);
-      }
-      __syncthreads();
-      sm_threshold(sh, 256, need, &T, &above);
-      need -= above;
-      prefix = (prefix << 8) | (uint32_t)T;
-      shift = 0;
-    }
+    prefix = (prefix << nb2) | (uint32_t)T;
+    shift = lo2;
+    n_at = sh.hist[T];
   }
   // selected: (key >> shift) > prefix, plus the `need` lowest columns with
   // (key >> shift) == prefix (all of whose keys equal the K-th key when
   // shift == 0; when the select stopped early, that bin is taken whole).
   // The column order among equal keys only matters when fewer than all of
   // them are taken and they are above mono(-inf) (else every one is -1).
-  const bool rank_eq = shift == 0 && sh.hist[T] > need && prefix > 0x007FFFFFu;
+  const bool rank_eq = shift == 0 && n_at > need && prefix > 0x007FFFFFu;
 
   // ---- collect the selected positions ----
   if (tid == 0) {
     sh.cnt = 0;
-    sh.eq_cnt = 0;
     sh.n_neg = 0;
     sh.pmin = 0x7FFFFFFF;
     sh.pmax = -1;
@@ -190,13 +218,8 @@ __global__ void __launch_bounds__(kSmThreads) shard_merge_kernel(
   __syncthreads();
   int lmin = 0x7FFFFFFF, lmax = -1;  // this thread's selected positions
   uint32_t lneg = 0;
-  auto emit = [&](int i) {
-    const int col = tid + i * kSmThreads;
-    const int s = col / K, c = col - s * K;
-    int32_t idx = -1;
-    if (key[i] > 0x007FFFFFu)  // above mono(-inf)
-      idx = __float_as_int(allf[((int64_t)s * R + r) * (2 * K) + K + c]);
-    const uint32_t slot = atomicAdd(&sh.cnt, 1u);
+  auto put = [&](int i, uint32_t slot) {
+    const int32_t idx = key[i] > 0x007FFFFFu ? pos[i] : -1;  // above mono(-inf)
     if (slot < (uint32_t)K) sh.sel[slot] = idx;
     if (idx < 0) {
       lneg++;
@@ -205,34 +228,83 @@ __global__ void __launch_bounds__(kSmThreads) shard_merge_kernel(
       lmax = max(lmax, idx);
     }
   };
-  if (rank_eq) {
+  // the wave's selected candidates of step i take consecutive slots: one LDS
+  // atomic per wave and step
+  auto emit = [&](int i, bool take) {
+    const uint64_t m = __ballot(take);
+    uint32_t base = 0;
+    if (lane == 0 && m) base = atomicAdd(&sh.cnt, (uint32_t)__popcll(m));
+    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+    if (!take) return;
+    put(i, base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                            __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)));
+  };
+  if (rank_eq && !VEC) {
     uint32_t eq_base = 0;
 #pragma unroll
     for (int i = 0; i < kSmMaxPer; i++) {
       if (i >= nper) continue;  // uniform: every thread runs the same scans
       const uint32_t kk = key[i] >> shift;
-      if (kk > prefix) emit(i);
       const uint32_t eq = kk == prefix ? 1u : 0u;
       uint32_t tot;
       const uint32_t rank = eq_base + sm_scan(eq, sh, &tot);  // column order
-      if (eq && rank < need) emit(i);
+      emit(i, kk > prefix || (eq && rank < need));
+      eq_base += tot;
+    }
+  } else if (rank_eq) {
+    // column order with four consecutive columns per thread and step j:
+    // one scan of the thread's count per step, then its own order
+    uint32_t eq_base = 0;
+#pragma unroll
+    for (int j = 0; j < kSmMaxPer / 4; j++) {
+      if (4 * j >= nper) continue;  // uniform
+      uint32_t eqm = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++) eqm |= ((key[4 * j + e] >> shift) == prefix ? 1u : 0u) << e;
+      uint32_t tot;
+      uint32_t rank = eq_base + sm_scan(__popc(eqm), sh, &tot);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t kk = key[4 * j + e] >> shift;
+        const bool eq = (eqm >> e) & 1u;
+        emit(4 * j + e, kk > prefix || (eq && rank < need));
+        rank += eq ? 1u : 0u;
+      }
       eq_base += tot;
     }
   } else {
+    // Any `need` of the equal ones will do: the bin is taken whole, or all
+    // of them are at or below mono(-inf).  One block scan of the packed
+    // (greater | equal << 16) counts numbers the slots: greater keys first,
+    // then the equal ones (per-step LDS atomics made a chain of dependent
+    // LDS round trips, ~5 us per row).
+    uint32_t gt_mask = 0, eq_mask = 0;
 #pragma unroll
     for (int i = 0; i < kSmMaxPer; i++) {
       if (i >= nper) continue;
       const uint32_t kk = key[i] >> shift;
-      if (kk > prefix || (kk == prefix && atomicAdd(&sh.eq_cnt, 1u) < need)) emit(i);
+      gt_mask |= (kk > prefix ? 1u : 0u) << i;
+      eq_mask |= (kk == prefix ? 1u : 0u) << i;
+    }
+    uint32_t tot;
+    const uint32_t ex = sm_scan(__popc(gt_mask) | (__popc(eq_mask) << 16), sh, &tot);
+    uint32_t gslot = ex & 0xFFFFu, erank = ex >> 16;
+    const uint32_t n_gt = tot & 0xFFFFu;
+#pragma unroll
+    for (int i = 0; i < kSmMaxPer; i++) {
+      if (i >= nper) continue;
+      if ((gt_mask >> i) & 1u) {
+        put(i, gslot++);
+      } else if ((eq_mask >> i) & 1u) {
+        if (erank < need) put(i, n_gt + erank);
+        erank++;
+      }
     }
   }
   // one LDS atomic per wave for the span and the -1 count
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    lmin = min(lmin, __shfl_xor(lmin, o, 64));
-    lmax = max(lmax, __shfl_xor(lmax, o, 64));
-    lneg += __shfl_xor(lneg, o, 64);
-  }
+  lmin = wave_min_i32(lmin);
+  lmax = wave_max_i32(lmax);
+  lneg = wave_sum_u32(lneg);
   if ((tid & 63) == 0) {
     atomicMin(&sh.pmin, lmin);
     atomicMax(&sh.pmax, lmax);
@@ -324,7 +396,12 @@ extern "C" int mi355_dsa_indexer_shard_merge(int32_t* out, int64_t out_stride, i
             "shard_merge: rows dst_base .. dst_base + R exceed out");
   DSA_CHECK(out_stride >= K, "shard_merge: out rows shorter than K");
   hipStream_t st = as_stream(stream);
-  shard_merge_kernel<<<R, kSmThreads, 0, st>>>(allf, dst_rows, out, out_stride, out_rows, R, K,
-                                                (int)(ncand / kSmThreads), dst_base);
+  const int nper = (int)(ncand / kSmThreads);
+  if (ncand % 2048 == 0 && aligned_to(allf, 16))
+    shard_merge_kernel<true><<<R, kSmThreads, 0, st>>>(allf, dst_rows, out, out_stride, out_rows,
+                                                        R, K, nper, dst_base);
+  else
+    shard_merge_kernel<false><<<R, kSmThreads, 0, st>>>(allf, dst_rows, out, out_stride,
+                                                         out_rows, R, K, nper, dst_base);
   return check_launch("indexer_shard_merge");
 }

@@ -42,43 +42,6 @@ struct TopkShared {
   uint32_t above;
 };
 
-// Inclusive prefix sum over the 64 lanes of a wave (all lanes active):
-// row_shr DPP steps within each 16-lane row, then the row totals read with
-// v_readlane.  No LDS traffic.
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true);  // row_shr:1
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true);  // row_shr:2
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, true);  // row_shr:4
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, true);  // row_shr:8
-  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)x, 15);
-  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)x, 31);
-  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)x, 47);
-  const int row = (int)(threadIdx.x & 63) >> 4;
-  return x + (row >= 1 ? r0 : 0u) + (row >= 2 ? r1 : 0u) + (row >= 3 ? r2 : 0u);
-}
-
-// Block-wide exclusive prefix sum over NT threads; *total gets the full sum.
-// wsum needs NT/64 + 1 words.
-template <int NT>
-__device__ uint32_t block_excl_scan_n(uint32_t v, uint32_t* wsum, uint32_t* total) {
-  constexpr int NW = NT / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t x = wave_incl_scan(v);
-  if (lane == 63) wsum[wave] = x;
-  __syncthreads();
-  if (wave == 0) {  // exclusive scan of the NW wave sums, in wave 0's lanes
-    const uint32_t t = lane < NW ? wsum[lane] : 0u;
-    const uint32_t y = wave_incl_scan(t);
-    if (lane < NW) wsum[lane] = y - t;
-    if (lane == NW - 1) wsum[NW] = y;
-  }
-  __syncthreads();
-  const uint32_t res = wsum[wave] + x - v;
-  *total = wsum[NW];
-  __syncthreads();
-  return res;
-}
-
 __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* wsum, uint32_t* total) {
   return block_excl_scan_n<kTkThreads>(v, wsum, total);
 }
