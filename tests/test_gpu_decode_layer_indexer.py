@@ -141,3 +141,37 @@ def test_indexer_step_rejects_too_many_tokens(pkg, lib):
         one, one, 64, one, 16, one, one, None)
     assert rc != 0
     assert b"at most 64" in lib.mi355_dsa_last_error()
+
+
+def test_layer_decode_graph_replays(pkg, dev):
+    """DsaLayer.decode captured in a HIP graph and replayed, with eager work
+    and synchronisations between replays: every replay gives the eager step's
+    out and top-k rows bit for bit, and leaves the layer's histogram zero
+    (the state the next replay's logits launch adds into)."""
+    case = (4, 1, True, False, [5000, 4100, 3000, 6100])
+    (m, ops, w, lat0, ik0, q, idx_q, idx_w, kv_c, k_pe, idx_k, bt, sl,
+     slot) = _case(pkg, dev, case, seed=11)
+    B = q.shape[0]
+    L = m.DsaLayer(w, lat0.clone(), ik0.clone())
+    args = (q, idx_q, idx_w, bt, sl, kv_c, k_pe, idx_k, slot)
+    want = L.decode(*args).clone()
+    want_idx = L.last_idx.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    res = {}
+    with torch.cuda.stream(s):
+        L.decode(*args)  # warm-up outside the capture
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            res["out"] = L.decode(*args)
+            res["idx"] = L.last_idx
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(3):
+        res["out"].fill_(0)
+        res["idx"].fill_(-7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(res["out"].view(torch.int16), want.view(torch.int16))
+        assert torch.equal(res["idx"], want_idx)
+        assert not L._zero_hist(B, dev).any()
