@@ -85,7 +85,8 @@ struct MlaParams {
   // 1: a key in range whose row does not resolve is a zero key with score 0
   // (row code -2); 0: such a key is masked (-1)
   int zero_unresolved;
-  int xcd_map;  // 1: decode workgroup order is XCD-aware (grid a multiple of 8)
+  int xcd_map;  // decode workgroup order (grid a multiple of 8): 0 plain; 1 a (token,
+                // split)'s head groups share an XCD; 2 a (token, head group)'s splits do
 };
 
 template <int HW, int KW, int NB>
@@ -687,14 +688,21 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int c = lane & 15, g = lane >> 4;
-  // work item: head group fastest, then split, then token; with the XCD
+  // work item: head group fastest, then split, then token (xcd_map 0, 1) or
+  // split fastest, then head group, then token (xcd_map 2); with an XCD
   // mapping, consecutive items share an XCD (workgroup i runs on XCD i % 8)
   const int G = (p.n_head + 15) / 16;
   const int nwg = (int)gridDim.x;
   const int item = p.xcd_map ? ((int)blockIdx.x % 8) * (nwg / 8) + (int)blockIdx.x / 8
                              : (int)blockIdx.x;
-  const int h0 = (item % G) * 16;
-  const int split = (item / G) % p.n_splits;
+  int h0, split;
+  if (p.xcd_map == 2) {
+    split = item % p.n_splits;
+    h0 = ((item / p.n_splits) % G) * 16;
+  } else {
+    h0 = (item % G) * 16;
+    split = (item / G) % p.n_splits;
+  }
   const int b = item / (G * p.n_splits);
   const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
   const int seq_len = p.seq_lens[b];
@@ -1620,10 +1628,21 @@ __device__ __forceinline__ int merge_dim(int i) {
   return 64 * (i >> 4) + 16 * (i & 3) + 4 * ((i >> 2) & 3);
 }
 
+// gpx > 0: the decode ran with xcd_map 2, gpx (token, head group) groups of
+// its splits per XCD; workgroup i then merges a (token, head) of a group on
+// XCD i % 8, whose partials that XCD's L2 still holds.
 __global__ void __launch_bounds__(128) sparse_mla_merge_kernel(
     const f16* __restrict__ part_o, const float* __restrict__ part_ml,
-    f16* __restrict__ O, float* __restrict__ LSE, int n_splits, float empty_lse) {
-  const int64_t bh[1] = {blockIdx.x};
+    f16* __restrict__ O, float* __restrict__ LSE, int n_splits, float empty_lse, int n_head,
+    int gpx) {
+  int64_t bh0 = blockIdx.x;
+  if (gpx > 0) {
+    const int x = (int)blockIdx.x % 8, k = (int)blockIdx.x / 8;
+    const int group = x * gpx + k / 16;  // token * G + head group
+    const int G = n_head / 16;
+    bh0 = (int64_t)(group / G) * n_head + (group % G) * 16 + k % 16;
+  }
+  const int64_t bh[1] = {bh0};
   const int i[1] = {(int)threadIdx.x};
   f16x4 o4[1];
   float m[1], l[1];
@@ -1908,7 +1927,7 @@ static int mla_decode_impl(
     int rc = launch_attn_f16(prm, dim3(B, (n_head + 63) / 64, S), st);
     if (rc != MI355_DSA_OK || S == 1) return rc;
     sparse_mla_merge_kernel<<<dim3((unsigned)((int64_t)B * n_head)), 128, 0, st>>>(
-        prm.part_o, prm.part_ml, prm.o, prm.lse, S, prm.empty_lse);
+        prm.part_o, prm.part_ml, prm.o, prm.lse, S, prm.empty_lse, n_head, 0);
     return check_launch("sparse_mla_merge");
   }
 
@@ -1943,6 +1962,12 @@ static int mla_decode_impl(
     const int64_t nwg = (int64_t)S * ((n_head + 15) / 16) * B;
     DSA_CHECK(nwg < ((int64_t)1 << 31), "sparse_mla_decode: grid too large");
     prm.xcd_map = (nwg % 8 == 0) ? 1 : 0;
+    // with the separate merge: a (token, head group)'s splits on one XCD, so
+    // that the merge reads their partials from that XCD's L2 (C3: 13.6 ->
+    // 12.2 us per layer); the fused epilogue reads every token of a head and
+    // keeps the head-group order
+    if (!epi && S > 1 && nwg % 8 == 0 && (nwg / 8) % S == 0 && n_head % 16 == 0)
+      prm.xcd_map = 2;
     sparse_mla_decode_dma_kernel<<<dim3((unsigned)nwg), kDmaThreads, sizeof(DmaSmem), st>>>(prm);
     rc = check_launch("sparse_mla_decode");
   } else {
@@ -1963,8 +1988,9 @@ static int mla_decode_impl(
       decode_epilogue_kernel<2><<<dim3((unsigned)nwg), kEpiThreads, 0, st>>>(*epi);
     return check_launch("decode_epilogue");
   }
+  const int gpx = prm.xcd_map == 2 ? (int)((int64_t)B * ((n_head + 15) / 16) / 8) : 0;
   sparse_mla_merge_kernel<<<dim3((unsigned)((int64_t)B * n_head)), 128, 0, st>>>(
-      prm.part_o, prm.part_ml, prm.o, prm.lse, S, prm.empty_lse);
+      prm.part_o, prm.part_ml, prm.o, prm.lse, S, prm.empty_lse, n_head, gpx);
   return check_launch("sparse_mla_merge");
 }
 
