@@ -469,6 +469,24 @@ __global__ void __launch_bounds__(kPkhWaves * 64, 2) indexer_logits_packed_h_ker
   pk_tile<KFP8, 2, kPkhWaves>(a, sh, q_base, (id % a.n_kt) * kPkKT);
 }
 
+// Quarter tiles: four-wave workgroups over 16 queries x 256 keys (each
+// wave: 64 keys x one 16-query block), with the four-wave kernel's LDS.  A
+// launch of at most kPkqMaxTiles full tiles runs as quarters, one per CU:
+// 11.7-12.8 us per launch against 15.6-16.4 for halves (128-row sub-chunks
+// of a causal prefill).  Larger launches gain nothing from them: two
+// quarters sharing a CU take as long as one half tile alone.
+constexpr int kPkqQT = 16;
+constexpr int64_t kPkqMaxTiles = kPkCUs / 4;
+
+template <bool KFP8>
+__global__ void __launch_bounds__(kPkhWaves * 64, 2) indexer_logits_packed_q_kernel(PkArgs a) {
+  __shared__ PkSmemH sh;
+  const int id = blockIdx.x;
+  const int q_base = (id / a.n_kt) * kPkqQT;
+  if (q_base >= a.B) return;
+  pk_tile<KFP8, 1, kPkhWaves>(a, sh, q_base, (id % a.n_kt) * kPkKT);
+}
+
 // Tiles of a launch with W full tiles that run as two half tiles.
 static int pk_split_tiles(int64_t W) {
   if (W <= kPkHalfMax) return (int)W;
@@ -575,7 +593,14 @@ extern "C" int mi355_dsa_indexer_logits_packed(
   a.n_kt = (int)n_kt;
   a.n_full = (int)(W - split);
   hipStream_t st = as_stream(stream);
-  if (W >= kPkhMinTiles) {
+  if (W <= kPkqMaxTiles) {
+    // small launches: quarter tiles, up to one per CU
+    const int64_t gq = n_kt * ((B + kPkqQT - 1) / kPkqQT);
+    if (k_fp8)
+      indexer_logits_packed_q_kernel<true><<<dim3((unsigned)gq), kPkhWaves * 64, 0, st>>>(a);
+    else
+      indexer_logits_packed_q_kernel<false><<<dim3((unsigned)gq), kPkhWaves * 64, 0, st>>>(a);
+  } else if (W >= kPkhMinTiles) {
     // large launches: four-wave 32-query workgroups, two per CU
     const int64_t gh = n_kt * ((B + kPkhQT - 1) / kPkhQT);
     DSA_CHECK(gh <= INT32_MAX, "B x max_kv too large");

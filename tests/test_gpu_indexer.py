@@ -199,7 +199,8 @@ def test_packed_matches_decode_kernel_on_dyadic(ops, dev):
 # x 256 keys; W = tiles per launch): all full (W = 200), full tiles plus a
 # tail run as half tiles (W = 260 -> 256 + 4 split; W = 280 with a partial
 # last query tile -> 256 + 24 split), and the fp8-key variant of the mixed
-# case.
+# case; launches of at most 64 tiles as 16-query quarter tiles, and of
+# 65-128 tiles as half tiles.
 SPLIT = [
     # seed, B, max_kv, fp8
     (31, 128, 256 * 100, False),
@@ -210,6 +211,12 @@ SPLIT = [
     (35, 128, 256 * 200, False),
     (36, 100, 256 * 200, True),      # a partial 32-query tile
     (37, 1000, 256 * 24, False),
+    # <= 64 full tiles: quarter tiles (16 queries), one per CU
+    (38, 128, 256 * 30, False),
+    (39, 37, 256 * 20, False),       # a partial 16-query tile
+    (40, 64, 256 * 50, True),
+    # 65-128 full tiles: every tile as two halves
+    (41, 128, 256 * 50, False),
 ]
 
 
@@ -232,7 +239,7 @@ def test_packed_tile_split(ops, dev, case):
     ops.sm70_indexer_logits_packed(b, O.pack_indexer_q(q).to(dev), kc.to(dev), w.to(dev),
                                    bt.to(dev), seq.to(dev))
     got = b.cpu()
-    rows = [0, 31, 32, 63, 64, B - 1]
+    rows = sorted({r for r in (0, 15, 16, 31, 32, 63, 64, B - 1) if r < B})
     if fp8:
         flat = kc.view(-1, 132)
         k16 = (O.e4m3_decode(flat[:, :128].contiguous()) *
