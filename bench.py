@@ -922,8 +922,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures the hot path on one GPU only; multi-GPU runs are "
-              "not part of this build (see DESIGN.md for how the path shards).",
-              file=sys.stderr)
+              "not part of this build (--gpus 1).", file=sys.stderr)
         sys.exit(2)
     import torch
 
