@@ -68,6 +68,12 @@ DECODE = [
     (4, 4, 64, 60, 64, True, 2048, [3800, 3800, 3800, 3800]),
     (5, 1, 128, 40, 64, False, 1024, [2400]),         # two 64-head groups
     (6, 2, 16, 30, 48, True, 512, [1400, 500]),      # page size not a power of two
+    # fp8 split decode with the merge numbered onto each token's XCDs: 8 / B
+    # XCDs per token (B = 1: 8, B = 8: 1), and B = 3, which takes plain order
+    (7, 1, 64, 40, 64, True, 2048, [2500]),
+    (8, 8, 16, 40, 64, True, 512, [2000, 1500, 700, 512, 90, 2400, 1, 1800]),
+    (9, 1, 16, 30, 64, True, 1024, [1500]),
+    (11, 3, 64, 40, 64, True, 2048, [2500, 2100, 900]),
 ]
 
 
