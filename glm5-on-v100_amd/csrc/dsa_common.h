@@ -253,6 +253,28 @@ __device__ uint32_t block_excl_scan_n(uint32_t v, uint32_t* wsum, uint32_t* tota
   return res;
 }
 
+// Block-wide exclusive prefix sum with one barrier: every wave reads all the
+// wave totals and scans them itself.  wsum holds 2 * NT/64 words, one half
+// per parity; consecutive calls must alternate the parity, so that a call's
+// writes never meet the previous call's reads (two calls of one parity are
+// separated by the barrier of the call between them).  *total gets the sum.
+template <int NT>
+__device__ uint32_t block_excl_scan1(uint32_t v, uint32_t* wsum, int parity, uint32_t* total) {
+  constexpr int NW = NT / 64;
+  static_assert(NW >= 1 && NW <= 64, "one wave scans the wave totals");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t* ws = wsum + parity * NW;
+  const uint32_t x = wave_incl_scan(v);
+  if (lane == 63) ws[wave] = x;
+  __syncthreads();
+  const uint32_t t = lane < NW ? ws[lane] : 0u;
+  const uint32_t y = wave_incl_scan(t);  // inclusive over the wave totals
+  const uint32_t before =
+      wave == 0 ? 0u : (uint32_t)__builtin_amdgcn_readlane((int)y, wave - 1);
+  *total = (uint32_t)__builtin_amdgcn_readlane((int)y, NW - 1);
+  return before + x - v;
+}
+
 // Reductions over the 64 lanes of a wave (all lanes active), the same value
 // in every lane: DPP steps within each 16-lane row, then the four row results
 // read with v_readlane (no LDS traffic, unlike a shuffle).

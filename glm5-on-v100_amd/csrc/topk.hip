@@ -688,9 +688,8 @@ constexpr int kSelBins = 1024;
 
 struct ScanShared {
   float v[kScanTile];
-  uint32_t wsum[kScanThreads / 64 + 1];
+  uint32_t wsum[2 * (kScanThreads / 64)];
   int T;
-  int status;
 };
 
 struct TopkWs {
@@ -754,14 +753,10 @@ __global__ void __launch_bounds__(kScanThreads) topk_scan_kernel(
     hb[i] = h[PER * threadIdx.x + i];
     cs += hb[i];
   }
+  if (threadIdx.x == 0) sh.T = -1;  // before the scan's barrier
   uint32_t total;
-  const uint32_t excl = block_excl_scan_n<kScanThreads>(cs, sh.wsum, &total);
-  if (threadIdx.x == 0) {
-    sh.T = -1;
-    sh.status = (total == (uint32_t)L) ? 0 : 1;
-  }
-  __syncthreads();
-  if (sh.status != 0) {
+  const uint32_t excl = block_excl_scan1<kScanThreads>(cs, sh.wsum, 0, &total);
+  if (total != (uint32_t)L) {  // the histogram does not count the row's L keys
     if (tile == 0 && threadIdx.x == 0) ws.meta[(int64_t)b * 4 + 2] = 1;
     return;
   }
@@ -792,7 +787,7 @@ __global__ void __launch_bounds__(kScanThreads) topk_scan_kernel(
     n += cand ? 1u : 0u;
   }
   uint32_t tot;
-  uint32_t off = block_excl_scan_n<kScanThreads>(n, sh.wsum, &tot);
+  uint32_t off = block_excl_scan1<kScanThreads>(n, sh.wsum, 1, &tot);
   const int64_t slot0 = ((int64_t)b * n_tiles + tile) * kScanTile;
 #pragma unroll
   for (int e = 0; e < 4; e++) {
@@ -816,28 +811,29 @@ struct SelShared {
       int32_t toff[1024 + 1];
     } c;
   } u;
-  uint32_t wsum[kTkWaves + 1];
-  int T;
-  uint32_t above;
+  uint32_t wsum[2 * kTkWaves];
+  int T[2];
+  uint32_t above[2];
   int n_cand;
 };
 
 // Bin T of an nbins (<= 1024) LDS histogram with above(T) < need <=
-// above(T) + hist[T]; one bin per thread.
+// above(T) + hist[T]; one bin per thread.  par: the parity of this block
+// scan (block_excl_scan1); it also selects the broadcast slot, so two calls
+// of one parity are separated by the barriers of the call between them.
 __device__ void sel_threshold(SelShared& sh, const uint32_t* hist, int nbins, uint32_t need,
-                              int* T, uint32_t* above) {
+                              int par, int* T, uint32_t* above) {
   const uint32_t hv = (int)threadIdx.x < nbins ? hist[threadIdx.x] : 0u;
   uint32_t total;
-  const uint32_t excl = block_excl_scan_n<kTkThreads>(hv, sh.wsum, &total);
+  const uint32_t excl = block_excl_scan1<kTkThreads>(hv, sh.wsum, par, &total);
   const uint32_t a = total - excl - hv;  // keys in higher bins
   if ((int)threadIdx.x < nbins && a < need && a + hv >= need) {
-    sh.T = threadIdx.x;
-    sh.above = a;
+    sh.T[par] = threadIdx.x;
+    sh.above[par] = a;
   }
   __syncthreads();
-  *T = sh.T;
-  *above = sh.above;
-  __syncthreads();
+  *T = sh.T[par];
+  *above = sh.above[par];
 }
 
 // Row b of the select (every return is workgroup-uniform).
@@ -853,8 +849,9 @@ __device__ __forceinline__ void topk_select_row(
       (uint32_t)ws.counts[(int64_t)b * n_tiles + min((int)threadIdx.x, n_tiles - 1)];
   const int status = ws.meta[(int64_t)b * 4 + 2];
   const uint32_t above1 = (uint32_t)ws.meta[(int64_t)b * 4 + 1];
+  const int T1 = ws.meta[(int64_t)b * 4 + 0];
   int L = seq_lens[b];
-  asm volatile("" ::"v"(cnt_own), "v"(status), "v"(above1), "v"(L));
+  asm volatile("" ::"v"(cnt_own), "v"(status), "v"(above1), "v"(T1), "v"(L));
   L = L < 0 ? 0 : (L > max_kv ? max_kv : L);
   if (L <= K) {
     for (int p = threadIdx.x; p < K; p += kTkThreads) out[p] = (p < L) ? p : -1;
@@ -867,13 +864,16 @@ __device__ __forceinline__ void topk_select_row(
     return;
   }
   const int used_tiles = (L + kScanTile - 1) / kScanTile;  // <= n_tiles <= 1024
+  // the second-level histogram starts zero (the scan's barrier orders this
+  // before the gather's counts)
+  for (int i = threadIdx.x; i < kSelBins; i += kTkThreads) sh.u.c.hist[i] = 0u;
   // ---- tile offsets of the candidate lists ----
   int total_c;
   {
     const int t = threadIdx.x;
     const uint32_t n = t < used_tiles ? cnt_own : 0u;
     uint32_t tot;
-    const uint32_t ex = block_excl_scan_n<kTkThreads>(n, sh.wsum, &tot);
+    const uint32_t ex = block_excl_scan1<kTkThreads>(n, sh.wsum, 0, &tot);
     if (t < used_tiles) sh.u.c.toff[t] = (int)ex;
     total_c = (int)tot;
   }
@@ -884,7 +884,8 @@ __device__ __forceinline__ void topk_select_row(
   }
   if (threadIdx.x == 0) sh.u.c.toff[used_tiles] = total_c;
   __syncthreads();
-  // ---- gather the candidates into LDS (tile lists are position ordered) ----
+  // ---- gather the candidates into LDS (tile lists are position ordered);
+  // the keys of bin T1 are counted by their next 10 bits on the way ----
   // Flat over the candidate index: candidate i lives in the tile t with
   // toff[t] <= i < toff[t+1] (binary search in LDS), so every thread's loads
   // are independent and kGatherU of them are in flight at once.
@@ -912,22 +913,16 @@ __device__ __forceinline__ void topk_select_row(
       if (i < total_c) {
         sh.u.c.ckey[i] = kk[u];
         sh.u.c.cpos[i] = pp[u];
+        if ((int)(kk[u] >> 20) == T1) atomicAdd(&sh.u.c.hist[(kk[u] >> 10) & 1023], 1u);
       }
     }
   }
-  for (int i = threadIdx.x; i < kSelBins; i += kTkThreads) sh.u.c.hist[i] = 0u;
   __syncthreads();
   // ---- exact threshold among the T1 keys: bits [10,20), then [0,10) ----
-  const int T1 = ws.meta[(int64_t)b * 4 + 0];
   const uint32_t need1 = (uint32_t)K - above1;  // keys to take from bin T1
-  for (int i = threadIdx.x; i < total_c; i += kTkThreads) {
-    const uint32_t k = sh.u.c.ckey[i];
-    if ((int)(k >> 20) == T1) atomicAdd(&sh.u.c.hist[(k >> 10) & 1023], 1u);
-  }
-  __syncthreads();
   int T2;
   uint32_t above2;
-  sel_threshold(sh, sh.u.c.hist, kSelBins, need1, &T2, &above2);
+  sel_threshold(sh, sh.u.c.hist, kSelBins, need1, 1, &T2, &above2);
   const uint32_t need2 = need1 - above2;
   const uint32_t pre2 = ((uint32_t)T1 << 10) | (uint32_t)T2;  // top 22 bits
   // The T1 keys (a few hundred) spread over 1024 second-level bins, so bin T2
@@ -936,6 +931,7 @@ __device__ __forceinline__ void topk_select_row(
   const bool whole = sh.u.c.hist[T2] == need2;
   uint32_t tau, take_eq;
   int sh_bits;  // keys compare as k >> sh_bits against tau
+  int par = 0;  // parity of the compaction's block scan
   if (whole) {
     tau = pre2;
     take_eq = need2;
@@ -951,7 +947,8 @@ __device__ __forceinline__ void topk_select_row(
     __syncthreads();
     int T3;
     uint32_t above3;
-    sel_threshold(sh, sh.u.c.hist, kSelBins, need2, &T3, &above3);
+    sel_threshold(sh, sh.u.c.hist, kSelBins, need2, 0, &T3, &above3);
+    par = 1;
     tau = (pre2 << 10) | (uint32_t)T3;
     take_eq = need2 - above3;  // keys equal to tau to take, lowest positions
     sh_bits = 0;
@@ -965,7 +962,7 @@ __device__ __forceinline__ void topk_select_row(
     packed += (k > tau ? 1u : 0u) + (k == tau ? (1u << 16) : 0u);
   }
   uint32_t tot;
-  const uint32_t ex = block_excl_scan_n<kTkThreads>(packed, sh.wsum, &tot);
+  const uint32_t ex = block_excl_scan1<kTkThreads>(packed, sh.wsum, par, &tot);
   uint32_t gt = ex & 0xFFFFu, eq = ex >> 16;
   for (int i = i0; i < i1; i++) {
     const uint32_t k = sh.u.c.ckey[i] >> sh_bits;
