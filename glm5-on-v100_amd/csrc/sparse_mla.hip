@@ -741,14 +741,23 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
 
   // ---- this wave's 16 raw rows into its LDS region: piece q = 64u + lane
   // is key q / 41, 16-byte chunk q % 41 (the last round has 16 pieces) ----
+  // The piece sources come first, all eleven cross-lane reads of the row
+  // codes in flight together; interleaved with the DMAs, each read waited
+  // for its own LDS round trip before the next gather went out.
   uint8_t* reg = sh.rows[w];
+  int rcv[kDecWaveRounds];
+#pragma unroll
+  for (int u = 0; u < kDecWaveRounds; u++) {
+    const int q = 64 * u + lane;
+    rcv[u] = __shfl(code, (q < kDecWavePieces ? q : 0) / 41, 64);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every shuffle is issued before the first is used
 #pragma unroll
   for (int u = 0; u < kDecWaveRounds; u++) {
     const int q = 64 * u + lane;
     const int r = (q < kDecWavePieces ? q : 0) / 41, ch = q - r * 41;
-    const int rc = __shfl(code, r, 64);
-    const uint8_t* src = rc >= 0 ? kv + (int64_t)rc * kDsmlaRowBytes + 16 * ch
-                                 : kZeroRow + 16 * (q < kDecWavePieces ? ch : 0);
+    const uint8_t* src = rcv[u] >= 0 ? kv + (int64_t)rcv[u] * kDsmlaRowBytes + 16 * ch
+                                     : kZeroRow + 16 * (q < kDecWavePieces ? ch : 0);
     if (u + 1 < kDecWaveRounds || lane < kDecWavePieces - 64 * (kDecWaveRounds - 1))
       dma16(src, reg + 1024 * u);
   }
