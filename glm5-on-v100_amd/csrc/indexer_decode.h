@@ -148,6 +148,20 @@ __device__ __forceinline__ void indexer_logits_body(
     int page_shift, int max_kv, int hist8, int tile, int b, const IdxNewKeys& nk) {
   const int p_lo = tile * kIdxPPB;
   const int p_hi = min(p_lo + kIdxPPB, max_kv);
+  // The block-table entries of the tile's pages are loaded beside seq_len
+  // (one round trip instead of two before the first key load); a tile past
+  // the context reads them for nothing.
+  constexpr int kNT = kIdxWaves * 64;
+  constexpr int kBtRegs = (kIdxPPB + 2 + kNT - 1) / kNT;
+  const int pg0 = p_lo >> page_shift;
+  const int npg = ((p_hi - 1) >> page_shift) - pg0 + 1;
+  const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
+  int32_t btv[kBtRegs];
+#pragma unroll
+  for (int k = 0; k < kBtRegs; k++) {
+    const int i = (int)threadIdx.x + kNT * k;
+    btv[k] = (i < npg && pg0 + i < max_blocks) ? bt_row[pg0 + i] : -1;
+  }
   const int seq_len = seq_lens[b];
   float* srow = score + (int64_t)b * max_kv;
 
@@ -161,11 +175,11 @@ __device__ __forceinline__ void indexer_logits_body(
   __shared__ uint32_t s_hist[kTopkBins];
   __shared__ int32_t s_new[NEWK ? 2 * kIdxMaxNew : 1];  // slots, then "this workgroup reads it"
   const int page = 1 << page_shift;
-  const int pg0 = p_lo >> page_shift;
-  const int npg = ((p_hi - 1) >> page_shift) - pg0 + 1;
-  const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
-  for (int i = threadIdx.x; i < npg; i += blockDim.x)
-    s_bt[i] = (pg0 + i < max_blocks) ? bt_row[pg0 + i] : -1;
+#pragma unroll
+  for (int k = 0; k < kBtRegs; k++) {
+    const int i = (int)threadIdx.x + kNT * k;
+    if (i < npg) s_bt[i] = btv[k];
+  }
   if (hist != nullptr)
     for (int i = threadIdx.x; i < kTopkBins; i += blockDim.x) s_hist[i] = 0u;
   if constexpr (NEWK) {
