@@ -153,3 +153,36 @@ def test_persistent_topk_causal_block(ops, dev):
     ops.persistent_topk(s.to(dev), seq.view(R, 1).to(dev), out,
                         torch.empty(1 << 20, dtype=torch.uint8, device=dev), 2048, W)
     assert torch.equal(out.cpu(), cref.topk_rows(s, seq, 2048))
+
+
+def _random_cases(n=16, seed=1234):
+    """Deterministic random shapes for the decode top-k: row counts on both
+    sides of the two-kernel limit, widths up to 180k, K from 1 to 4095,
+    seq_len from 0 to the width, every score kind above."""
+    import random
+    rng = random.Random(seed)
+    kinds = ["randn", "ties", "equal", "narrow", "rising", "falling", "mixed"]
+    out = []
+    for i in range(n):
+        kind = rng.choice(kinds)
+        B = rng.choice([1, 2, 3, 4, 7, 16, 33, 64, 65])
+        W = rng.choice([2100, 4096, 9000, 20000, 65536, 184320])
+        while B * W > 3_000_000:
+            B = max(1, B // 2)
+        K = rng.choice([1, 7, 100, 512, 2047, 2048, 4095])
+        seq = [rng.choice([W, W - rng.randrange(0, max(1, W // 2)), rng.randrange(0, W + 1)])
+               for _ in range(B)]
+        out.append((i, kind, B, W, K, seq))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_cases(), ids=lambda c: f"r{c[0]}-{c[1]}-{c[2]}x{c[3]}-k{c[4]}")
+def test_decode_topk_random_shapes(ops, dev, case):
+    """Randomised shapes and lengths, bit-exact against the C oracle."""
+    i, kind, B, W, K, seq = case
+    g = torch.Generator().manual_seed(1000 + i)
+    s = scores(kind, B, W, g)
+    seq = torch.tensor(seq, dtype=torch.int32)
+    idx = torch.full((B, K), 123, dtype=torch.int32, device=dev)
+    ops.sm70_decode_topk(idx, s.to(dev), seq.to(dev), hist_of(s, seq).to(dev), K)
+    assert torch.equal(idx.cpu(), cref.topk_rows(s, seq, K))
