@@ -453,11 +453,12 @@ __global__ void __launch_bounds__(kPkThreads) indexer_logits_packed_kernel(PkArg
 // 32 queries, as a full tile's wave), ~68 KB of LDS with 8 KB ring slots,
 // so that two workgroups share a CU and one's prologue (64 KB of keys, the
 // first Q pairs) and epilogue (its score stores) run beside the other's
-// MFMAs.  Used for launches of at least kPkhMinTiles full tiles: 4-5 %
-// faster there, ~1 % slower on launches of a round or less.
+// MFMAs.  Used for launches of more than one round (kPkhMinTiles full
+// tiles and up): 4-5 % faster at 384 tiles and up, 0.5-1 us per launch
+// faster at 257-383, ~1 % slower on launches of a round or less.
 constexpr int kPkhWaves = 4;
 constexpr int kPkhQT = 32;
-constexpr int64_t kPkhMinTiles = 384;
+constexpr int64_t kPkhMinTiles = kPkCUs + 1;
 using PkSmemH = PkSmemT<kPkhQT>;
 
 template <bool KFP8>
@@ -487,13 +488,10 @@ __global__ void __launch_bounds__(kPkhWaves * 64, 2) indexer_logits_packed_q_ker
   pk_tile<KFP8, 1, kPkhWaves>(a, sh, q_base, (id % a.n_kt) * kPkKT);
 }
 
-// Tiles of a launch with W full tiles that run as two half tiles.
-static int pk_split_tiles(int64_t W) {
-  if (W <= kPkHalfMax) return (int)W;
-  if (W <= kPkCUs) return 0;
-  const int r = (int)(W % kPkCUs);
-  return r <= kPkHalfMax ? r : 0;
-}
+// Tiles of a launch with W full tiles that run as two half tiles: all of
+// them up to kPkHalfMax tiles (launches of more than one round take the
+// four-wave kernel instead).
+static int pk_split_tiles(int64_t W) { return W <= kPkHalfMax ? (int)W : 0; }
 
 }  // namespace mi355dsa
 

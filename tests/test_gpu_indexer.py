@@ -196,18 +196,17 @@ def test_packed_matches_decode_kernel_on_dyadic(ops, dev):
 
 
 # Launch shapes of the packed kernel's tile split (full tiles are 64 queries
-# x 256 keys; W = tiles per launch): all full (W = 200), full tiles plus a
-# tail run as half tiles (W = 260 -> 256 + 4 split; W = 280 with a partial
-# last query tile -> 256 + 24 split), and the fp8-key variant of the mixed
-# case; launches of at most 64 tiles as 16-query quarter tiles, and of
-# 65-128 tiles as half tiles.
+# x 256 keys; W = tiles per launch): all full (W = 200); more than one round
+# (W = 260, 280 with a partial last query tile, and fp8 keys), which takes
+# the four-wave 32-query kernel; launches of at most 64 tiles as 16-query
+# quarter tiles, and of 65-128 tiles as half tiles.
 SPLIT = [
     # seed, B, max_kv, fp8
     (31, 128, 256 * 100, False),
     (32, 128, 256 * 130, False),
     (33, 100, 256 * 140, False),
     (34, 128, 256 * 130, True),
-    # >= 384 full tiles: the four-wave 32-query kernel
+    # more full tiles: the four-wave 32-query kernel as well
     (35, 128, 256 * 200, False),
     (36, 100, 256 * 200, True),      # a partial 32-query tile
     (37, 1000, 256 * 24, False),
