@@ -203,14 +203,27 @@ def unpack_indexer_q(qp: torch.Tensor, n: int) -> torch.Tensor:
 
 
 def indexer_logits_packed(qp: torch.Tensor, k_cache, w, bt, seq_lens, max_kv,
-                          dtype=torch.float64):
-    """Prefill logits from packed Q; every query tile gathers keys with the
-    block-table row of the call's first row (sm70_mla_decode.cu:566-567);
-    callers pass one shared row, expanded."""
+                          dtype=torch.float64, qt: int = 32):
+    """Prefill logits from packed Q (sm70_mla_decode.cu:542-653).  Two
+    things differ from the decode kernel's contract:
+      * every 32-query tile gathers its keys with the block-table row of the
+        tile's first query, qbase = tile * 32 (:556, :566; QT = 32, :548);
+        rows of the tile below it are not consulted (callers pass one row,
+        expanded, sparse_attn_indexer.py:764-781);
+      * an fp8 key is dequantised to fp16 before the dot:
+        fp16_rn(fp32(e4m3 * scale)) (idxk_fp8_load4 :106-115, then
+        __float2half into the key tile, :561-580); fp16 keys are used as
+        stored."""
     B = w.shape[0]
     q = unpack_indexer_q(qp, B)
-    bt0 = bt[:1].expand(B, bt.shape[1])
-    return indexer_logits(q, k_cache, w, bt0, seq_lens, max_kv, dtype)[0]
+    first = (torch.arange(B) // qt) * qt
+    bt_tile = bt.index_select(0, first)
+    if k_cache.dtype == torch.uint8:
+        flat = k_cache.reshape(-1, IDXK_FP8_ROW_BYTES)
+        k16 = (e4m3_decode(flat[:, :128].contiguous()) *
+               flat[:, 128:132].contiguous().view(torch.float32)).to(torch.float16)
+        k_cache = k16.view(*k_cache.shape[:-1], 128)
+    return indexer_logits(q, k_cache, w, bt_tile, seq_lens, max_kv, dtype)[0]
 
 
 # ---------------------------------------------------------------------------

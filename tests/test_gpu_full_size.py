@@ -49,18 +49,24 @@ def test_c4_last_indexer_subchunk(ops, dev, idx_chunk):
     assert torch.equal(out.cpu()[rows], wt)
 
 
-@pytest.mark.parametrize("fp8", [True, False], ids=["fp8", "fp16"])
-def test_c4_sparse_prefill_launch(ops, pkg, dev, fp8):
+@pytest.mark.parametrize("fp8,o1", [(True, False), (False, False), (False, True)],
+                         ids=["fp8", "fp16", "fp16_o1"])
+def test_c4_sparse_prefill_launch(ops, pkg, dev, fp8, o1):
     """The last 4096-token launch of the 64k causal prefill (64 heads, top-2048
     spread over each token's causal range), fp8_ds_mla or fp16 latent cache of
-    the sequence."""
+    the sequence.  The spec data (latents and q N(0,1)/24) give a near-uniform
+    softmax and |o| ~ 1e-3; o1=True uses N(0,1) latents and 2 N(0,1) q, so
+    that o is O(1) and the tolerance binds (the fp8 cache's O(1) companion,
+    with four different tile scales per row, is in test_gpu_tile_scales.py)."""
     S = pkg.synthetic
     g = torch.Generator(device=dev)
     g.manual_seed(102)
     sub = 4096
     kv = S.latent_cache(T, fp8, g, dev)
+    if o1:
+        kv = (kv.float() * 24.0).to(torch.float16)
     bt = torch.randperm(NBLK, generator=g, device=dev).to(torch.int32)[None].expand(sub, NBLK).contiguous()
-    q = (torch.randn(sub, 64, 576, generator=g, device=dev) / 24.0).to(torch.float16)
+    q = (torch.randn(sub, 64, 576, generator=g, device=dev) * (2.0 if o1 else 1 / 24.0)).to(torch.float16)
     t = torch.arange(T - sub, T, device=dev, dtype=torch.float64)
     n = t + 1
     j = torch.arange(2048, device=dev, dtype=torch.float64)
@@ -75,3 +81,5 @@ def test_c4_sparse_prefill_launch(ops, pkg, dev, fp8):
                           seq[sel].cpu(), 576 ** -0.5)
     torch.testing.assert_close(o[sel].float().cpu(), ro, rtol=2e-3, atol=1e-3)
     assert (lse[sel].cpu() - rl).abs().max() <= 1e-4
+    if o1:
+        assert float(ro.abs().mean()) > 0.05

@@ -135,3 +135,48 @@ def test_pack_q_layout():
         want = q[tok, h, 16 * kt + c] if tok < n else 0.0
         assert float(qp[h, t, kt, r, c]) == float(want)
     assert torch.equal(O.unpack_indexer_q(qp, n), q)
+
+
+def test_packed_uses_each_tiles_first_row():
+    """The packed kernel gathers a 32-query tile's keys with the table row of
+    the tile's first query (sm70_mla_decode.cu:556, :566): rows 0-31 use
+    bt[0], rows 32-63 bt[32], rows 64-69 bt[64]; the other rows' tables are
+    never read."""
+    g = torch.Generator().manual_seed(5)
+    page, nblk, B, max_kv = 8, 9, 70, 48
+    kc = torch.randn(nblk, page, 128, generator=g).to(torch.float16)
+    q = torch.randn(B, 32, 128, generator=g).to(torch.float16)
+    w = torch.randn(B, 32, generator=g).to(torch.float16)
+    bt = torch.stack([torch.randperm(nblk, generator=g)[:6] for _ in range(B)]).to(torch.int32)
+    seq = torch.randint(1, max_kv + 1, (B,), generator=g).to(torch.int32)
+    got = O.indexer_logits_packed(O.pack_indexer_q(q), kc, w, bt, seq, max_kv)
+    first = torch.tensor([0] * 32 + [32] * 32 + [64] * 6)
+    want = brute_logits(q, kc.view(-1, 128), w, bt[first], seq, page, max_kv)
+    fin = torch.isfinite(want)
+    assert torch.equal(torch.isinf(got), ~fin)
+    assert torch.allclose(got[fin].double(), want[fin], rtol=1e-6, atol=1e-5)
+    per_row, _ = O.indexer_logits(q, kc, w, bt, seq, max_kv)
+    assert not torch.equal(per_row[1:32], got[1:32])  # the distinction is visible
+
+
+def test_packed_fp8_keys_round_to_fp16_first():
+    """Known answer: a key byte 0x39 (e4m3 1.125) with scale 1 + 2^-12.  The
+    decode kernel multiplies the fp32 dot by the scale: 1.125 * (1 + 2^-12);
+    the packed kernel rounds the dequantised key to fp16 first
+    (sm70_mla_decode.cu:561-580): fp16_rn(1.12527...) = 1.125."""
+    page = 4
+    row = torch.zeros(132, dtype=torch.uint8)
+    row[0] = 0x39
+    row[128:132] = torch.tensor([1 + 2 ** -12], dtype=torch.float32).view(torch.uint8)
+    assert float(O.e4m3_decode(row[:1])) == 1.125
+    kc = row[None].repeat(page, 1).view(1, page, 132)
+    q = torch.zeros(1, 32, 128, dtype=torch.float16)
+    q[0, 0, 0] = 1
+    w = torch.zeros(1, 32, dtype=torch.float16)
+    w[0, 0] = 1
+    bt = torch.zeros(1, 1, dtype=torch.int32)
+    seq = torch.tensor([page], dtype=torch.int32)
+    packed = O.indexer_logits_packed(O.pack_indexer_q(q), kc, w, bt, seq, page)
+    dec, _ = O.indexer_logits(q, kc, w, bt, seq, page)
+    assert torch.all(packed == 1.125)
+    assert torch.all(dec == torch.tensor(1.125 * (1 + 2 ** -12), dtype=torch.float32))
