@@ -121,10 +121,21 @@ def capture(torch, fn):
     return g
 
 
+def cache_copies(cache_bytes, layers, pool_bytes=3 << 30):
+    """Distinct latent caches the timed decode graph rotates over: enough that
+    their total (at least 3 GB, and at least 8 caches) dwarfs the 256 MB MALL,
+    so a layer's gathered rows were last touched several GB of traffic ago."""
+    return max(1, min(layers, max(8, -(-pool_bytes // cache_bytes))))
+
+
 def bench_decode(torch, pkg, dev, ctx, layers, steps, warmup, seed=3):
+    """C3 decode: `layers` layers with their own q and idx, layer l reading
+    cache copy l % n (cache_copies), replayed from one HIP graph."""
     S = pkg.synthetic
     ops = pkg._sm70_ops
     d = S.decode_inputs(B=4, H=64, ctx=ctx, topk=2048, fp8=True, device=dev, seed=seed)
+    n_kv = cache_copies(d["kv"].numel(), layers)
+    kvs = [d["kv"]] + [d["kv"].clone() for _ in range(n_kv - 1)]
     g = torch.Generator(device=dev)
     g.manual_seed(seed + 100)
     idxs = [S.sorted_unique_positions(4, 2048, ctx, g, dev) for _ in range(layers)]
@@ -132,16 +143,17 @@ def bench_decode(torch, pkg, dev, ctx, layers, steps, warmup, seed=3):
           for _ in range(layers)]
     outs = [torch.empty(4, 64, 512, dtype=torch.float16, device=dev) for _ in range(layers)]
     lses = [torch.empty(4, 64, device=dev) for _ in range(layers)]
+    d["n_caches"] = n_kv
 
     def run():
         for l in range(layers):
-            ops.sm70_sparse_mla_decode(outs[l], lses[l], qs[l], d["kv"], idxs[l], d["bt"],
+            ops.sm70_sparse_mla_decode(outs[l], lses[l], qs[l], kvs[l % n_kv], idxs[l], d["bt"],
                                        d["seq"], d["scale"])
 
     graph = capture(torch, run)
     ms = time_graph(torch, graph, steps, warmup)
     assert all(torch.isfinite(o).all() for o in outs[:2])
-    del graph
+    del graph, kvs[1:]
     return ms, d, idxs, qs
 
 
@@ -969,9 +981,13 @@ def main():
         "config": {
             "workload": ("C3 sparse MLA decode: B=4 tokens, 64 heads, qk 576 / v 512, "
                          "topk 2048, ctx 184320, fp8_ds_mla paged cache (page 64, "
-                         "11520 pages), one step = %d layers replayed from a HIP graph" % L),
+                         "11520 pages), one step = %d layers replayed from a HIP graph, "
+                         "layer l reading cache copy l %% %d (distinct %d MB caches, so the "
+                         "gathered rows come from HBM, not the 256 MB MALL)"
+                         % (L, d["n_caches"], d["kv"].numel() >> 20)),
             "batch": 4, "heads": 64, "topk": 2048, "ctx": 184320, "kv": "fp8_ds_mla",
             "layers_per_step": L,
+            "distinct_caches": d["n_caches"],
             # the library's split count at this shape (BASELINE C3 names 8; results
             # are split-invariant, tested); each split is one 128-key workgroup
             "splits": decode_splits(pkg, 4),
