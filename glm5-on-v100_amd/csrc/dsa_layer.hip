@@ -297,6 +297,7 @@ extern "C" int mi355_dsa_decode_layer_indexer(
   a.nk.ik = reinterpret_cast<const u32x4*>(idx_k);
   a.nk.slot = idx_slot;
   a.nk.T = T;
+  a.nk.dst = idx_cache;
   a.n_pro = (int)n_pro;
   a.n_tiles = (max_kv + kIdxPPB - 1) / kIdxPPB;
   const int64_t total = n_pro + (int64_t)a.n_tiles * B;

@@ -116,6 +116,8 @@ struct IdxNewKeys {
   const u32x4* ik;      // [T][16] 16-byte chunks
   const int32_t* slot;  // [T]; slots < 0 or >= n_kv_rows are not written
   int T;                // <= kIdxMaxNew
+  void* dst;            // the index-key cache they are written to: the memory
+                        // the launch also reads keys from (Kv)
 };
 
 // One indexer-K row written as the cache's store kernel writes it: 16 lanes
@@ -139,10 +141,11 @@ __device__ __forceinline__ void idx_key_row_store(const u32x4 raw, void* dst, in
 // code without that step.
 // (The pointers are restrict parameters of this function, not fields read
 // from a struct, so that the compiler keeps knowing that the score stores
-// do not alias the key loads.)
+// do not alias the key loads.  Kv is not restrict: with NEWK the same rows
+// are written through nk.dst, and read after the workgroup barrier.)
 template <bool KFP8, bool NEWK>
 __device__ __forceinline__ void indexer_logits_body(
-    const f16* __restrict__ Q, const void* __restrict__ Kv, const f16* __restrict__ W,
+    const f16* __restrict__ Q, const void* Kv, const f16* __restrict__ W,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens,
     float* __restrict__ score, uint32_t* __restrict__ hist, int64_t n_kv_rows, int max_blocks,
     int page_shift, int max_kv, int hist8, int tile, int b, const IdxNewKeys& nk) {
@@ -216,10 +219,9 @@ __device__ __forceinline__ void indexer_logits_body(
         if (t < nk.T && s_new[kIdxMaxNew + t]) {
           const int sub = threadIdx.x & 15;
           const int64_t row = s_new[t];
-          void* dst = KFP8 ? (void*)(reinterpret_cast<uint8_t*>(const_cast<void*>(Kv)) +
+          void* dst = KFP8 ? (void*)(reinterpret_cast<uint8_t*>(nk.dst) +
                                      row * (int64_t)kIdxkFp8RowBytes)
-                           : (void*)(reinterpret_cast<f16*>(const_cast<void*>(Kv)) +
-                                     row * kIdxHeadDim);
+                           : (void*)(reinterpret_cast<f16*>(nk.dst) + row * kIdxHeadDim);
           idx_key_row_store<KFP8>(nk.ik[(int64_t)t * 16 + sub], dst, sub);
         }
       }

@@ -133,6 +133,8 @@ def v_up(o: torch.Tensor, w: DsaLayerWeights) -> torch.Tensor:
 class DsaLayer:
     """One layer's caches and weights; decode() / prefill() run a step."""
 
+    _HIST_ROWS = 64  # tokens the fused indexer launch takes per step
+
     def __init__(self, weights: DsaLayerWeights, latent_cache: torch.Tensor,
                  idx_k_cache: torch.Tensor, topk: int = 2048):
         self.w = weights
@@ -261,19 +263,24 @@ class DsaLayer:
         """The fused prologue + logits launch takes at most 64 new tokens and
         the logits op's own operand forms."""
         B = q.shape[0]
-        return (B <= 64 and idx_q.dtype == torch.float16 and idx_q.dim() == 3
+        return (B <= self._HIST_ROWS and idx_q.dtype == torch.float16 and idx_q.dim() == 3
                 and tuple(idx_q.shape) == (B, 32, 128) and idx_w.dtype == torch.float16
                 and idx_w.numel() == B * 32)
 
     def _zero_hist(self, B: int, device) -> torch.Tensor:
-        """The layer's own [B, 4096] top-k histogram, zero between steps: the
-        fused logits launch adds into it and the consuming top-k clears it."""
-        key = (B, str(device))
+        """Rows [0, B) of the layer's top-k histogram on `device`, zero
+        between steps: the fused logits launch adds into them and the
+        consuming top-k clears exactly the rows it used, so one [64, 4096]
+        buffer per device (the fused path takes at most 64 tokens) serves
+        every batch size.  The buffer is state shared by the layer's steps:
+        one DsaLayer must not be stepped on two streams at once."""
+        assert B <= self._HIST_ROWS
+        key = str(device)
         h = self._hists.get(key)
         if h is None:
-            h = torch.zeros(B, 4096, dtype=torch.int32, device=device)
+            h = torch.zeros(self._HIST_ROWS, 4096, dtype=torch.int32, device=device)
             self._hists[key] = h
-        return h
+        return h[:B]
 
     def _indexer_step(self, q, idx_q, idx_w, bt, sl, kv_c, k_pe, idx_k, slot_mapping):
         """mi355_dsa_decode_layer_indexer (the latent and indexer-K writes and
