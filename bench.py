@@ -38,6 +38,7 @@ METRIC = ("sparse MLA decode µs/layer @180k ctx (HBM GB/s); "
           "indexer prefill TFLOPS @64k")
 HBM_PEAK_GBPS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
 # The reference's own published kernel figures (NVIDIA V100, other shapes;
 # reference README.md:42-44, sm70_mla_decode.cu:483-484 and :1805-1806,
 # sm70_attn_fp8.cu:10-12), quoted beside the matching extra records.
@@ -568,13 +569,14 @@ def bench_dense_decode(torch, pkg, dev):
 def bench_varlen_prefill(torch, pkg, dev, L=16384, H=64, dqk=192, dv=128):
     """Dense varlen MLA prefill attention (the reference's _varlen_attention):
     one causal sequence of L new tokens, H heads, qk 192 / v 128, fp16 and
-    bf16.  FLOPs count the unmasked (causal) scores only."""
+    bf16 (fp16 / bf16 MFMA), and fp32 (fp32 MFMA, whose peak is 157.3
+    TFLOP/s).  FLOPs count the unmasked (causal) scores only."""
     out = {}
     g = torch.Generator(device=dev)
     g.manual_seed(11)
     cu = torch.tensor([0, L], dtype=torch.int32, device=dev)
     flops = H * (L * (L + 1) / 2) * (dqk + dv) * 2
-    for dtype in (torch.float16, torch.bfloat16):
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
         q = torch.randn(L, H, dqk, generator=g, device=dev).to(dtype)
         k = torch.randn(L, H, dqk, generator=g, device=dev).to(dtype)
         v = torch.randn(L, H, dv, generator=g, device=dev).to(dtype)
@@ -585,9 +587,13 @@ def bench_varlen_prefill(torch, pkg, dev, L=16384, H=64, dqk=192, dv=128):
 
         us = graph_time_per_call(torch, fn, 1, steps=5, warmup=1)
         tf = flops / (us * 1e-6) / 1e12
-        out["fp16" if dtype == torch.float16 else "bf16"] = {
-            "ms": round(us / 1000, 3), "tflops": round(tf, 1),
-            "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)}
+        if dtype == torch.float32:
+            out["fp32"] = {"ms": round(us / 1000, 3), "tflops": round(tf, 1),
+                           "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+        else:
+            out["fp16" if dtype == torch.float16 else "bf16"] = {
+                "ms": round(us / 1000, 3), "tflops": round(tf, 1),
+                "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)}
         del q, k, v
     out["workload"] = (f"one causal sequence of {L} tokens, {H} heads, qk {dqk} / v {dv}, "
                        "causal FLOPs only")

@@ -331,13 +331,225 @@ int dispatch_va(const VaArgs& a, int d_qk, int d_v, int num_seqs, int max_q_len,
                    "(192, 128), (128, 128), (64, 64), (256, 256)", d_qk, d_v);
 }
 
+// ---------------------------------------------------------------------------
+// fp32 inputs: the same attention in fp32 arithmetic throughout, on the fp32
+// MFMA (v_mfma_f32_16x16x4_f32), as the reference computes fp32 inputs
+// (sm70_triton.py:193 lists fp32; :54-187 runs it in fp32 torch).  Nothing
+// is rounded to 16 bits, so the whole fp32 range is accepted.
+//
+// Workgroup = (query tile of 64 rows, sequence, head), 4 waves; wave w owns
+// query rows [16 w, +16).  Key tiles of 32 keys stream through two LDS
+// stages by LDS-DMA (rows at a pitch of d + 4 floats: 16 consecutive rows
+// then cover all 64 banks).  Per tile and wave:
+//   * S^T = K Q^T: K step j of dims 16 u .. 16 u + 15 takes dim 16 u + 4 g +
+//     j from lane group g (one 16-byte LDS read per lane feeds 4 MFMAs); Q
+//     is resident in registers in the same dim order;
+//   * online softmax per query column (exp2, scale folded in), P kept fp32;
+//   * O^T += V^T P^T: MFMA step r of a 16-key block takes key 4 g + r from
+//     lane group g, which is element r of that lane's own S^T accumulator,
+//     so P never moves; V^T[dim 16 t + c][key] is one fp32 LDS read.
+// ---------------------------------------------------------------------------
+template <int DQK, int DV>
+struct VaShape32 {
+  static constexpr int KT = 32;
+  static constexpr int PK = DQK / 4 + 1;  // row pitch in 16-B pieces (4 floats), one pad
+  static constexpr int PV = DV / 4 + 1;
+  static constexpr int RK = (KT * PK + kVaThreads - 1) / kVaThreads;  // DMA rounds
+  static constexpr int RV = (KT * PV + kVaThreads - 1) / kVaThreads;
+  static constexpr int KBYTES = RK * kVaThreads * 16;
+  static constexpr int VBYTES = RV * kVaThreads * 16;
+  static constexpr int STAGE = KBYTES + VBYTES;
+};
+
+__device__ __forceinline__ f32x4 mma32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int DQK, int DV>
+__global__ void __launch_bounds__(kVaThreads) varlen_attn_f32_kernel(VaArgs a) {
+  using Sh = VaShape32<DQK, DV>;
+  constexpr int KT = Sh::KT;
+  constexpr int NKB = KT / 16;
+  constexpr int QROWS = 16 * kVaWaves;
+  constexpr int NU = DQK / 16;  // 16-dim groups of the QK product
+  constexpr int NDT = DV / 16;  // O^T dim tiles
+  constexpr int PKF = 4 * Sh::PK, PVF = 4 * Sh::PV;  // row pitches in floats
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const float* qg = reinterpret_cast<const float*>(a.q);
+  const float* kg = reinterpret_cast<const float*>(a.k);
+  const float* vg = reinterpret_cast<const float*>(a.v);
+  float* og = reinterpret_cast<float*>(a.o);
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int seq = blockIdx.y, h = blockIdx.z;
+  const int qs = a.cu_q[seq], q_len = a.cu_q[seq + 1] - qs;
+  const int ks = a.cu_k[seq], k_len = a.cu_k[seq + 1] - ks;
+  const int tile = a.causal ? a.n_qtiles - 1 - (int)blockIdx.x : (int)blockIdx.x;
+  const int q0 = tile * QROWS;
+  if (q0 >= q_len) return;
+  const int offset = a.causal ? k_len - q_len : 0;
+  const int kend = a.causal ? max(0, min(k_len, q0 + QROWS + offset)) : k_len;
+  const int n_kt = (kend + KT - 1) / KT;
+
+  // ---- Q (B operand): row q0 + 16 w + c, dims 16 u + 4 g .. +3 ----
+  const int qi = q0 + 16 * w + c;
+  f32x4 qf[NU];
+  {
+    const float* qrow = qg + (int64_t)(qs + (qi < q_len ? qi : 0)) * a.q_st + (int64_t)h * a.q_sh +
+                        4 * g;
+#pragma unroll
+    for (int u = 0; u < NU; u++) qf[u] = *reinterpret_cast<const f32x4*>(qrow + 16 * u);
+  }
+
+  auto issue_tile = [&](int kt) {
+    unsigned char* st = smem_raw + (kt & 1) * Sh::STAGE;
+    const int k0 = kt * KT;
+#pragma unroll
+    for (int u = 0; u < Sh::RK; u++) {
+      const int qq = kVaThreads * u + 64 * w + lane;
+      const int r = qq / Sh::PK, ch = qq - r * Sh::PK;
+      const bool ok = r < KT && ch < DQK / 4 && k0 + r < kend;
+      const void* src = ok ? (const void*)(kg + (int64_t)(ks + k0 + r) * a.k_st +
+                                           (int64_t)h * a.k_sh + 4 * ch)
+                           : (const void*)kVaZero;
+      dma16(src, st + 16 * (kVaThreads * u + 64 * w));
+    }
+#pragma unroll
+    for (int u = 0; u < Sh::RV; u++) {
+      const int qq = kVaThreads * u + 64 * w + lane;
+      const int r = qq / Sh::PV, ch = qq - r * Sh::PV;
+      const bool ok = r < KT && ch < DV / 4 && k0 + r < kend;
+      const void* src = ok ? (const void*)(vg + (int64_t)(ks + k0 + r) * a.v_st +
+                                           (int64_t)h * a.v_sh + 4 * ch)
+                           : (const void*)kVaZero;
+      dma16(src, st + Sh::KBYTES + 16 * (kVaThreads * u + 64 * w));
+    }
+  };
+
+  f32x4 oacc[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; t++) oacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float m_run = -1e30f, l_part = 0.f;
+
+  if (n_kt > 0) issue_tile(0);
+#pragma unroll
+  for (int u = 0; u < NU; u++) asm volatile("" ::"v"(qf[u]));  // Q lands with tile 0
+  const int jmax_q = a.causal ? qi + offset + 1 : kend;  // keys < jmax of this column
+  for (int kt = 0; kt < n_kt; kt++) {
+    if (kt + 1 < n_kt) {
+      issue_tile(kt + 1);
+      va_wait<Sh::RK + Sh::RV>();
+    } else {
+      va_wait<0>();
+    }
+    lds_barrier();  // tile kt landed for every wave
+    const float* kst = reinterpret_cast<const float*>(smem_raw + (kt & 1) * Sh::STAGE);
+    const float* vst = reinterpret_cast<const float*>(smem_raw + (kt & 1) * Sh::STAGE + Sh::KBYTES);
+    const int k0 = kt * KT;
+
+    // ---- S^T blocks: keys 16 kb + 4 g + r, query column c ----
+    f32x4 sacc[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+      sacc[kb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      const float* krow = kst + (16 * kb + c) * PKF + 4 * g;
+#pragma unroll
+      for (int u = 0; u < NU; u++) {
+        const f32x4 kf = *reinterpret_cast<const f32x4*>(krow + 16 * u);
+#pragma unroll
+        for (int j = 0; j < 4; j++) sacc[kb] = mma32(kf[j], qf[u][j], sacc[kb]);
+      }
+    }
+
+    // ---- masks and online softmax of column c ----
+    const int jmax = min(kend, jmax_q);
+    float mt = -1e30f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        if (k0 + 16 * kb + 4 * g + r >= jmax) sacc[kb][r] = -INFINITY;
+        mt = fmaxf(mt, sacc[kb][r]);
+      }
+    mt = fmaxf(mt, shfl_xor_f(mt, 16));
+    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = exp2f((m_run - m_new) * a.scale_log2);
+    m_run = m_new;
+    const float mb = m_new * a.scale_log2;
+    float ls = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float sv = sacc[kb][r];
+        const float pr = (sv > -INFINITY) ? exp2f(__builtin_fmaf(sv, a.scale_log2, -mb)) : 0.f;
+        sacc[kb][r] = pr;
+        ls += pr;
+      }
+    l_part = l_part * alpha + ls;
+#pragma unroll
+    for (int t = 0; t < NDT; t++) oacc[t] *= alpha;
+
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float* vrow = vst + (16 * kb + 4 * g + r) * PVF + c;
+#pragma unroll
+        for (int t = 0; t < NDT; t++) oacc[t] = mma32(vrow[16 * t], sacc[kb][r], oacc[t]);
+      }
+    lds_barrier();  // every wave is done with this stage before it is refilled
+  }
+
+  // ---- outputs: O^T rows 4 g + r of tile t are dims 16 t + 4 g + r ----
+  float l = l_part;
+  l += shfl_xor_f(l, 16);
+  l += shfl_xor_f(l, 32);
+  if (qi >= q_len) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  float* orow = og + (int64_t)(qs + qi) * a.o_st + (int64_t)h * a.o_sh + 4 * g;
+#pragma unroll
+  for (int t = 0; t < NDT; t++) *reinterpret_cast<f32x4*>(orow + 16 * t) = oacc[t] * inv;
+  if (a.lse != nullptr && g == 0)
+    a.lse[(int64_t)h * a.total_q + qs + qi] = l > 0.f ? m_run * a.scale + logf(l) : -INFINITY;
+}
+
+template <int DQK, int DV>
+int launch_va32(const VaArgs& a0, int num_seqs, int max_q_len, hipStream_t st) {
+  using Sh = VaShape32<DQK, DV>;
+  constexpr int QROWS = 16 * kVaWaves;
+  auto kern = varlen_attn_f32_kernel<DQK, DV>;
+  const int rc = reserve_lds(reinterpret_cast<const void*>(kern), 2 * Sh::STAGE,
+                             "varlen_attention_f32");
+  if (rc) return rc;
+  VaArgs a = a0;
+  a.n_qtiles = (max_q_len + QROWS - 1) / QROWS;
+  if (a.n_qtiles == 0) return MI355_DSA_OK;
+  kern<<<dim3(a.n_qtiles, num_seqs, a.H), kVaThreads, 2 * Sh::STAGE, st>>>(a);
+  return check_launch("varlen_attention_f32");
+}
+
+int dispatch_va32(const VaArgs& a, int d_qk, int d_v, int num_seqs, int max_q_len,
+                  hipStream_t st) {
+  if (d_qk == 192 && d_v == 128) return launch_va32<192, 128>(a, num_seqs, max_q_len, st);
+  if (d_qk == 128 && d_v == 128) return launch_va32<128, 128>(a, num_seqs, max_q_len, st);
+  if (d_qk == 64 && d_v == 64) return launch_va32<64, 64>(a, num_seqs, max_q_len, st);
+  if (d_qk == 256 && d_v == 256) return launch_va32<256, 256>(a, num_seqs, max_q_len, st);
+  return set_error(MI355_DSA_EINVAL,
+                   "varlen_attention: head dims (%d, %d) not built; supported (qk, v): "
+                   "(192, 128), (128, 128), (64, 64), (256, 256)", d_qk, d_v);
+}
+
 }  // namespace
 }  // namespace mi355dsa
 
 using namespace mi355dsa;
 
 extern "C" int mi355_dsa_varlen_attention(
-    void* out, float* lse, const void* q, const void* k, const void* v, int bf16, int num_seqs,
+    void* out, float* lse, const void* q, const void* k, const void* v, int dtype, int num_seqs,
     int n_head, int d_qk, int d_v, int64_t q_tok_stride, int64_t q_head_stride,
     int64_t k_tok_stride, int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,
     int64_t o_tok_stride, int64_t o_head_stride, const int32_t* cu_seqlens_q,
@@ -347,13 +559,17 @@ extern "C" int mi355_dsa_varlen_attention(
   DSA_CHECK(num_seqs >= 0 && n_head > 0 && max_q_len >= 0 && total_q >= 0, "varlen_attention: bad sizes");
   if (num_seqs == 0 || max_q_len == 0 || total_q == 0) return MI355_DSA_OK;
   DSA_CHECK(out && q && k && v && cu_seqlens_q && cu_seqlens_k, "varlen_attention: null pointer argument");
+  DSA_CHECK(dtype >= 0 && dtype <= 2, "varlen_attention: dtype must be 0 (fp16), 1 (bf16) or 2 (fp32)");
   DSA_CHECK(num_seqs <= 65535 && n_head <= 65535, "varlen_attention: too many sequences or heads");
-  DSA_CHECK(aligned_to(q, 16) && aligned_to(k, 16) && aligned_to(v, 16) && aligned_to(out, 8),
-            "varlen_attention: q / k / v must be 16-byte and out 8-byte aligned");
-  DSA_CHECK(q_tok_stride % 8 == 0 && q_head_stride % 8 == 0 && k_tok_stride % 8 == 0 &&
-                k_head_stride % 8 == 0 && v_tok_stride % 8 == 0 && v_head_stride % 8 == 0 &&
+  const bool f32 = dtype == 2;
+  DSA_CHECK(aligned_to(q, 16) && aligned_to(k, 16) && aligned_to(v, 16) &&
+                aligned_to(out, f32 ? 16 : 8),
+            "varlen_attention: q / k / v must be 16-byte and out %d-byte aligned", f32 ? 16 : 8);
+  const int64_t sm = f32 ? 4 : 8;  // elements per 16-byte piece
+  DSA_CHECK(q_tok_stride % sm == 0 && q_head_stride % sm == 0 && k_tok_stride % sm == 0 &&
+                k_head_stride % sm == 0 && v_tok_stride % sm == 0 && v_head_stride % sm == 0 &&
                 o_tok_stride % 4 == 0 && o_head_stride % 4 == 0,
-            "varlen_attention: strides must be multiples of 8 elements (out: 4)");
+            "varlen_attention: strides must be multiples of %d elements (out: 4)", (int)sm);
   VaArgs a{};
   a.q = reinterpret_cast<const uint16_t*>(q);
   a.k = reinterpret_cast<const uint16_t*>(k);
@@ -376,6 +592,7 @@ extern "C" int mi355_dsa_varlen_attention(
   a.scale = softmax_scale;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   hipStream_t st = as_stream(stream);
-  return bf16 ? dispatch_va<true>(a, d_qk, d_v, num_seqs, max_q_len, st)
-              : dispatch_va<false>(a, d_qk, d_v, num_seqs, max_q_len, st);
+  if (f32) return dispatch_va32(a, d_qk, d_v, num_seqs, max_q_len, st);
+  return dtype == 1 ? dispatch_va<true>(a, d_qk, d_v, num_seqs, max_q_len, st)
+                    : dispatch_va<false>(a, d_qk, d_v, num_seqs, max_q_len, st);
 }

@@ -13,13 +13,9 @@ entry points, `run_prefill_new_tokens` (:229-244) and
 The reference computes in fp32 from fp16/bf16 inputs; the kernel multiplies
 fp16 (bf16) inputs exactly into fp32 accumulators and rounds P to fp16 (bf16
 P is kept as a hi + lo pair) for the PV product.  The reference backend also
-lists fp32 (sm70_triton.py:193), where it computes in fp32 throughout.  This
-build takes fp32 inputs by rounding q, k and v to fp16 (one conversion pass
-each) and running the fp16 kernel; the output is returned in fp32 and the LSE
-is fp32 as for the other dtypes.  The results differ from fp32 arithmetic by
-that rounding (2^-11 relative per input element, so |x| must stay below
-fp16's 65504; larger values become inf and show in the output); the GPU test
-bounds the difference against the fp64 oracle.
+lists fp32 (sm70_triton.py:193), where it computes in fp32 throughout; fp32
+inputs here run a kernel of their own on the fp32 MFMA, in fp32 arithmetic
+end to end (P included) over the whole fp32 range, with an fp32 output.
 """
 from __future__ import annotations
 
@@ -27,6 +23,10 @@ import torch
 
 from . import _lib
 from .ops import _check, _stream
+
+
+# the C ABI's dtype argument
+_DTYPE_CODE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
 
 def _cu(t: torch.Tensor, dev) -> torch.Tensor:
@@ -40,19 +40,10 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """q [total_q, H, Dq], k [total_k, H, Dq], v [total_k, H, Dv] (fp16, bf16
     or fp32, last dim contiguous); cu_seqlens_* int [num_seqs + 1].  Returns
     out [total_q, H, Dv] (q.dtype) and, if asked, lse [H, total_q] fp32.
-    fp32 inputs are rounded to fp16 for the kernel (see the module note).
     max_seqlen_q saves the host read of the longest query run."""
     _check(q.is_cuda and k.is_cuda and v.is_cuda, "q, k and v must be on the GPU")
-    _check(q.dtype in (torch.float16, torch.bfloat16, torch.float32),
-           "varlen_attention: fp16, bf16 or fp32 inputs")
+    _check(q.dtype in _DTYPE_CODE, "varlen_attention: fp16, bf16 or fp32 inputs")
     _check(k.dtype == q.dtype and v.dtype == q.dtype, "q, k and v must share one dtype")
-    if q.dtype == torch.float32:
-        res = varlen_attention(q.to(torch.float16), k.to(torch.float16), v.to(torch.float16),
-                               cu_seqlens_q, cu_seqlens_k, softmax_scale, causal,
-                               return_softmax_lse, max_seqlen_q)
-        if return_softmax_lse:
-            return res[0].to(torch.float32), res[1]
-        return res.to(torch.float32)
     _check(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "q, k, v must be [tokens, heads, dim]")
     total_q, H, d_qk = q.shape
     total_k = k.shape[0]
@@ -67,8 +58,10 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     lse = (torch.empty(H, total_q, dtype=torch.float32, device=q.device)
            if return_softmax_lse else None)
     if num_seqs > 0 and total_q > 0:
+        per16 = 16 // q.element_size()  # elements per 16-byte piece
+
         def rows(x):
-            ok = x.stride(2) == 1 and x.stride(0) % 8 == 0 and x.stride(1) % 8 == 0 \
+            ok = x.stride(2) == 1 and x.stride(0) % per16 == 0 and x.stride(1) % per16 == 0 \
                 and x.data_ptr() % 16 == 0
             return x if ok else x.contiguous()
         q, k, v = rows(q), rows(k), rows(v)
@@ -78,7 +71,7 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         with torch.cuda.device(q.device):
             _lib.call("mi355_dsa_varlen_attention", out.data_ptr(),
                       lse.data_ptr() if lse is not None else None,
-                      q.data_ptr(), k.data_ptr(), v.data_ptr(), int(q.dtype == torch.bfloat16),
+                      q.data_ptr(), k.data_ptr(), v.data_ptr(), _DTYPE_CODE[q.dtype],
                       num_seqs, H, d_qk, d_v, q.stride(0), q.stride(1), k.stride(0), k.stride(1),
                       v.stride(0), v.stride(1), out.stride(0), out.stride(1), cq.data_ptr(),
                       ck.data_ptr(), max_seqlen_q, total_q, float(softmax_scale), int(causal),

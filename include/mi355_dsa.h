@@ -138,15 +138,17 @@ int mi355_dsa_indexer_shard_merge(int32_t* out, int64_t out_stride, int64_t out_
  * device arrays of num_seqs + 1).  causal != 0: query i (0-based in its
  * sequence of q_len) sees keys j <= i + k_len - q_len.  lse (nullable) is
  * fp32 [n_head, total_q], natural log; a query with no key gets out = 0 and
- * lse = -inf.  q/k/v/out are fp16 (bf16 = 0) or bf16 (bf16 = 1) with unit
- * last-dim stride and the given element strides (multiples of 8; out: 4),
- * q/k/v 16-byte aligned.  (d_qk, d_v) in {(192,128), (128,128), (64,64),
+ * lse = -inf.  q/k/v/out are fp16 (dtype = 0), bf16 (dtype = 1) or fp32
+ * (dtype = 2, computed in fp32 arithmetic on the fp32 MFMA) with unit
+ * last-dim stride and the given element strides (multiples of one 16-byte
+ * piece: 8 elements, 4 for fp32; out: 4), q/k/v 16-byte aligned, out 8-byte
+ * (fp32: 16-byte) aligned.  (d_qk, d_v) in {(192,128), (128,128), (64,64),
  * (256,256)}.  max_q_len = the longest query run.
  * Replaces the reference's dense MLA prefill attention, _varlen_attention
  * (vllm/v1/attention/backends/mla/prefill/sm70_triton.py:54-187).
  */
 int mi355_dsa_varlen_attention(void* out, float* lse, const void* q, const void* k,
-                               const void* v, int bf16, int num_seqs, int n_head, int d_qk,
+                               const void* v, int dtype, int num_seqs, int n_head, int d_qk,
                                int d_v, int64_t q_tok_stride, int64_t q_head_stride,
                                int64_t k_tok_stride, int64_t k_head_stride,
                                int64_t v_tok_stride, int64_t v_head_stride,

@@ -110,18 +110,10 @@ def test_equal_scores_closed_form(pkg, dev):
         torch.testing.assert_close(out[t], v[ks:ks + n].float().mean(0), rtol=2e-3, atol=1e-3)
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"c{c[0]}" for c in CASES])
-def test_varlen_attention_fp32_inputs(pkg, dev, case):
-    """fp32 q, k, v (the reference backend's third dtype, sm70_triton.py:193)
-    are rounded to fp16 for the kernel and the output comes back in fp32.
-    Against the fp64 oracle of the unrounded fp32 inputs the input rounding
-    alone moves lse by up to 1e-3 and o by up to 1.05x the fp16 bar on these
-    cases (computed on the CPU), so the bars are twice the fp16 ones:
-    o 4e-3 relative / 2e-3 absolute, lse 2e-3."""
-    seed, cu_q, cu_k, H, dqk, dv, causal = case
-    cu_k = cu_k or cu_q
-    q, k, v = make(seed, cu_q, cu_k, H, dqk, dv, torch.float32)
-    scale = dqk ** -0.5
+F32_RTOL, F32_ATOL, F32_LSE = 2e-5, 2e-5, 2e-5
+
+
+def run32(pkg, dev, q, k, v, cu_q, cu_k, scale, causal):
     cq = torch.tensor(cu_q, dtype=torch.int32, device=dev)
     ck = torch.tensor(cu_k, dtype=torch.int32, device=dev)
     out, lse = pkg.mla_prefill.varlen_attention(q.to(dev), k.to(dev), v.to(dev), cq, ck, scale,
@@ -130,10 +122,47 @@ def test_varlen_attention_fp32_inputs(pkg, dev, case):
     out2 = pkg.mla_prefill.varlen_attention(q.to(dev), k.to(dev), v.to(dev), cq, ck, scale,
                                             causal, False)
     assert torch.equal(out, out2)
-    ro, rl = O.varlen_attention(q, k, v, cu_q, cu_k, scale, causal)
-    lse, out = lse.cpu(), out.cpu()
+    return out.cpu(), lse.cpu()
+
+
+def check32(out, lse, ro, rl, scale_o=1.0):
+    """fp32-grade bars: o within 2e-5 relative / 2e-5 x the output scale
+    absolute, lse within 2e-5 (the north-star bars are 2e-3 / 1e-3 / 1e-4)."""
     assert torch.equal(torch.isinf(lse), torch.isinf(rl))
     fin = torch.isfinite(rl)
     if fin.any():
-        assert (lse[fin].double() - rl[fin]).abs().max().item() <= 2e-3
-    torch.testing.assert_close(out.double(), ro, rtol=4e-3, atol=2e-3)
+        assert (lse[fin].double() - rl[fin]).abs().max().item() <= F32_LSE
+    torch.testing.assert_close(out.double(), ro, rtol=F32_RTOL, atol=F32_ATOL * scale_o)
+
+
+def f32_case(case):
+    seed, cu_q, cu_k, H, dqk, dv, causal = case
+    cu_k = cu_k or cu_q
+    q, k, v = make(seed, cu_q, cu_k, H, dqk, dv, torch.float32)
+    return q, k, v, cu_q, cu_k, dqk ** -0.5, causal
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"c{c[0]}" for c in CASES])
+def test_varlen_attention_fp32_inputs(pkg, dev, case):
+    """fp32 q, k, v (the reference backend's third dtype, sm70_triton.py:193,
+    computed there in fp32) run the fp32-MFMA kernel: the fp64 oracle of the
+    same inputs is met to fp32 precision."""
+    q, k, v, cu_q, cu_k, scale, causal = f32_case(case)
+    out, lse = run32(pkg, dev, q, k, v, cu_q, cu_k, scale, causal)
+    ro, rl = O.varlen_attention(q, k, v, cu_q, cu_k, scale, causal)
+    check32(out, lse, ro, rl)
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[3], CASES[7]], ids=["c0", "c3", "c7"])
+def test_varlen_attention_fp32_beyond_fp16_range(pkg, dev, case):
+    """Inputs far outside fp16's range: q scaled by 2^17 (entries up to
+    ~6e5 > 65504) and k by 2^-17, so the scores are unchanged, and v by 1e6.
+    The fp32 kernel keeps the oracle's results to fp32 precision; rounding
+    the inputs to fp16 would turn q and v into inf."""
+    q, k, v, cu_q, cu_k, scale, causal = f32_case(case)
+    q, k, v = q * 2.0 ** 17, k * 2.0 ** -17, v * 1e6
+    assert q.abs().max() > 65504 and v.abs().max() > 65504
+    out, lse = run32(pkg, dev, q, k, v, cu_q, cu_k, scale, causal)
+    ro, rl = O.varlen_attention(q, k, v, cu_q, cu_k, scale, causal)
+    assert torch.isfinite(out).all()
+    check32(out, lse, ro, rl, scale_o=1e6)

@@ -65,3 +65,21 @@ def test_single_key_and_empty_keys():
     assert torch.allclose(out[0], v[0])
     assert torch.allclose(lse[:, 0], 0.25 * (q[0] * k[0]).sum(-1))
     assert torch.all(out[1] == 0) and torch.all(torch.isinf(lse[:, 1])) and torch.all(lse[:, 1] < 0)
+
+
+def test_fp32_bars_see_fp16_input_rounding():
+    """The fp32 GPU tests' bars (2e-5) reject a path that rounds fp32 inputs
+    to fp16: on the first varlen case that rounding alone moves o or lse by
+    far more than 2e-5."""
+    g = torch.Generator().manual_seed(0)
+    cu = [0, 1, 18, 148, 448]
+    q = torch.randn(448, 8, 192, generator=g)
+    k = torch.randn(448, 8, 192, generator=g)
+    v = torch.randn(448, 8, 128, generator=g)
+    ro, rl = O.varlen_attention(q, k, v, cu, cu, 192 ** -0.5, True)
+    h = lambda x: x.to(torch.float16).to(torch.float32)
+    ho, hl = O.varlen_attention(h(q), h(k), h(v), cu, cu, 192 ** -0.5, True)
+    fin = torch.isfinite(rl)
+    err_o = ((ho - ro).abs() - 2e-5 * ro.abs()).max().item()
+    err_l = (hl[fin] - rl[fin]).abs().max().item()
+    assert err_o > 10 * 2e-5 and err_l > 10 * 2e-5
