@@ -965,8 +965,20 @@ __device__ __forceinline__ void pf_dma_tile(const uint8_t* __restrict__ kv, cons
 // Y = {softmax of tile i+1, LDS-DMA of tile i+3, wait for tile i+2}.
 // ---------------------------------------------------------------------------
 constexpr int kP3Ring = 3;
-constexpr int kP3SPitch = 36;  // floats per (dim quarter, head) row of S partials
-constexpr int kP3PPitch = 40;  // halves per (scale tile, head) row of P
+// S partials and the P table: one unpadded row of 32 keys per head, the key
+// chunks (4 floats of S, 8 halves of P) permuted by an XOR with bits of the
+// head.  Measured with SQ_LDS_BANK_CONFLICT on gfx950, these orders make the
+// QK stores of S (16 heads x 4 chunks per instruction), the softmax reads of
+// S and stores of P, and the PV reads of P conflict-free; the padded rows
+// they replace (36 floats, 40 halves) cost two cycles per access.
+constexpr int kP3SPitch = 32;  // floats per (dim part, head) row of S partials
+constexpr int kP3PPitch = 32;  // halves per (scale tile, head) row of P
+__device__ __forceinline__ int sp_at(int head, int key) {  // key % 4 == 0
+  return head * kP3SPitch + ((((key >> 2) ^ head) & 7) << 2);
+}
+__device__ __forceinline__ int pt_at(int head, int key) {  // key % 4 == 0
+  return head * kP3PPitch + ((((key >> 3) ^ (2 * ((head >> 3) & 1))) & 3) << 3) + (key & 4);
+}
 
 struct P3Smem {
   uint8_t ring[kP3Ring][kPfSlotBytes];
@@ -1084,16 +1096,16 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
       f32x4 v;
 #pragma unroll
       for (int r = 0; r < 4; r++) v[r] = accr[hg][r] + ksc[r] * accn[hg][r];
-      *reinterpret_cast<f32x4*>(&sh.sp[qd][(16 * hg + c) * kP3SPitch + 16 * kb + 4 * g]) = v;
+      *reinterpret_cast<f32x4*>(&sh.sp[qd][sp_at(16 * hg + c, 16 * kb + 4 * g)]) = v;
     }
   };
 
   // softmax of the tile in slot cb (rows trows) from sh.sp -> sh.pt, alpha
   auto softmax = [&](const uint8_t* cb, const int32_t* trows, int* flag) {
-    f32x4 s4 = *reinterpret_cast<const f32x4*>(&sh.sp[0][sm_h * kP3SPitch + 4 * sm_k]);
+    f32x4 s4 = *reinterpret_cast<const f32x4*>(&sh.sp[0][sp_at(sm_h, 4 * sm_k)]);
 #pragma unroll
     for (int q = 1; q < 4; q++)
-      s4 += *reinterpret_cast<const f32x4*>(&sh.sp[q][sm_h * kP3SPitch + 4 * sm_k]);
+      s4 += *reinterpret_cast<const f32x4*>(&sh.sp[q][sp_at(sm_h, 4 * sm_k)]);
     const int4 vr = *reinterpret_cast<const int4*>(trows + 4 * sm_k);
     f32x4 ks[4];
 #pragma unroll
@@ -1129,7 +1141,7 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
       f16x4 ph;
 #pragma unroll
       for (int r = 0; r < 4; r++) ph[r] = (f16)(pr[r] * ks[r][st]);
-      *reinterpret_cast<f16x4*>(&sh.pt[st][sm_h * kP3PPitch + 4 * sm_k]) = ph;
+      *reinterpret_cast<f16x4*>(&sh.pt[st][pt_at(sm_h, 4 * sm_k)]) = ph;
     }
   };
 
@@ -1145,7 +1157,7 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
     f16x8 pb[4];
 #pragma unroll
     for (int hg = 0; hg < 4; hg++)
-      pb[hg] = *reinterpret_cast<const f16x8*>(&sh.pt[st_pv][(16 * hg + c) * kP3PPitch + 8 * g]);
+      pb[hg] = *reinterpret_cast<const f16x8*>(&sh.pt[st_pv][pt_at(16 * hg + c, 8 * g)]);
     // transpose source: lane i of a 16-lane group points at key 8g + i/2,
     // bytes 64 w + 16 t + 8 (i % 2); lane j receives keys 8g .. 8g+7 at
     // dim 64 w + 16 t + j
@@ -1273,7 +1285,7 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
 // decode (idx == nullptr) split over the context.
 //
 // Workgroup = (token, 64 heads, split), 8 waves; tiles of raw 1152-byte rows
-// stream through a 3-slot LDS ring by LDS-DMA, each row at a 1168-byte pitch
+// stream through a 3-slot LDS ring by LDS-DMA, each row at a 1184-byte pitch
 // (72 pieces + one zero pad, so the 16 rows of an MFMA operand spread over
 // the banks as the fp8 rows do).
 //   * QK: wave w = (key block kb = w & 1, dim half dh = (w >> 1) & 1, head
@@ -1291,9 +1303,12 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
 // top-k list, or positions [0, seq_len) in dense mode) and, with more than
 // one split, writes its normalised partial for the merge kernel.
 // ---------------------------------------------------------------------------
-constexpr int kHfPitchPieces = kLatentDim / 8 + 1;                       // 73
-constexpr int kHfRowPitch = kHfPitchPieces * 16;                         // 1168 B
-constexpr int kHfPieces = kPfTileKeys * kHfPitchPieces;                  // 2336
+// Row pitch 74 pieces (two zero pads): with it the QK reads of 16 rows x 4
+// adjacent pieces are free of LDS bank conflicts (measured; 73 pieces, a
+// 1168-byte pitch, conflicted two-way).
+constexpr int kHfPitchPieces = kLatentDim / 8 + 2;                       // 74
+constexpr int kHfRowPitch = kHfPitchPieces * 16;                         // 1184 B
+constexpr int kHfPieces = kPfTileKeys * kHfPitchPieces;                  // 2368
 constexpr int kHfRounds = (kHfPieces + kPfThreads - 1) / kPfThreads;     // 5
 constexpr int kHfSlotBytes = kHfRounds * kPfThreads * 16;                // 40960
 constexpr int kHfSegKeys = 1024;
@@ -1398,13 +1413,13 @@ __global__ void __launch_bounds__(kPfThreads) mla_attn_f16_kernel(MlaParams p) {
     }
 #pragma unroll
     for (int hg = 0; hg < 2; hg++)
-      *reinterpret_cast<f32x4*>(&sh.sp[dh][(32 * hh + 16 * hg + c) * kP3SPitch + 16 * kb + 4 * g]) =
+      *reinterpret_cast<f32x4*>(&sh.sp[dh][sp_at(32 * hh + 16 * hg + c, 16 * kb + 4 * g)]) =
           acc[hg];
   };
 
   auto softmax = [&](const int32_t* trows, int* flag) {
-    f32x4 s4 = *reinterpret_cast<const f32x4*>(&sh.sp[0][sm_h * kP3SPitch + 4 * sm_k]);
-    s4 += *reinterpret_cast<const f32x4*>(&sh.sp[1][sm_h * kP3SPitch + 4 * sm_k]);
+    f32x4 s4 = *reinterpret_cast<const f32x4*>(&sh.sp[0][sp_at(sm_h, 4 * sm_k)]);
+    s4 += *reinterpret_cast<const f32x4*>(&sh.sp[1][sp_at(sm_h, 4 * sm_k)]);
     const int4 vr = *reinterpret_cast<const int4*>(trows + 4 * sm_k);
     const int vv[4] = {vr.x, vr.y, vr.z, vr.w};
     float mt = -1e30f;
@@ -1432,7 +1447,7 @@ __global__ void __launch_bounds__(kPfThreads) mla_attn_f16_kernel(MlaParams p) {
       ph[r] = (f16)pr;
     }
     l_run += sum8(ls);
-    *reinterpret_cast<f16x4*>(&sh.pt[sm_h * kP3PPitch + 4 * sm_k]) = ph;
+    *reinterpret_cast<f16x4*>(&sh.pt[pt_at(sm_h, 4 * sm_k)]) = ph;
   };
 
   auto pv = [&](const uint8_t* cb, bool rescale) {
@@ -1446,7 +1461,7 @@ __global__ void __launch_bounds__(kPfThreads) mla_attn_f16_kernel(MlaParams p) {
     f16x8 pb[4];
 #pragma unroll
     for (int hg = 0; hg < 4; hg++)
-      pb[hg] = *reinterpret_cast<const f16x8*>(&sh.pt[(16 * hg + c) * kP3PPitch + 8 * g]);
+      pb[hg] = *reinterpret_cast<const f16x8*>(&sh.pt[pt_at(16 * hg + c, 8 * g)]);
     // transpose reads: lane i of group g supplies key 8 g + i / 4 (+4 for the
     // second read), dims 64 w + 16 t + 4 (i % 4) .. +3; lane j receives keys
     // 8 g .. 8 g + 3 (then + 4 .. + 7) at dim 64 w + 16 t + j
