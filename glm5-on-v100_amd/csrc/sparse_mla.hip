@@ -1286,8 +1286,8 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
 //
 // Workgroup = (token, 64 heads, split), 8 waves; tiles of raw 1152-byte rows
 // stream through a 3-slot LDS ring by LDS-DMA, each row at a 1184-byte pitch
-// (72 pieces + one zero pad, so the 16 rows of an MFMA operand spread over
-// the banks as the fp8 rows do).
+// (72 pieces + two zero pads, so that the QK operand reads of 16 rows are
+// free of bank conflicts).
 //   * QK: wave w = (key block kb = w & 1, dim half dh = (w >> 1) & 1, head
 //     half hh = w >> 2) computes S^T for keys [16 kb, +16) x heads
 //     [32 hh, +32) over dims [288 dh, +288), Q of its 32 heads for those dims
