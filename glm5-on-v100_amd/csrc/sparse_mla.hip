@@ -604,7 +604,13 @@ constexpr int kDecWaveRounds = (kDecWavePieces + 63) / 64;               // 11 L
 constexpr int kDecWaveBytes = kDecWaveKeys * kDsmlaRowBytes;            // 10496 B
 constexpr int kQPitchPieces = kLatentDim / 8 + 1;                        // 73 x 16 B: padded Q row
 constexpr int kQRounds = (16 * kQPitchPieces + kDmaThreads - 1) / kDmaThreads;  // 3
-constexpr int kPPitch = kDmaSplitKeys + 4;                               // fp32 P row pitch (floats)
+constexpr int kPPitch = kDmaSplitKeys;                                   // fp32 P row pitch (floats)
+// P[head c][key] at row c, 4-key chunk (key / 4) XOR c: the stores (16 heads x
+// 4 chunks per instruction) and the PV reads are then free of LDS bank
+// conflicts (measured; a padded 132-float row conflicted two-way on both)
+__device__ __forceinline__ int dpt_at(int c, int key) {  // key % 4 == 0
+  return c * kPPitch + ((((key >> 2) ^ c) & (kDmaSplitKeys / 4 - 1)) << 2);
+}
 constexpr int kDimsPerWave = kValueDim / kDmaWaves;                      // 64
 constexpr int kTilesPerWave = kDimsPerWave / 16;                         // 4
 
@@ -810,7 +816,7 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
     sh.l[w * 16 + c] = ls;
   }
   // P[head c][key]: keys 16w + 4g + r
-  *reinterpret_cast<f32x4*>(&sh.pt[c * kPPitch + kDecWaveKeys * w + 4 * g]) = pr;
+  *reinterpret_cast<f32x4*>(&sh.pt[dpt_at(c, kDecWaveKeys * w + 4 * g)]) = pr;
   lds_barrier();
   float M = -1e30f;
 #pragma unroll
@@ -831,8 +837,8 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
     const uint8_t* cb = sh.rows[src_w] + 8 * (g & 1) * kDsmlaRowBytes;
     // P^T operand: keys 32kb + 8g + e of head c, times the key's scale of
     // tile st and the source wave's rescale factor
-    const f32x4 pa = *reinterpret_cast<const f32x4*>(&sh.pt[c * kPPitch + 32 * kb + 8 * g]);
-    const f32x4 pc = *reinterpret_cast<const f32x4*>(&sh.pt[c * kPPitch + 32 * kb + 8 * g + 4]);
+    const f32x4 pa = *reinterpret_cast<const f32x4*>(&sh.pt[dpt_at(c, 32 * kb + 8 * g)]);
+    const f32x4 pc = *reinterpret_cast<const f32x4*>(&sh.pt[dpt_at(c, 32 * kb + 8 * g + 4)]);
     const float alpha = __expf(sh.m[src_w * 16 + c] - M);  // the source wave's rescale factor
     float ks[8];
 #pragma unroll
