@@ -12,7 +12,7 @@
 //
 // Workgroup = (query tile of 64 QB rows, sequence, head), 4 waves; wave w
 // owns query rows [16 QB w, +16 QB).  Key tiles of KT keys stream through
-// two LDS stages by LDS-DMA (K and V rows at padded pitches, so the 16 rows
+// two LDS stages by LDS-DMA (K and V rows at padded pitches, so that the rows
 // of an MFMA operand spread over the banks), the next tile in flight while
 // the current one is used; two workgroups share a CU.  Per tile and wave:
 //   * S^T = K Q^T (v_mfma_f32_16x16x32): keys are the A operand read from
@@ -78,10 +78,14 @@ __device__ __forceinline__ float from16(uint16_t x) {
   else return (float)__builtin_bit_cast(f16, x);
 }
 
+// K and V rows at a pitch of d / 8 + 2 pieces (two pads): the QK reads (16
+// rows x 4 adjacent pieces per instruction) and the V^T transpose reads (8
+// rows x 32 bytes per half-wave) are then free of LDS bank conflicts (both
+// measured on gfx950; with one pad both conflicted two-way)
 template <int DQK, int DV, int KT>
 struct VaShape {
-  static constexpr int PK = DQK / 8 + 1;  // K row pitch in 16-B pieces (one pad)
-  static constexpr int PV = DV / 8 + 1;
+  static constexpr int PK = DQK / 8 + 2;  // K row pitch in 16-B pieces
+  static constexpr int PV = DV / 8 + 2;
   static constexpr int RK = (KT * PK + kVaThreads - 1) / kVaThreads;  // DMA rounds
   static constexpr int RV = (KT * PV + kVaThreads - 1) / kVaThreads;
   static constexpr int KBYTES = RK * kVaThreads * 16;
