@@ -81,6 +81,8 @@ def parse():
     p.add_argument("--layers", type=int, default=78)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="only the headline decode")
+    p.add_argument("--no-kernel-times", action="store_true",
+                   help="skip the per-kernel device times (torch.profiler) of the headline")
     p.add_argument("--extra", default="all",
                    help="comma list of extra records: sweep, indexer_prefill, sparse_prefill, "
                         "indexer_decode, gemv, k_store (default all)")
@@ -129,9 +131,36 @@ def cache_copies(cache_bytes, layers, pool_bytes=3 << 30):
     return max(1, min(layers, max(8, -(-pool_bytes // cache_bytes))))
 
 
-def bench_decode(torch, pkg, dev, ctx, layers, steps, warmup, seed=3):
+def kernel_times(torch, graph, replays=2):
+    """Average device duration (us) of each kernel of `graph` over `replays`
+    replays, from torch.profiler's device timestamps; {} if the profiler is
+    unavailable here (e.g. under another tracer)."""
+    try:
+        from torch.profiler import profile, ProfilerActivity
+        with profile(activities=[ProfilerActivity.CUDA]) as prof:
+            for _ in range(replays):
+                graph.replay()
+            torch.cuda.synchronize()
+        agg = {}
+        for e in prof.events():
+            if e.device_type != torch.autograd.DeviceType.CUDA:
+                continue
+            name = e.name.split("(")[0].replace("mi355dsa::", "")
+            for k in ("sparse_mla_decode_dma_kernel", "sparse_mla_merge_kernel"):
+                if k in name:
+                    name = k
+            agg.setdefault(name, []).append(e.device_time_total)
+        return {k: (sum(v) / len(v), len(v)) for k, v in agg.items()}
+    except Exception as exc:  # profiler absent or refused: report nothing
+        log(f"kernel times unavailable: {exc}")
+        return {}
+
+
+def bench_decode(torch, pkg, dev, ctx, layers, steps, warmup, seed=3, per_kernel=False):
     """C3 decode: `layers` layers with their own q and idx, layer l reading
-    cache copy l % n (cache_copies), replayed from one HIP graph."""
+    cache copy l % n (cache_copies), replayed from one HIP graph.  With
+    per_kernel, d["kernel_us"] holds each kernel's average device time over
+    two more replays of the same graph."""
     S = pkg.synthetic
     ops = pkg._sm70_ops
     d = S.decode_inputs(B=4, H=64, ctx=ctx, topk=2048, fp8=True, device=dev, seed=seed)
@@ -154,6 +183,8 @@ def bench_decode(torch, pkg, dev, ctx, layers, steps, warmup, seed=3):
     graph = capture(torch, run)
     ms = time_graph(torch, graph, steps, warmup)
     assert all(torch.isfinite(o).all() for o in outs[:2])
+    if per_kernel:
+        d["kernel_us"] = kernel_times(torch, graph)
     del graph, kvs[1:]
     return ms, d, idxs, qs
 
@@ -964,7 +995,8 @@ def main():
     # ---- headline: C3 decode at 180k ----
     L = args.layers
     torch.cuda.synchronize()
-    ms, d, idxs, qs = bench_decode(torch, pkg, dev, 184320, L, args.steps, args.warmup)
+    ms, d, idxs, qs = bench_decode(torch, pkg, dev, 184320, L, args.steps, args.warmup,
+                                   per_kernel=not args.no_kernel_times)
     ms_per_step = ms / args.steps
     us_layer = ms_per_step * 1000.0 / L
     gbps = DECODE_BYTES / (us_layer * 1e-6) / 1e9
@@ -1012,6 +1044,24 @@ def main():
             "bytes_per_launch": DECODE_BYTES,
         },
     }
+    # the dominant kernel alone: the layer's algorithmic bytes over the split
+    # decode kernel's own device time (torch.profiler timestamps of two more
+    # replays of the timed graph), beside the whole-layer figure above
+    kt = d.get("kernel_us", {})
+    if "sparse_mla_decode_dma_kernel" in kt:
+        us_k, n_k = kt["sparse_mla_decode_dma_kernel"]
+        gb_k = DECODE_BYTES / (us_k * 1e-6) / 1e9
+        line["roofline"]["dominant_kernel"] = {
+            "name": "sparse_mla_decode_dma_kernel",
+            "avg_us": round(us_k, 3),
+            "launches": n_k,
+            "achieved": round(gb_k, 1),
+            "frac": round(gb_k / HBM_PEAK_GBPS, 4),
+            "source": "torch.profiler device timestamps, 2 replays of the timed graph",
+        }
+        if "sparse_mla_merge_kernel" in kt:
+            line["roofline"]["merge_kernel_avg_us"] = round(kt["sparse_mla_merge_kernel"][0], 3)
+        log(f"decode kernels: {kt}")
 
     extras = set(EXTRAS if args.extra == "all" else args.extra.split(","))
     if args.no_extra:
