@@ -470,6 +470,29 @@ __global__ void __launch_bounds__(kPkhWaves * 64, 2) indexer_logits_packed_h_ker
   pk_tile<KFP8, 2, kPkhWaves>(a, sh, q_base, (id % a.n_kt) * kPkKT);
 }
 
+// Launches of more than one round of four-wave workgroups whose last round
+// holds at most half a round (R = workgroups mod 512, 0 < R <= 256): the
+// first n_full workgroups are four-wave 32-query workgroups as in
+// indexer_logits_packed_h_kernel, and the last R of them run as 2R quarter
+// tiles (16 queries each, at most one round), so that the last round takes
+// a quarter tile's time instead of a 32-query workgroup's.
+template <bool KFP8>
+__global__ void __launch_bounds__(kPkhWaves * 64, 2) indexer_logits_packed_hq_kernel(PkArgs a) {
+  __shared__ PkSmemH sh;
+  const int id = blockIdx.x;
+  if (id < a.n_full) {
+    const int q_base = (id / a.n_kt) * kPkhQT;
+    if (q_base >= a.B) return;
+    pk_tile<KFP8, 2, kPkhWaves>(a, sh, q_base, (id % a.n_kt) * kPkKT);
+  } else {
+    const int j = id - a.n_full;
+    const int hq = a.n_full + (j >> 1);  // the 32-query workgroup this quarter is half of
+    const int q_base = (hq / a.n_kt) * kPkhQT + 16 * (j & 1);
+    if (q_base >= a.B) return;
+    pk_tile<KFP8, 1, kPkhWaves>(a, sh, q_base, (hq % a.n_kt) * kPkKT);
+  }
+}
+
 // Quarter tiles: four-wave workgroups over 16 queries x 256 keys (each
 // wave: 64 keys x one 16-query block), with the four-wave kernel's LDS.  A
 // launch of at most kPkqMaxTiles full tiles runs as quarters, one per CU:
@@ -599,13 +622,23 @@ extern "C" int mi355_dsa_indexer_logits_packed(
     else
       indexer_logits_packed_q_kernel<false><<<dim3((unsigned)gq), kPkhWaves * 64, 0, st>>>(a);
   } else if (W >= kPkhMinTiles) {
-    // large launches: four-wave 32-query workgroups, two per CU
+    // large launches: four-wave 32-query workgroups, two per CU; a last
+    // round of at most half a round runs as quarter tiles
     const int64_t gh = n_kt * ((B + kPkhQT - 1) / kPkhQT);
-    DSA_CHECK(gh <= INT32_MAX, "B x max_kv too large");
-    if (k_fp8)
+    DSA_CHECK(gh + kPkCUs <= INT32_MAX, "B x max_kv too large");
+    const int64_t R = gh % (2 * kPkCUs);
+    if (R > 0 && R <= kPkCUs) {
+      a.n_full = (int)(gh - R);
+      const unsigned grid_hq = (unsigned)(gh + R);
+      if (k_fp8)
+        indexer_logits_packed_hq_kernel<true><<<dim3(grid_hq), kPkhWaves * 64, 0, st>>>(a);
+      else
+        indexer_logits_packed_hq_kernel<false><<<dim3(grid_hq), kPkhWaves * 64, 0, st>>>(a);
+    } else if (k_fp8) {
       indexer_logits_packed_h_kernel<true><<<dim3((unsigned)gh), kPkhWaves * 64, 0, st>>>(a);
-    else
+    } else {
       indexer_logits_packed_h_kernel<false><<<dim3((unsigned)gh), kPkhWaves * 64, 0, st>>>(a);
+    }
   } else if (k_fp8) {
     indexer_logits_packed_kernel<true><<<dim3((unsigned)grid), kPkThreads, 0, st>>>(a);
   } else {

@@ -190,8 +190,10 @@ def test_packed_matches_decode_kernel_on_dyadic(ops, dev):
 # Launch shapes of the packed kernel's tile split (full tiles are 64 queries
 # x 256 keys; W = tiles per launch): all full (W = 200); more than one round
 # (W = 260, 280 with a partial last query tile, and fp8 keys), which takes
-# the four-wave 32-query kernel; launches of at most 64 tiles as 16-query
-# quarter tiles, and of 65-128 tiles as half tiles.
+# the four-wave 32-query kernel, its last round as 16-query quarter tiles when
+# that round holds at most 256 of its workgroups (W = 260, 280, 384; W = 400
+# keeps a full last round); launches of at most 64 tiles as quarter tiles,
+# and of 65-128 tiles as half tiles.
 SPLIT = [
     # seed, B, max_kv, fp8
     (31, 128, 256 * 100, False),
