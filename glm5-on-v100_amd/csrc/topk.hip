@@ -420,58 +420,91 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
     for (int i = tid; i < kTopkBins; i += kTkThreads) sh.hist[i] = 0u;
     if (tid == 0) sh.n_list = 0u;
     __syncthreads();
-    // double buffered: the next step's loads are in flight while this one
-    // is counted and listed
+    // Double buffered: the next step's loads are in flight while this one
+    // is tested and listed.  The first step builds the histogram that sets
+    // te; every step then lists its keys of bin >= te.  The test is one
+    // float compare: for a non-NaN v, mono_key(v) >= te << 20 exactly when
+    // v >= fte, the smallest float of bin te, except v = -0 against
+    // fte = +0 (te = 0x800), which the bit test excl removes; bins below
+    // mono_key(-inf) hold only NaNs, so there fte = -inf.  The list holds
+    // the raw float bits until read 1 ends.
     float v[kTk2U], w[kTk2U];
     r1_load<V4>(row, 0, L, v);
-    for (int base = 0; base < L; base += kS0) {
-      r1_load<V4>(row, base + kS0, L, w);  // past the row: re-reads its last group, unused
-      if (base == 0) {
+    r1_load<V4>(row, kS0, L, w);  // past the row: re-reads its last group, unused
 #pragma unroll
-        for (int e = 0; e < kTk2U; e++) {
-          const int p = r1_pos<V4>(base, e);
-          if (p < L) atomicAdd(&sh.hist[mono_key(v[e]) >> 20], 1u);
-        }
-        __syncthreads();
-        const int S = min(L, kS0);
-        uint64_t tgt = (3ull * (uint64_t)K * S + 2ull * L - 1) / (2ull * L);
-        tgt = tgt < 1 ? 1 : (tgt > (uint64_t)S ? (uint64_t)S : tgt);
-        int Te;
-        uint32_t ab;
-        find_threshold(sh, kTopkBins, (uint32_t)tgt, &Te, &ab);
-        te = (uint32_t)Te;
-      }
-      // candidates of the step: one LDS atomic per wave for all of them
+    for (int e = 0; e < kTk2U; e++)
+      if (r1_pos<V4>(0, e) < L) atomicAdd(&sh.hist[mono_key(v[e]) >> 20], 1u);
+    __syncthreads();
+    {
+      const int S = min(L, kS0);
+      uint64_t tgt = (3ull * (uint64_t)K * S + 2ull * L - 1) / (2ull * L);
+      tgt = tgt < 1 ? 1 : (tgt > (uint64_t)S ? (uint64_t)S : tgt);
+      int Te;
+      uint32_t ab;
+      find_threshold(sh, kTopkBins, (uint32_t)tgt, &Te, &ab);
+      te = (uint32_t)Te;
+    }
+    const uint32_t tkey = te << 20;
+    const float fte = tkey <= 0x007fffffu
+                          ? -INFINITY
+                          : __uint_as_float((tkey & 0x80000000u) ? (tkey & 0x7fffffffu) : ~tkey);
+    const uint32_t excl = tkey == 0x80000000u ? 0x80000000u : 0xffffffffu;  // 0xffffffff: a NaN
+    const int lp0 = V4 ? 4 * tid : tid;  // this lane's position offset within a step
+    // lists the keys of bin >= te among vals (positions base + ...); the
+    // tag says whether the step reaches past L (conditions combined with &,
+    // not &&, so that no branch splits the tests)
+    auto step = [&](const float (&vals)[kTk2U], int base, auto check_tag) {
+      constexpr bool check = decltype(check_tag)::value;
       bool tk[kTk2U];
       uint64_t m[kTk2U];
       uint32_t cnt = 0;
 #pragma unroll
       for (int e = 0; e < kTk2U; e++) {
-        tk[e] = r1_pos<V4>(base, e) < L && (mono_key(v[e]) >> 20) >= te;
-        m[e] = __ballot(tk[e]);
+        tk[e] = (vals[e] >= fte) & (__float_as_uint(vals[e]) != excl);
+        if constexpr (check)
+          tk[e] = tk[e] & (base + lp0 + (V4 ? (e >> 2) * (4 * kTkThreads) + (e & 3) : e * kTkThreads) < L);
+        m[e] = __builtin_amdgcn_ballot_w64(tk[e]);
         cnt += (uint32_t)__popcll(m[e]);
       }
-      if (cnt != 0u) {
-        uint32_t b0 = 0;
-        if (lane == 0) b0 = atomicAdd(&sh.n_list, cnt);
-        b0 = __builtin_amdgcn_readlane(b0, 0);
+      if (cnt == 0u) return;
+      uint32_t b0 = 0;
+      if (lane == 0) b0 = atomicAdd(&sh.n_list, cnt);
+      b0 = __builtin_amdgcn_readlane(b0, 0);
 #pragma unroll
-        for (int e = 0; e < kTk2U; e++) {
-          if (tk[e]) {
-            // rank among the wave's taking lanes below this one
-            const uint32_t j = b0 + __builtin_amdgcn_mbcnt_hi(
-                                        (uint32_t)(m[e] >> 32),
-                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m[e], 0u));
-            if (j < (uint32_t)cap) {
-              lkey[j] = mono_key(v[e]);
-              lpos[j] = r1_pos<V4>(base, e);
-            }
+      for (int e = 0; e < kTk2U; e++) {
+        if (tk[e]) {
+          // rank among the wave's taking lanes below this one
+          const uint32_t j = b0 + __builtin_amdgcn_mbcnt_hi(
+                                      (uint32_t)(m[e] >> 32),
+                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m[e], 0u));
+          if (j < (uint32_t)cap) {
+            lkey[j] = __float_as_uint(vals[e]);
+            lpos[j] = base + lp0 + (V4 ? (e >> 2) * (4 * kTkThreads) + (e & 3) : e * kTkThreads);
           }
-          b0 += (uint32_t)__popcll(m[e]);
         }
+        b0 += (uint32_t)__popcll(m[e]);
       }
-#pragma unroll
-      for (int e = 0; e < kTk2U; e++) v[e] = w[e];
+    };
+    // steps alternate between the two buffers; a step wholly below L skips
+    // the position test
+    int base = 0;
+    while (true) {
+      if (base + kS0 > L) {
+        step(v, base, std::true_type{});
+        break;
+      }
+      step(v, base, std::false_type{});
+      base += kS0;
+      if (base >= L) break;
+      r1_load<V4>(row, base + kS0, L, v);
+      if (base + kS0 > L) {
+        step(w, base, std::true_type{});
+        break;
+      }
+      step(w, base, std::false_type{});
+      base += kS0;
+      if (base >= L) break;
+      r1_load<V4>(row, base + kS0, L, w);
     }
     __syncthreads();
     const uint32_t n_list = sh.n_list;
@@ -479,8 +512,12 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
     __syncthreads();  // every thread has read n_list and the first-step histogram
     for (int i = tid; i < kTopkBins; i += kTkThreads) sh.hist[i] = 0u;
     __syncthreads();
-    if (spec) {  // level-1 histogram of the listed keys
-      for (int i = tid; i < (int)n_list; i += kTkThreads) atomicAdd(&sh.hist[lkey[i] >> 20], 1u);
+    if (spec) {  // the list's keys as monotone keys, and their level-1 histogram
+      for (int i = tid; i < (int)n_list; i += kTkThreads) {
+        const uint32_t k = mono_key(__uint_as_float(lkey[i]));
+        lkey[i] = k;
+        atomicAdd(&sh.hist[k >> 20], 1u);
+      }
     } else {     // the estimate missed: level-1 histogram of the whole row
       row_pass<kTk2U>(row, L, [&](int, uint32_t key) { atomicAdd(&sh.hist[key >> 20], 1u); });
     }
