@@ -22,6 +22,10 @@
 //    spread over the row's 1024-key tiles.
 // The decode paths start from the level-1 histogram the indexer kernel
 // already built.  Every path is deterministic.
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "capi_internal.h"
 #include "dsa_common.h"
 #include "head_proj.h"
@@ -873,6 +877,12 @@ __device__ void sel_threshold(SelShared& sh, const uint32_t* hist, int nbins, ui
   *above = sh.above[par];
 }
 
+template <int TILE, bool AGENT>
+__device__ void topk_select_body(SelShared& sh, const float* __restrict__ row, int L, int K,
+                                 int32_t* __restrict__ out, const uint32_t* hrow, int n_tiles,
+                                 const TopkWs& ws, int b, int status, int T1, uint32_t above1,
+                                 uint32_t cnt_own);
+
 // Row b of the select (every return is workgroup-uniform).
 __device__ __forceinline__ void topk_select_row(
     SelShared& sh, const float* __restrict__ score, int max_kv,
@@ -894,13 +904,35 @@ __device__ __forceinline__ void topk_select_row(
     for (int p = threadIdx.x; p < K; p += kTkThreads) out[p] = (p < L) ? p : -1;
     return;
   }
-  const float* row = score + (int64_t)b * max_kv;
-  const uint32_t* hrow = hist + (int64_t)b * kTopkBins;
+  topk_select_body<kScanTile, false>(sh, score + (int64_t)b * max_kv, L, K, out,
+                                     hist + (int64_t)b * kTopkBins, n_tiles, ws, b, status, T1,
+                                     above1, cnt_own);
+}
+
+// Loads of the candidate lists and counts: agent-scope (coherent across
+// XCDs) where the lists were written in the same launch.
+template <bool AGENT, class T>
+__device__ __forceinline__ T ws_load(const T* p) {
+  if constexpr (AGENT)
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    return *p;
+}
+
+// The select of one row (L > K) from the level-1 threshold bin T1, the keys
+// above it (above1) and the candidate lists of TILE-position tiles; cnt_own
+// is thread t's tile count (t < used tiles).  status != 0: the histogram
+// was inconsistent with L, and the row is selected whole.
+template <int TILE, bool AGENT>
+__device__ void topk_select_body(SelShared& sh, const float* __restrict__ row, int L, int K,
+                                 int32_t* __restrict__ out, const uint32_t* hrow, int n_tiles,
+                                 const TopkWs& ws, int b, int status, int T1, uint32_t above1,
+                                 uint32_t cnt_own) {
   if (status != 0) {  // histogram inconsistent with L: rebuild from the row
     topk_row_select(sh.u.full, row, L, K, out, nullptr);
     return;
   }
-  const int used_tiles = (L + kScanTile - 1) / kScanTile;  // <= n_tiles <= 1024
+  const int used_tiles = (L + TILE - 1) / TILE;  // <= n_tiles <= 1024
   // the second-level histogram starts zero (the scan's barrier orders this
   // before the gather's counts)
   for (int i = threadIdx.x; i < kSelBins; i += kTkThreads) sh.u.c.hist[i] = 0u;
@@ -939,9 +971,9 @@ __device__ __forceinline__ void topk_select_row(
           const int mid = (lo + hi) >> 1;
           if (sh.u.c.toff[mid] <= i) lo = mid; else hi = mid;
         }
-        const int64_t src = ((int64_t)b * n_tiles + lo) * kScanTile + (i - sh.u.c.toff[lo]);
-        kk[u] = ws.ckey[src];
-        pp[u] = ws.cpos[src];
+        const int64_t src = ((int64_t)b * n_tiles + lo) * TILE + (i - sh.u.c.toff[lo]);
+        kk[u] = ws_load<AGENT>(ws.ckey + src);
+        pp[u] = ws_load<AGENT>(ws.cpos + src);
       }
     }
 #pragma unroll
@@ -1059,6 +1091,147 @@ __global__ void __launch_bounds__(kTkThreads) topk_select_kernel(
   }
 }
 
+// ===========================================================================
+// Decode top-k in one launch, for calls whose scan is one round of
+// workgroups (rows x groups <= 256, one workgroup per CU).  Workgroup (b, g)
+// of 1024 threads scans positions [4096 g, 4096 g + 4096) of row b as
+// topk_scan_kernel does -- T1 from the row's histogram, then the keys of bin
+// >= T1 in position order -- and writes its list and count with agent-scope
+// stores (coherent across XCDs).  It then counts itself in on the row's
+// arrival counter (one device atomic add); the workgroup that completes the
+// count resets the counter to zero and selects the row (topk_select_body,
+// reading the lists with agent-scope loads).  No workgroup waits on
+// another.
+// The counters live in a per-device pool, zero at load and left zero by
+// every call.  The host gives each stream one slot of kArriveRows counters
+// for its eager calls (calls on one stream never overlap) and each call
+// captured into a graph a slot of its own, kept for the graph's replays;
+// when the pool is spent, calls take the two-kernel path.
+// ===========================================================================
+constexpr int kFTile = 4 * kTkThreads;  // positions per workgroup
+constexpr int kFusedMaxWgs = 256;
+constexpr int kArriveRows = 64;         // counters per slot: rows per call, at most
+constexpr int kArriveSlots = 16384;
+__device__ uint32_t g_topk_arrive[kArriveSlots * kArriveRows];
+
+struct FusedShared {
+  SelShared sel;
+  uint32_t wsum[2 * kTkWaves];
+  int T1;
+  uint32_t above1;
+  int last;
+};
+
+template <bool PROJ>
+__global__ void __launch_bounds__(kTkThreads) topk_fused_kernel(
+    const float* __restrict__ score, int max_kv, const int32_t* __restrict__ seq_lens,
+    const uint32_t* hist, int32_t* __restrict__ idx, int K, int n_groups, TopkWs ws,
+    uint32_t* arrive, uint32_t* clear_hist, int n_rows, SelProj proj) {
+  const int id = blockIdx.x;
+  if constexpr (PROJ) {
+    if (id >= n_rows * n_groups) {
+      const int vb = (id - n_rows * n_groups) * 4 + (int)(threadIdx.x >> 8);
+      if (vb < proj.wgs) head_proj_block<4, 1>(proj.hp, vb % proj.gx, vb / proj.gx, threadIdx.x & 255);
+      return;
+    }
+  }
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  FusedShared& sh = *reinterpret_cast<FusedShared*>(smem_raw);
+  const int tid = threadIdx.x;
+  const int b = id / n_groups, g = id - b * n_groups;
+  int32_t* out = idx + (int64_t)b * K;
+  const float* row = score + (int64_t)b * max_kv;
+  const uint32_t* hrow = hist + (int64_t)b * kTopkBins;
+  int L = seq_lens[b];
+  L = L < 0 ? 0 : (L > max_kv ? max_kv : L);
+  if (L <= K) {  // every position, -1 padded: workgroup 0 of the row
+    if (g == 0) {
+      for (int p = tid; p < K; p += kTkThreads) out[p] = (p < L) ? p : -1;
+      if (clear_hist != nullptr) {
+        u32x4* h = reinterpret_cast<u32x4*>(clear_hist + (int64_t)b * kTopkBins);
+        for (int i = tid; i < kTopkBins / 4; i += kTkThreads) h[i] = (u32x4){0u, 0u, 0u, 0u};
+      }
+    }
+    return;
+  }
+  const int ng = (L + kFTile - 1) / kFTile;  // the row's workgroups
+  if (g >= ng) return;
+  // ---- scan: thread t's 4 positions and 4 histogram bins, loaded together ----
+  const int p0 = g * kFTile + 4 * tid;
+  float v[4];
+  uint32_t hb[4], cs = 0;
+#pragma unroll
+  for (int e = 0; e < 4; e++) v[e] = row[min(p0 + e, L - 1)];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    hb[i] = hrow[4 * tid + i];
+    cs += hb[i];
+  }
+  uint32_t total;
+  const uint32_t excl = block_excl_scan1<kTkThreads>(cs, sh.wsum, 0, &total);
+  const bool bad = total != (uint32_t)L;  // the histogram does not count the row's L keys
+  if (!bad) {
+    uint32_t a = total - excl - cs;  // keys in bins above this thread's bins
+#pragma unroll
+    for (int i = 3; i >= 0; i--) {
+      if (a < (uint32_t)K && a + hb[i] >= (uint32_t)K) {
+        sh.T1 = 4 * tid + i;
+        sh.above1 = a;
+      }
+      a += hb[i];
+    }
+  }
+  __syncthreads();
+  const int T1 = bad ? 0 : sh.T1;
+  const uint32_t above1 = bad ? 0u : sh.above1;
+  if (!bad) {  // the candidates, in position order
+    uint32_t key[4], n = 0;
+    bool cand[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      key[e] = mono_key(v[e]);
+      cand[e] = p0 + e < L && (int)(key[e] >> 20) >= T1;
+      n += cand[e] ? 1u : 0u;
+    }
+    uint32_t tot;
+    uint32_t off = block_excl_scan1<kTkThreads>(n, sh.wsum, 1, &tot);
+    const int64_t slot0 = ((int64_t)b * n_groups + g) * kFTile;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      if (cand[e]) {
+        __hip_atomic_store(ws.ckey + slot0 + off, key[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ws.cpos + slot0 + off, p0 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        off++;
+      }
+    }
+    if (tid == 0)
+      __hip_atomic_store(ws.counts + (int64_t)b * n_groups + g, (int32_t)tot, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // ---- arrival: every wave's list stores are complete before the count moves ----
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t before =
+        __hip_atomic_fetch_add(arrive + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = before + 1u == (uint32_t)ng;
+    if (last) __hip_atomic_store(arrive + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh.last = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (sh.last == 0) return;
+  // ---- the row's select, by the workgroup that completed the count ----
+  const uint32_t cnt_own = (uint32_t)ws_load<true>(ws.counts + (int64_t)b * n_groups +
+                                                   min(tid, n_groups - 1));
+  topk_select_body<kFTile, true>(sh.sel, row, L, K, out, hrow, n_groups, ws, b, bad ? 1 : 0, T1,
+                                 above1, cnt_own);
+  if (clear_hist != nullptr) {
+    __syncthreads();  // every read of the row's histogram is done
+    u32x4* h = reinterpret_cast<u32x4*>(clear_hist + (int64_t)b * kTopkBins);
+    for (int i = tid; i < kTopkBins / 4; i += kTkThreads) h[i] = (u32x4){0u, 0u, 0u, 0u};
+  }
+}
+
 }  // namespace mi355dsa
 
 using namespace mi355dsa;
@@ -1066,14 +1239,83 @@ using namespace mi355dsa;
 // Rows per call up to which the two-kernel path is used: it needs fewer
 // launches' worth of parallelism than one workgroup per row provides.
 constexpr int kTwoKernelMaxRows = 64;
+static_assert(kArriveRows >= kTwoKernelMaxRows, "an arrival slot covers every row of a call");
 
 static bool two_kernel_topk(int B, int max_kv, int k) {
   return B <= kTwoKernelMaxRows && max_kv > k && (max_kv + kScanTile - 1) / kScanTile <= 1024;
 }
 
+// The one-launch path: the scan is at most one round of workgroups.
+static bool fused_topk(int B, int max_kv, int k) {
+  return two_kernel_topk(B, max_kv, k) &&
+         (int64_t)B * ((max_kv + kFTile - 1) / kFTile) <= kFusedMaxWgs;
+}
+
+// One-launch workspace: the group counts, then the 4096 (key, position)
+// candidate slots per group.
+static size_t fused_ws_bytes(int B, int ng) {
+  return ((size_t)B * ng * sizeof(int32_t) + 15) / 16 * 16 +
+         (size_t)B * ng * kFTile * (sizeof(uint32_t) + sizeof(int32_t));
+}
+
+static void fused_ws(void* base, int B, int ng, TopkWs* ws) {
+  char* p = reinterpret_cast<char*>(base);
+  ws->meta = nullptr;
+  ws->counts = reinterpret_cast<int32_t*>(p);
+  p += ((size_t)B * ng * sizeof(int32_t) + 15) / 16 * 16;
+  ws->ckey = reinterpret_cast<uint32_t*>(p);
+  p += (size_t)B * ng * kFTile * sizeof(uint32_t);
+  ws->cpos = reinterpret_cast<int32_t*>(p);
+}
+
+// The arrival counters of a one-launch call on stream st: the stream's own
+// slot for an eager call, a new slot for a call being captured into a graph
+// (its replays keep it).  nullptr when the pool is spent or cannot be found;
+// the caller then takes the two-kernel path.
+static uint32_t* arrive_slot(hipStream_t st) {
+  static std::mutex mu;
+  static std::map<int, uint32_t*> pool;                     // device -> pool base
+  static std::map<int, int> used;                           // device -> slots handed out
+  static std::map<std::pair<int, hipStream_t>, int> eager;  // (device, stream) -> slot
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  auto pit = pool.find(dev);
+  if (pit == pool.end()) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_topk_arrive)) != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    pit = pool.emplace(dev, reinterpret_cast<uint32_t*>(p)).first;
+  }
+  int& n = used[dev];
+  if (cs == hipStreamCaptureStatusNone) {
+    const auto it = eager.find({dev, st});
+    if (it != eager.end()) return pit->second + (size_t)it->second * kArriveRows;
+    if (n >= kArriveSlots) return nullptr;
+    eager.emplace(std::make_pair(dev, st), n);
+  } else if (n >= kArriveSlots) {
+    return nullptr;
+  }
+  return pit->second + (size_t)(n++) * kArriveRows;
+}
+
 extern "C" size_t mi355_dsa_decode_topk_workspace_size(int B, int max_kv, int k) {
   if (B <= 0 || max_kv <= 0 || !two_kernel_topk(B, max_kv, k)) return 0;
-  return topk_ws_bytes(B, (max_kv + kScanTile - 1) / kScanTile);
+  const size_t two = topk_ws_bytes(B, (max_kv + kScanTile - 1) / kScanTile);
+  if (!fused_topk(B, max_kv, k)) return two;
+  // the one-launch layout, or the two-kernel one should the arrival pool be spent
+  const size_t one = fused_ws_bytes(B, (max_kv + kFTile - 1) / kFTile);
+  return one > two ? one : two;
 }
 
 // Shared by mi355_dsa_decode_topk and the layer step's variant.  clear: the
@@ -1092,6 +1334,36 @@ static int decode_topk_impl(int32_t* idx, const float* score, const int32_t* seq
   DSA_CHECK(!clear || aligned_to(hist, 16), "hist must be 16-byte aligned");
   hipStream_t st = as_stream(stream);
   uint32_t* h = reinterpret_cast<uint32_t*>(hist);
+  uint32_t* arrive = nullptr;
+  if (fused_topk(B, max_kv, k)) arrive = arrive_slot(st);
+  if (arrive != nullptr) {
+    const int ng = (max_kv + kFTile - 1) / kFTile;
+    const size_t need = fused_ws_bytes(B, ng);
+    DSA_CHECK(workspace && workspace_bytes >= need,
+              "workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    DSA_CHECK(aligned_to(workspace, 16), "workspace must be 16-byte aligned");
+    TopkWs ws;
+    fused_ws(workspace, B, ng, &ws);
+    uint32_t* ch = clear ? h : nullptr;
+    int rc;
+    if (proj != nullptr) {
+      rc = reserve_lds(reinterpret_cast<const void*>(topk_fused_kernel<true>), sizeof(FusedShared),
+                       "decode_topk");
+      if (rc) return rc;
+      const int64_t grid = (int64_t)B * ng + (proj->wgs + 3) / 4;
+      DSA_CHECK(grid < ((int64_t)1 << 31), "decode_topk: grid too large");
+      topk_fused_kernel<true><<<(unsigned)grid, kTkThreads, sizeof(FusedShared), st>>>(
+          score, max_kv, seq_lens, h, idx, k, ng, ws, arrive, ch, B, *proj);
+      if (proj_done) *proj_done = true;
+    } else {
+      rc = reserve_lds(reinterpret_cast<const void*>(topk_fused_kernel<false>), sizeof(FusedShared),
+                       "decode_topk");
+      if (rc) return rc;
+      topk_fused_kernel<false><<<(unsigned)(B * ng), kTkThreads, sizeof(FusedShared), st>>>(
+          score, max_kv, seq_lens, h, idx, k, ng, ws, arrive, ch, B, SelProj{});
+    }
+    return check_launch("decode_topk fused");
+  }
   if (two_kernel_topk(B, max_kv, k)) {
     const int n_tiles = (max_kv + kScanTile - 1) / kScanTile;
     const size_t need = topk_ws_bytes(B, n_tiles);

@@ -282,7 +282,10 @@ int mi355_dsa_indexer_logits_packed(float* score, int B, int max_kv,
  * Decode top-k: idx[b,:] = the positions p < seq_len[b] of the k largest
  * score[b,p] (exact 32-bit order; equal scores prefer the lower position),
  * written in ascending position order and padded with -1.  hist is the
- * [B,4096] level-1 histogram built by mi355_dsa_indexer_logits.
+ * [B,4096] level-1 histogram built by mi355_dsa_indexer_logits.  The
+ * workspace holds candidate lists only (no state between calls); per-row
+ * arrival counters of the one-launch path live in a library-owned device
+ * array, one slot per stream and per captured call.
  * Replaces sm70_decode_topk (csrc/attention/sm70_mla_decode.cu:2844-2905).
  */
 size_t mi355_dsa_decode_topk_workspace_size(int B, int max_kv, int k);
@@ -297,8 +300,9 @@ int mi355_dsa_decode_topk(int32_t* idx, const float* score,
  * also leaves hist zero (16-byte aligned) for the next step's
  * mi355_dsa_decode_layer_indexer, and the q_nope -> latent projection as
  * mi355_dsa_head_proj (x = q, wt = W_UK_T^T [H, N, K], carried tail
- * columns).  On the two-kernel top-k path with K < 256 the projection runs
- * in the select launch, on the CUs the select leaves idle.  Results are
+ * columns).  On the one-launch and two-kernel top-k paths with K < 256 the
+ * projection runs in the launch that selects, on CUs the select leaves
+ * idle.  Results are
  * bit-identical to the two calls.  The reference zeroes a fresh histogram
  * each step (reference/sparse_attn_indexer.py:601) and projects q in the MLA
  * layer (triton_mla.py:413-418).

@@ -76,6 +76,7 @@ def test_decode_topk_rebuilds_bad_hist(ops, dev):
     ("equal", 1, 40000, [40000], 2048),       # candidate set above the LDS cap: whole-row path
     ("ties", 2, 50000, [50000, 30001], 2048),  # many keys share the threshold bin
     ("randn", 100, 5000, None, 256),            # more rows than the two-kernel path takes
+    ("randn", 64, 20000, None, 2048),           # rows x 4096-key groups past one launch round: scan + select
     ("randn", 3, 3000, [2049, 2048, 3000], 2048),
 ])
 def test_decode_topk_paths(ops, dev, kind, B, W, seq, K):
@@ -126,6 +127,95 @@ def test_persistent_topk_select_paths(ops, dev, case):
     ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
     ops.persistent_topk(s.to(dev), seq.view(B, 1).to(dev), out, ws, 2048, W)
     assert torch.equal(out.cpu(), cref.topk_rows(s, seq, 2048))
+
+
+def _decode_topk_abi(pkg, idx, s, seq, h, K, ws, stream=None):
+    st = stream if stream is not None else torch.cuda.current_stream()
+    pkg._lib.call("mi355_dsa_decode_topk", idx.data_ptr(), s.data_ptr(), seq.data_ptr(),
+                  h.data_ptr(), s.size(0), s.size(1), K, ws.data_ptr(), ws.numel(), st.cuda_stream)
+
+
+def test_decode_topk_one_launch_workspace(pkg, dev):
+    """The one-launch decode top-k keeps no state in its workspace (its
+    arrival counters live in the library's per-device pool): a workspace
+    holding arbitrary bytes, one reused across calls of other shapes and bad
+    histograms, and calls on two streams at once (each stream its own
+    counter slot) all give the exact selection."""
+    L = pkg._lib.lib()
+    g = torch.Generator().manual_seed(77)
+    calls = [
+        ("randn", 4, 65536, [65536, 60000, 3000, 2049], 2048, False),
+        ("ties", 2, 9000, [9000, 8000], 512, False),
+        ("narrow", 3, 20000, [20000, 19000, 100], 2048, True),   # bad histogram: whole row
+        ("randn", 4, 65536, [65536] * 4, 2048, False),
+        ("mixed", 1, 184320, [184320], 2048, False),
+    ]
+    wsb = max(L.mi355_dsa_decode_topk_workspace_size(B, W, K) for _, B, W, _, K, _ in calls)
+    for fill in (0xFF, None):
+        ws = (torch.full((wsb,), fill, dtype=torch.uint8, device=dev) if fill is not None
+              else torch.randint(0, 256, (wsb,), dtype=torch.uint8, device=dev))
+        for kind, B, W, seq, K, bad in calls:
+            s = scores(kind, B, W, g)
+            seq_t = torch.tensor(seq, dtype=torch.int32)
+            h = hist_of(s, seq_t)
+            if bad:
+                h[0] = 0
+            idx = torch.full((B, K), 123, dtype=torch.int32, device=dev)
+            _decode_topk_abi(pkg, idx, s.to(dev), seq_t.to(dev), h.to(dev), K, ws)
+            assert torch.equal(idx.cpu(), cref.topk_rows(s, seq_t, K)), (fill, kind, B, W)
+    # two streams, each with its own workspace, launched back to back
+    st = [torch.cuda.Stream(), torch.cuda.Stream()]
+    jobs = []
+    for i in range(2):
+        s = scores("randn", 4, 65536, g)
+        seq_t = torch.tensor([65536, 65000 - i, 40000, 2100], dtype=torch.int32)
+        jobs.append((s, seq_t, s.to(dev), seq_t.to(dev), hist_of(s, seq_t).to(dev),
+                     torch.empty(4, 2048, dtype=torch.int32, device=dev),
+                     torch.empty(wsb, dtype=torch.uint8, device=dev)))
+    torch.cuda.synchronize()
+    for i, (_, _, sd, qd, hd, idx, ws) in enumerate(jobs):
+        _decode_topk_abi(pkg, idx, sd, qd, hd, 2048, ws, stream=st[i])
+    torch.cuda.synchronize()
+    for s, seq_t, _, _, _, idx, _ in jobs:
+        assert torch.equal(idx.cpu(), cref.topk_rows(s, seq_t, 2048))
+
+
+def test_decode_topk_one_launch_graph_replays(pkg, dev):
+    """One-launch decode top-k captured in a HIP graph: every replay, with the
+    scores and histograms rewritten in place between replays and an eager
+    call on the same workspace in between, equals the oracle (each row's
+    last workgroup leaves its arrival counter zero)."""
+    L = pkg._lib.lib()
+    B, W, K = 4, 65536, 2048
+    seq = torch.tensor([65536, 50000, 2049, 30000], dtype=torch.int32)
+    g = torch.Generator().manual_seed(78)
+    wsb = L.mi355_dsa_decode_topk_workspace_size(B, W, K)
+    sd = torch.empty(B, W, device=dev)
+    hd = torch.empty(B, 4096, dtype=torch.int32, device=dev)
+    qd = seq.to(dev)
+    idx = torch.empty(B, K, dtype=torch.int32, device=dev)
+    ws = torch.full((wsb,), 0x5A, dtype=torch.uint8, device=dev)
+    s = scores("randn", B, W, g)
+    sd.copy_(s)
+    hd.copy_(hist_of(s, seq))
+    _decode_topk_abi(pkg, idx, sd, qd, hd, K, ws)  # eager first call, outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _decode_topk_abi(pkg, idx, sd, qd, hd, K, ws)
+    for i, kind in enumerate(["ties", "randn", "mixed"]):
+        s = scores(kind, B, W, g)
+        sd.copy_(s)
+        hd.copy_(hist_of(s, seq))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(idx.cpu(), cref.topk_rows(s, seq, K)), f"replay {i}"
+        other = torch.empty_like(idx)
+        _decode_topk_abi(pkg, other, sd, qd, hd, K, ws)  # eager, same workspace
+        torch.cuda.synchronize()
+        assert torch.equal(other, idx), f"eager after replay {i}"
+    del graph
 
 
 def test_decode_topk_many_rows_bad_hist(ops, dev):
