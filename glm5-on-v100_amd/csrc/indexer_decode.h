@@ -22,7 +22,8 @@ constexpr int kIdxGroup = 2;              // 16-key blocks per pipeline stage
 // fp16 rows: dims 32s + 8g .. +8 for steps s = 0..3, four 16-byte loads of
 // which load s of the four lanes of a key covers 64 contiguous bytes of its
 // row (one half cache line per key and instruction).  fp8 rows: dims
-// [32g, 32g+32), 32 bytes.
+// [16g, 16g+16) and [64 + 16g, 64 + 16g + 16), two 16-byte loads of which
+// each covers 64 contiguous bytes of the row across the four lanes of a key.
 struct KeyFrag {
   u32x4 v[4];
   float scale;  // fp8: row scale; fp16: 1
@@ -41,9 +42,8 @@ __device__ __forceinline__ void load_key_frag(KeyFrag& f, const void* kv,
   if constexpr (KFP8) {
     const uint8_t* rp =
         reinterpret_cast<const uint8_t*>(kv) + row * (int64_t)kIdxkFp8RowBytes;
-    const u32x4_a4* p = reinterpret_cast<const u32x4_a4*>(rp + 32 * g);
-    f.v[0] = p[0];
-    f.v[1] = p[1];
+    f.v[0] = *reinterpret_cast<const u32x4_a4*>(rp + 16 * g);
+    f.v[1] = *reinterpret_cast<const u32x4_a4*>(rp + 64 + 16 * g);
     f.scale = *reinterpret_cast<const float*>(rp + 128);
   } else {
     const u32x4* p = reinterpret_cast<const u32x4*>(
@@ -66,9 +66,8 @@ __device__ __forceinline__ void load_key_frag_nb(KeyFrag& f, const void* kv, int
   const int64_t r = row < 0 ? 0 : row;
   if constexpr (KFP8) {
     const uint8_t* rp = reinterpret_cast<const uint8_t*>(kv) + r * (int64_t)kIdxkFp8RowBytes;
-    const u32x4_a4* p = reinterpret_cast<const u32x4_a4*>(rp + 32 * g);
-    f.v[0] = p[0];
-    f.v[1] = p[1];
+    f.v[0] = *reinterpret_cast<const u32x4_a4*>(rp + 16 * g);
+    f.v[1] = *reinterpret_cast<const u32x4_a4*>(rp + 64 + 16 * g);
     f.scale = *reinterpret_cast<const float*>(rp + 128);
   } else {
     const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const f16*>(kv) +
@@ -80,7 +79,7 @@ __device__ __forceinline__ void load_key_frag_nb(KeyFrag& f, const void* kv, int
 }
 
 // B operand for step s from a key fragment (dims 32s + 8g .. +8 for fp16
-// rows, 32g + 8s .. +8 for fp8 rows).
+// rows, 64 (s >> 1) + 16g + 8 (s & 1) .. +8 for fp8 rows).
 template <bool KFP8>
 __device__ __forceinline__ f16x8 key_operand(const KeyFrag& f, int s) {
   if constexpr (KFP8) {
@@ -236,8 +235,9 @@ __device__ __forceinline__ void indexer_logits_body(
   const int c = lane & 15, g = lane >> 4;
 
   // A operands: q rows (heads c and 16 + c), with the keys' k-slot mapping:
-  // step s, group g, slot e -> dim 32s + 8g + e (fp16 keys) or 32g + 8s + e
-  // (fp8 keys, whose 32 bytes per lane are one contiguous span).
+  // step s, group g, slot e -> dim 32s + 8g + e (fp16 keys) or
+  // 64 (s >> 1) + 16g + 8 (s & 1) + e (fp8 keys, whose two 16-byte loads per
+  // lane are [16g, +16) and [64 + 16g, +16)).
   f16x8 qa[2][4];
   const f16* qb = Q + (int64_t)b * kIdxHeads * kIdxHeadDim;
 #pragma unroll
@@ -245,7 +245,8 @@ __device__ __forceinline__ void indexer_logits_body(
 #pragma unroll
     for (int s = 0; s < 4; s++)
       qa[t][s] = *reinterpret_cast<const f16x8*>(
-          qb + (16 * t + c) * kIdxHeadDim + (KFP8 ? 32 * g + 8 * s : 32 * s + 8 * g));
+          qb + (16 * t + c) * kIdxHeadDim +
+          (KFP8 ? 64 * (s >> 1) + 16 * g + 8 * (s & 1) : 32 * s + 8 * g));
   // head weights of this lane's D rows: heads 4g + r and 16 + 4g + r
   float wv[2][4];
 #pragma unroll
