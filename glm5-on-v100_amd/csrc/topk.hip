@@ -1097,11 +1097,12 @@ __global__ void __launch_bounds__(kTkThreads) topk_select_kernel(
 // of 1024 threads scans positions [4096 g, 4096 g + 4096) of row b as
 // topk_scan_kernel does -- T1 from the row's histogram, then the keys of bin
 // >= T1 in position order -- and writes its list and count with agent-scope
-// stores (coherent across XCDs).  It then counts itself in on the row's
-// arrival counter (one device atomic add); the workgroup that completes the
-// count resets the counter to zero and selects the row (topk_select_body,
-// reading the lists with agent-scope loads).  No workgroup waits on
-// another.
+// stores (written through the XCD's L2 to memory).  After s_waitcnt
+// vmcnt(0) -- every such store acknowledged -- it counts itself in on the
+// row's arrival counter (one device atomic add); the workgroup that
+// completes the count resets the counter to zero and selects the row
+// (topk_select_body), reading the lists with agent-scope loads, which do
+// not take stale lines from its own L2.  No workgroup waits on another.
 // The counters live in a per-device pool, zero at load and left zero by
 // every call.  The host gives each stream one slot of kArriveRows counters
 // for its eager calls (calls on one stream never overlap) and each call
