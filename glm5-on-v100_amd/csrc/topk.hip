@@ -292,6 +292,46 @@ struct Tk2Head {
 constexpr int kTk2U = 8;
 constexpr int kTk2HeadBytes = (int)((sizeof(Tk2Head) + 15) / 16 * 16);
 
+// find_threshold by wave 0 alone; the other waves wait at one barrier.  Lane
+// l sums bins [l per, l per + per) with 16-byte LDS reads, a suffix scan
+// over the lanes finds the lane whose bins hold the threshold, and a second
+// scan over that lane's bins, one per lane, finds the bin: the bin T with
+// above(T) < need <= above(T) + hist[T], as find_threshold returns.  nbins
+// is 1024 or 4096; requires 1 <= need <= total.  It ends without a barrier:
+// a caller that writes hist next puts one first.
+__device__ void find_threshold_w0(Tk2Head& sh, int nbins, uint32_t need, int* T,
+                                  uint32_t* above) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int per = nbins >> 6;  // 16 or 64 bins per lane
+    const u32x4* h4 = reinterpret_cast<const u32x4*>(sh.hist) + lane * (per >> 2);
+    uint32_t cs = 0;
+    for (int i = 0; i < (per >> 2); i++) {
+      const u32x4 q = h4[i];
+      cs += q[0] + q[1] + q[2] + q[3];
+    }
+    const uint32_t incl = wave_incl_scan(cs);
+    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    const uint32_t a = total - incl;  // keys in the bins of the lanes above
+    const uint64_t hit = __ballot((a < need) & (a + cs >= need));
+    const int L = hit != 0ull ? (int)__builtin_ctzll(hit) : 0;
+    const uint32_t aL = (uint32_t)__builtin_amdgcn_readlane((int)a, L);
+    const uint32_t hv = lane < per ? sh.hist[L * per + lane] : 0u;
+    const uint32_t incl2 = wave_incl_scan(hv);
+    const uint32_t a2 = aL + ((uint32_t)__builtin_amdgcn_readlane((int)incl2, 63) - incl2);
+    const uint64_t hit2 = __ballot((lane < per) & (a2 < need) & (a2 + hv >= need));
+    const int j = hit2 != 0ull ? (int)__builtin_ctzll(hit2) : 0;
+    const uint32_t aj = (uint32_t)__builtin_amdgcn_readlane((int)a2, j);
+    if (lane == 0) {
+      sh.T = L * per + j;
+      sh.above = aj;
+    }
+  }
+  __syncthreads();
+  *T = sh.T;
+  *above = sh.above;
+}
+
 // wave_incl_scan of two packed 32-bit counts whose sums stay below 2^32.
 __device__ __forceinline__ uint64_t wave_incl_scan64(uint64_t x) {
   const uint32_t lo = wave_incl_scan((uint32_t)x);
@@ -445,7 +485,7 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
       tgt = tgt < 1 ? 1 : (tgt > (uint64_t)S ? (uint64_t)S : tgt);
       int Te;
       uint32_t ab;
-      find_threshold(sh, kTopkBins, (uint32_t)tgt, &Te, &ab);
+      find_threshold_w0(sh, kTopkBins, (uint32_t)tgt, &Te, &ab);
       te = (uint32_t)Te;
     }
     const uint32_t tkey = te << 20;
@@ -529,7 +569,7 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
   }
   int T;
   uint32_t above;
-  find_threshold(sh, kTopkBins, (uint32_t)K, &T, &above);
+  find_threshold_w0(sh, kTopkBins, (uint32_t)K, &T, &above);
   uint32_t need = (uint32_t)K - above;   // keys still to take among the undecided
   uint32_t prefix = (uint32_t)T;         // undecided: (key >> shift) == prefix
   int shift = 20;
@@ -555,7 +595,7 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
         if ((key >> shift) == prefix) atomicAdd(&sh.hist[(key >> s2) & 1023u], 1u);
       });
       __syncthreads();
-      find_threshold(sh, 1024, need, &T, &above);
+      find_threshold_w0(sh, 1024, need, &T, &above);
       need -= above;
       prefix = (prefix << 10) | (uint32_t)T;
       shift = s2;
@@ -613,7 +653,7 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
         if ((k >> shift) == prefix) atomicAdd(&sh.hist[(k >> s2) & 1023u], 1u);
       }
       __syncthreads();
-      find_threshold(sh, 1024, need, &T, &above);
+      find_threshold_w0(sh, 1024, need, &T, &above);
       need -= above;
       prefix = (prefix << 10) | (uint32_t)T;
       shift = s2;
