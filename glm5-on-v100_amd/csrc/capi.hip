@@ -150,6 +150,46 @@ static double e4m3_value(int b) {
   return s ? -mag : mag;
 }
 
+constexpr int kArriveSlots = 16384;
+__device__ uint32_t g_arrive[kArriveSlots * kArriveRows];
+
+uint32_t* arrive_slot(hipStream_t st) {
+  static std::mutex mu;
+  static std::map<int, uint32_t*> pool;                     // device -> pool base
+  static std::map<int, int> used;                           // device -> slots handed out
+  static std::map<std::pair<int, hipStream_t>, int> eager;  // (device, stream) -> slot
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  auto pit = pool.find(dev);
+  if (pit == pool.end()) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_arrive)) != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    pit = pool.emplace(dev, reinterpret_cast<uint32_t*>(p)).first;
+  }
+  int& n = used[dev];
+  if (cs == hipStreamCaptureStatusNone) {
+    const auto it = eager.find({dev, st});
+    if (it != eager.end()) return pit->second + (size_t)it->second * kArriveRows;
+    if (n >= kArriveSlots) return nullptr;
+    eager.emplace(std::make_pair(dev, st), n);
+  } else if (n >= kArriveSlots) {
+    return nullptr;
+  }
+  return pit->second + (size_t)(n++) * kArriveRows;
+}
+
 }  // namespace mi355dsa
 
 using namespace mi355dsa;

@@ -23,6 +23,17 @@ int check_launch(const char* what);
 // per device and kernel; thread-safe); MI355_DSA_EHIP on failure.
 int reserve_lds(const void* kernel, size_t bytes, const char* what);
 
+// Arrival counters for launches whose last workgroup of a group finishes
+// the group's work (one device atomic add per workgroup, no waiting): a slot
+// of kArriveRows counters in a per-device pool that is zero at load, each
+// call's last workgroups leaving their counters zero again.  An eager call
+// gets its stream's slot (calls on one stream never overlap, so every op of
+// a stream can share it); a call being captured into a graph gets a slot of
+// its own, kept by the graph's replays.  nullptr when the pool is spent or
+// unavailable: the caller then takes a path without counters.
+constexpr int kArriveRows = 64;
+uint32_t* arrive_slot(hipStream_t st);
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline bool aligned_to(const void* p, uintptr_t a) {

@@ -22,10 +22,6 @@
 //    spread over the row's 1024-key tiles.
 // The decode paths start from the level-1 histogram the indexer kernel
 // already built.  Every path is deterministic.
-#include <map>
-#include <mutex>
-#include <utility>
-
 #include "capi_internal.h"
 #include "dsa_common.h"
 #include "head_proj.h"
@@ -1143,17 +1139,11 @@ __global__ void __launch_bounds__(kTkThreads) topk_select_kernel(
 // completes the count resets the counter to zero and selects the row
 // (topk_select_body), reading the lists with agent-scope loads, which do
 // not take stale lines from its own L2.  No workgroup waits on another.
-// The counters live in a per-device pool, zero at load and left zero by
-// every call.  The host gives each stream one slot of kArriveRows counters
-// for its eager calls (calls on one stream never overlap) and each call
-// captured into a graph a slot of its own, kept for the graph's replays;
-// when the pool is spent, calls take the two-kernel path.
+// The counters come from the library's pool (arrive_slot); when it is
+// spent, calls take the two-kernel path.
 // ===========================================================================
 constexpr int kFTile = 4 * kTkThreads;  // positions per workgroup
 constexpr int kFusedMaxWgs = 256;
-constexpr int kArriveRows = 64;         // counters per slot: rows per call, at most
-constexpr int kArriveSlots = 16384;
-__device__ uint32_t g_topk_arrive[kArriveSlots * kArriveRows];
 
 struct FusedShared {
   SelShared sel;
@@ -1307,47 +1297,6 @@ static void fused_ws(void* base, int B, int ng, TopkWs* ws) {
   ws->ckey = reinterpret_cast<uint32_t*>(p);
   p += (size_t)B * ng * kFTile * sizeof(uint32_t);
   ws->cpos = reinterpret_cast<int32_t*>(p);
-}
-
-// The arrival counters of a one-launch call on stream st: the stream's own
-// slot for an eager call, a new slot for a call being captured into a graph
-// (its replays keep it).  nullptr when the pool is spent or cannot be found;
-// the caller then takes the two-kernel path.
-static uint32_t* arrive_slot(hipStream_t st) {
-  static std::mutex mu;
-  static std::map<int, uint32_t*> pool;                     // device -> pool base
-  static std::map<int, int> used;                           // device -> slots handed out
-  static std::map<std::pair<int, hipStream_t>, int> eager;  // (device, stream) -> slot
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  std::lock_guard<std::mutex> lock(mu);
-  auto pit = pool.find(dev);
-  if (pit == pool.end()) {
-    void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_topk_arrive)) != hipSuccess || p == nullptr) {
-      (void)hipGetLastError();
-      return nullptr;
-    }
-    pit = pool.emplace(dev, reinterpret_cast<uint32_t*>(p)).first;
-  }
-  int& n = used[dev];
-  if (cs == hipStreamCaptureStatusNone) {
-    const auto it = eager.find({dev, st});
-    if (it != eager.end()) return pit->second + (size_t)it->second * kArriveRows;
-    if (n >= kArriveSlots) return nullptr;
-    eager.emplace(std::make_pair(dev, st), n);
-  } else if (n >= kArriveSlots) {
-    return nullptr;
-  }
-  return pit->second + (size_t)(n++) * kArriveRows;
 }
 
 extern "C" size_t mi355_dsa_decode_topk_workspace_size(int B, int max_kv, int k) {
