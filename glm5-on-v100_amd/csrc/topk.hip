@@ -446,9 +446,9 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
     rebuild = (total != (uint32_t)L);
   }
   // A rebuilding read 1 lists the keys of level-1 bin >= te, with te taken
-  // from the histogram of the first step so that about 1.5 k keys of a row
-  // with stationary scores qualify; past the first step it builds no
-  // histogram.  When at least k and at most cap keys were listed, the list
+  // from a histogram of every fourth key of the first step (elements 0 and
+  // 4 of each thread's eight) so that about 1.5 k keys of a row with
+  // stationary scores qualify; past the first step it builds no histogram.  When at least k and at most cap keys were listed, the list
   // holds every key of the bins from te up, so the threshold bin (>= te)
   // and its neighbours' counts come from a histogram of the list, and the
   // second read is skipped.  Otherwise a histogram read of the row follows
@@ -472,11 +472,13 @@ __global__ void __launch_bounds__(kTkThreads) __attribute__((amdgpu_waves_per_eu
     r1_load<V4>(row, 0, L, v);
     r1_load<V4>(row, kS0, L, w);  // past the row: re-reads its last group, unused
 #pragma unroll
-    for (int e = 0; e < kTk2U; e++)
+    for (int e = 0; e < kTk2U; e += 4)
       if (r1_pos<V4>(0, e) < L) atomicAdd(&sh.hist[mono_key(v[e]) >> 20], 1u);
     __syncthreads();
     {
-      const int S = min(L, kS0);
+      // sampled positions below L: 4t and 4t + 4096 (V4), t and t + 1024 (else)
+      const int S = V4 ? (min(L, kS0) + 3) / 4
+                       : min(L, kTkThreads) + min(max(L - 4 * kTkThreads, 0), kTkThreads);
       uint64_t tgt = (3ull * (uint64_t)K * S + 2ull * L - 1) / (2ull * L);
       tgt = tgt < 1 ? 1 : (tgt > (uint64_t)S ? (uint64_t)S : tgt);
       int Te;
