@@ -218,6 +218,43 @@ def test_decode_topk_one_launch_graph_replays(pkg, dev):
     del graph
 
 
+MANY_ROW_CASES = [
+    ("randn", 600, 8192, "causal"),     # lengths crossing k (rows <= k select everything)
+    ("randn", 1024, 20001, "full"),     # row stride not a multiple of 4: 4-byte loads
+    ("ties", 530, 6000, "full"),
+    ("equal", 512, 5000, "full"),       # one level-1 bin: ties down to the last digit
+    ("equal", 520, 20000, "full"),      # every list overflows: rows selected again
+    ("alternate", 700, 12000, "full"),  # neighbouring rows 100x apart in scale
+    ("rising", 600, 12000, "full"),
+    ("mixed", 777, 9000, "ragged"),     # lengths from 0 to the width
+]
+
+
+@pytest.mark.parametrize("case", MANY_ROW_CASES, ids=[f"{c[0]}-{c[1]}x{c[2]}-{c[3]}" for c in MANY_ROW_CASES])
+def test_persistent_topk_many_rows(ops, dev, case):
+    """Calls of more rows than CUs, several workgroups per CU: every branch
+    (candidate list within bounds, list overflow re-selected by the whole
+    workgroup, ties, rows of length <= k, ragged lengths) gives the exact
+    selection."""
+    kind, R, W, lens = case
+    g = torch.Generator().manual_seed(R * 3 + W)
+    if kind == "alternate":
+        s = torch.randn(R, W, generator=g) * (1.0 + 99.0 * (torch.arange(R) % 2)).view(R, 1)
+    else:
+        s = scores(kind, R, W, g)
+    if lens == "causal":
+        seq = torch.clamp(torch.arange(R) + (W - R + 1), min=1)
+    elif lens == "full":
+        seq = torch.full((R,), W)
+    else:
+        seq = torch.randint(0, W + 1, (R,), generator=g)
+    seq = seq.to(torch.int32)
+    out = torch.full((R, 2048), 77, dtype=torch.int32, device=dev)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+    ops.persistent_topk(s.to(dev), seq.view(R, 1).to(dev), out, ws, 2048, W)
+    assert torch.equal(out.cpu(), cref.topk_rows(s, seq, 2048))
+
+
 def test_decode_topk_many_rows_bad_hist(ops, dev):
     """More rows than the two-kernel path takes, with histograms that do not
     count the rows: each row's histogram is rebuilt from its scores."""
