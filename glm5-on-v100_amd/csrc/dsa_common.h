@@ -324,5 +324,16 @@ __device__ __forceinline__ void dma16(const void* gptr, const void* lds) {
   const uint32_t off = (uint32_t)(uintptr_t)lds;
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(off) : "memory");
 }
+// dma16 of the 16 bytes at gptr + IMM (IMM in the instruction's offset
+// field, so that several loads share one address register).  The offset
+// field applies to the LDS address too, so M0 carries lds - IMM (the caller
+// passes lds >= IMM).
+template <int IMM>
+__device__ __forceinline__ void dma16_at(const void* gptr, const void* lds) {
+  static_assert(IMM >= 0 && IMM < 4096, "offset field");
+  const uint32_t off = (uint32_t)(uintptr_t)lds - (uint32_t)IMM;
+  asm volatile("global_load_lds_dwordx4 %0, off offset:%2" ::"v"(gptr), "{m0}"(off), "n"(IMM)
+               : "memory");
+}
 
 }  // namespace mi355dsa

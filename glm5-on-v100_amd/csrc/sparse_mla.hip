@@ -1286,6 +1286,456 @@ __global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaP
 }
 
 // ---------------------------------------------------------------------------
+// fp8_ds_mla 64-head attention with wave roles: the arithmetic of
+// sparse_mla_prefill_fp8_kernel (every S partial, softmax sum, P value and O
+// accumulation in the same order), laid out so that MFMA work and VALU work
+// run in different waves of each SIMD.
+//
+// Workgroup = one token x 64 heads (x one key split), 12 waves, three per
+// SIMD (<= 168 VGPRs each):
+//   * waves 0-3, QK: wave qd holds Q of all 64 heads for NoPE dims
+//     [128 qd, +128) (one fp8 scale tile) and RoPE dims [512 + 16 qd, +16),
+//     and computes that dim part of S^T for all 32 keys of a tile.
+//   * waves 4-7, PV: wave pw owns O^T of value dims [128 pw, +128) (scale
+//     tile pw) for all 64 heads.  After its PV of a tile it refills that
+//     tile's slot with its own dim quarter of the tile three ahead.
+//   * waves 8-11, softmax: thread t owns head t / 4 and keys 8 (t % 4) .. +7
+//     of a tile; these waves also fetch each tile's scales and RoPE dims.
+// A tile slot holds, for its 32 keys: four NoPE blocks (one per dim quarter),
+// the four scales (16 B per key) and the RoPE dims.  The NoPE and RoPE blocks
+// are chunk-major: 16-B chunk j of key r at 512 j + 16 r, so the QK operand
+// reads and the PV transpose reads of 16 keys are contiguous (free of LDS
+// bank conflicts) and every DMA instruction fills 1 KB (two chunks of all 32
+// keys).
+// A 4-slot ring, one S partial buffer and two P buffers.  Each role runs its
+// own copy of the tile loop (Q and O stay in registers only in the waves that
+// use them); all copies take the same barriers:
+//   iteration s (s = -1 .. ntiles - 1):
+//     phase 1: QK(s+1) into registers | softmax(s) -> P[s & 1], DMA of tile
+//              s+3's scales and RoPE | PV(s-1), then DMA of tile s+3's dim
+//              quarter into the same slot
+//     barrier
+//     phase 2: QK(s+1) partials -> LDS | DMA waves wait for tile s+2
+//     barrier
+//   then PV(ntiles - 1) and a barrier.
+// ---------------------------------------------------------------------------
+constexpr int kWsWaves = 12;
+constexpr int kWsThreads = 64 * kWsWaves;
+constexpr int kWsRing = 4;
+constexpr int kWsSubBytes = kPfTileKeys * 128;                // one NoPE dim quarter
+constexpr int kWsScaleOff = 4 * kWsSubBytes;                   // 16384
+constexpr int kWsRopeOff = kWsScaleOff + kPfTileKeys * 16;     // 16896
+constexpr int kWsSlotBytes = kWsRopeOff + kPfTileKeys * 128;   // 20992
+static_assert(kWsSlotBytes == kPfTileKeys * kDsmlaRowBytes, "a slot holds whole rows");
+
+struct WsSmem {
+  uint8_t ring[kWsRing][kWsSlotBytes];
+  int32_t rows[kSegKeys];
+  float sp[4][64 * kP3SPitch];   // [dim quarter][head][key]
+  f16 pt[2][4][64 * kP3PPitch];  // [tile parity][scale tile][head][key]: fp16(p * scale)
+  f32x4 alpha[2][16];            // [tile parity][head % 16][head / 16]
+  f32x4 lsum[16];
+  int rescale[2];
+};
+
+// The PV wave pw's part of a tile's DMA: NoPE bytes [128 pw, +128) of the 32
+// keys, four instructions; lane l of instruction i fetches chunk 2 i + l / 32
+// of key l % 32.  Masked keys (row < 0) read zeros.
+__device__ __forceinline__ void ws_dma_nope(const uint8_t* __restrict__ kv, const int32_t* trows,
+                                            uint8_t* slot, int pw, int lane) {
+  const int row = trows[lane & 31];
+  const uint8_t* src = (row >= 0 ? kv + (int64_t)row * kDsmlaRowBytes : kZeroRow) + 128 * pw +
+                       16 * (lane >> 5);
+  uint8_t* dst = slot + pw * kWsSubBytes;
+  dma16_at<0>(src, dst);
+  dma16_at<32>(src, dst + 1024);
+  dma16_at<64>(src, dst + 2048);
+  dma16_at<96>(src, dst + 3072);
+}
+
+// The softmax wave sw's part: RoPE chunks 2 sw and 2 sw + 1 of the 32 keys
+// (one instruction), and for wave 0 the 16 scale bytes of every key (lanes
+// 0-31).  Per tile wave 0 issues 2 DMA instructions, waves 1-3 issue 1.
+__device__ __forceinline__ void ws_dma_tail(const uint8_t* __restrict__ kv, const int32_t* trows,
+                                            uint8_t* slot, int sw, int lane) {
+  const int row = trows[lane & 31];
+  const uint8_t* base = row >= 0 ? kv + (int64_t)row * kDsmlaRowBytes : kZeroRow;
+  dma16(base + (kDsmlaRowBytes - 128) + 16 * (2 * sw + (lane >> 5)), slot + kWsRopeOff + 1024 * sw);
+  if (sw == 0 && lane < kPfTileKeys) dma16(base + 512, slot + kWsScaleOff);
+}
+
+// vmcnt waits of the DMA waves: at most one tile's DMAs of this wave still in
+// flight (one = true), or none.
+__device__ __forceinline__ void ws_wait_pv(bool one) {
+  if (one) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+__device__ __forceinline__ void ws_wait_sm(bool one, int sw) {
+  if (!one) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if (sw == 0) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+}
+
+// The workgroup's token / head base / split and key range.
+struct WsCtx {
+  int b, hbase, split, seq_len, k_lo, k_hi;
+};
+
+__device__ __forceinline__ WsCtx ws_ctx(const MlaParams& p) {
+  WsCtx x;
+  const int nx = gridDim.x, bid = blockIdx.x;
+  const int xcd = bid & 7, j = bid >> 3;
+  const int per = nx >> 3, rem = nx & 7;
+  x.b = xcd * per + (xcd < rem ? xcd : rem) + j;  // consecutive tokens share an XCD
+  x.hbase = blockIdx.y * 64;
+  x.split = blockIdx.z;
+  x.seq_len = p.seq_lens[x.b];
+  const int kps = ((p.topk + p.n_splits - 1) / p.n_splits + kPfTileKeys - 1) / kPfTileKeys *
+                  kPfTileKeys;
+  x.k_lo = min(x.split * kps, p.topk);
+  x.k_hi = min(x.k_lo + kps, p.topk);
+  return x;
+}
+
+// idx -> block table -> row of the segment's keys, by all 768 threads, then
+// a barrier.  The caller's previous barrier ended every use of rows and ring.
+__device__ __forceinline__ void ws_resolve(const MlaParams& p, const WsCtx& x, int seg_lo,
+                                           int nkeys, int ntiles, int32_t* rows) {
+  for (int base = 0; base < ntiles * kPfTileKeys; base += kWsThreads * kResU) {
+    int pos[kResU], pg[kResU], blk[kResU];
+#pragma unroll
+    for (int u = 0; u < kResU; u++) {
+      const int j = base + u * kWsThreads + (int)threadIdx.x;
+      pos[u] = (j < nkeys) ? p.idx[(int64_t)x.b * p.topk + seg_lo + j] : -1;
+    }
+    resolve_bt<kWsThreads>(p, x.b, x.seq_len, pos, pg, blk);
+#pragma unroll
+    for (int u = 0; u < kResU; u++) {
+      const int j = base + u * kWsThreads + (int)threadIdx.x;
+      if (j < ntiles * kPfTileKeys) {
+        const int64_t row = (int64_t)blk[u] * p.page_size + (pos[u] - pg[u] * p.page_size);
+        const bool in_range = pos[u] >= 0 && pos[u] < x.seq_len && pg[u] < p.max_blocks;
+        rows[j] = (blk[u] < 0 || row >= p.n_kv_rows)
+                      ? ((in_range && p.zero_unresolved) ? -2 : -1) : (int32_t)row;
+      }
+    }
+  }
+  lds_barrier();
+}
+
+// ---- QK waves ----
+__device__ __forceinline__ void ws_qk_role(const MlaParams& p, const WsCtx& x, WsSmem& sh) {
+  const int lane = threadIdx.x & 63, qd = threadIdx.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  // NoPE step s: lane (head c of group hg, g) holds dims 128 qd + 32 g + 8 s .. +8;
+  // RoPE: dims 512 + 16 qd + 4 g .. +4 (Q scaled in fp16)
+  f16x8 qn[4][4];
+  f16x4 qr[4];
+  {
+    const f16 sc = (f16)p.scale_h;
+    const f16x8 sc8 = {sc, sc, sc, sc, sc, sc, sc, sc};
+    const f16x4 sc4 = {sc, sc, sc, sc};
+#pragma unroll
+    for (int hg = 0; hg < 4; hg++) {
+      const int h = x.hbase + 16 * hg + c;
+      const f16* qrow = p.q + ((int64_t)x.b * p.n_head + (h < p.n_head ? h : 0)) * kLatentDim;
+#pragma unroll
+      for (int s = 0; s < 4; s++)
+        qn[hg][s] = *reinterpret_cast<const f16x8*>(qrow + 128 * qd + 32 * g + 8 * s) * sc8;
+      qr[hg] = *reinterpret_cast<const f16x4*>(qrow + 512 + 16 * qd + 4 * g) * sc4;
+    }
+  }
+  // S^T partial of key block kb of the tile in slot cb: keys 16 kb + 4 g + r x head 16 hg + c
+  auto qk = [&](const uint8_t* cb, int kb, f32x4 (&v)[4]) {
+    const int r = 16 * kb + c;
+    const uint8_t* krow = cb + qd * kWsSubBytes + 16 * r;
+    const u32x4 k0 = *reinterpret_cast<const u32x4*>(krow + 512 * (2 * g));
+    const u32x4 k1 = *reinterpret_cast<const u32x4*>(krow + 512 * (2 * g + 1));
+    const f16x4 kr = *reinterpret_cast<const f16x4*>(cb + kWsRopeOff + 512 * (2 * qd + (g >> 1)) +
+                                                     16 * r + 8 * (g & 1));
+    float ksc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      ksc[i] = *reinterpret_cast<const float*>(cb + kWsScaleOff + (16 * kb + 4 * g + i) * 16 + 4 * qd);
+    f32x4 accn[4], accr[4];
+#pragma unroll
+    for (int hg = 0; hg < 4; hg++) {
+      accn[hg] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      accr[hg] = mfma16x16x16(kr, qr[hg], (f32x4){0.f, 0.f, 0.f, 0.f});
+    }
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const uint32_t d0 = s < 2 ? k0[2 * s] : k1[2 * (s - 2)];
+      const uint32_t d1 = s < 2 ? k0[2 * s + 1] : k1[2 * (s - 2) + 1];
+      const f16x4 a0 = e4m3x4_to_f16x4(d0), a1 = e4m3x4_to_f16x4(d1);
+      const f16x8 kf = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+#pragma unroll
+      for (int hg = 0; hg < 4; hg++) accn[hg] = mfma16x16x32(kf, qn[hg][s], accn[hg]);
+    }
+#pragma unroll
+    for (int hg = 0; hg < 4; hg++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[hg][i] = accr[hg][i] + ksc[i] * accn[hg][i];
+  };
+  for (int seg_lo = x.k_lo; seg_lo < x.k_hi; seg_lo += kSegKeys) {
+    const int nkeys = min(x.k_hi - seg_lo, kSegKeys);
+    const int ntiles = (nkeys + kPfTileKeys - 1) / kPfTileKeys;
+    ws_resolve(p, x, seg_lo, nkeys, ntiles, sh.rows);
+    lds_barrier();  // tile 0 landed
+    for (int s = -1; s < ntiles; s++) {
+      f32x4 v[2][4];
+      const bool work = s + 1 < ntiles;
+      if (work) {
+        const uint8_t* cb = sh.ring[(s + 1) % kWsRing];
+        qk(cb, 0, v[0]);
+        qk(cb, 1, v[1]);
+      }
+      lds_barrier();  // softmax(s) has read sp
+      if (work) {
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+          for (int hg = 0; hg < 4; hg++)
+            *reinterpret_cast<f32x4*>(&sh.sp[qd][sp_at(16 * hg + c, 16 * kb + 4 * g)]) = v[kb][hg];
+      }
+      lds_barrier();
+    }
+    lds_barrier();  // PV(ntiles - 1)
+  }
+  lds_barrier();  // l of every head in sh.lsum
+}
+
+// ---- PV waves ----
+__device__ __forceinline__ void ws_pv_role(const MlaParams& p, const WsCtx& x, WsSmem& sh) {
+  const int lane = threadIdx.x & 63, pw = (threadIdx.x >> 6) - 4;
+  const int c = lane & 15, g = lane >> 4;
+  const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
+  // PV and softmax waves issue ahead of the QK waves, which have the most slack
+  __builtin_amdgcn_s_setprio(2);
+  f32x4 oacc[8][4];  // [dim tile][head group]: O^T of dims 128 pw + 16 t + 4 g + r, head 16 hg + c
+#pragma unroll
+  for (int t = 0; t < 8; t++)
+#pragma unroll
+    for (int hg = 0; hg < 4; hg++) oacc[t][hg] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  auto pv = [&](int tile) {
+    const uint8_t* cb = sh.ring[tile % kWsRing];
+    if (sh.rescale[tile & 1] != 0) {
+      const f32x4 al = sh.alpha[tile & 1][c];
+#pragma unroll
+      for (int t = 0; t < 8; t++)
+#pragma unroll
+        for (int hg = 0; hg < 4; hg++) oacc[t][hg] *= al[hg];
+    }
+    f16x8 pb[4];
+#pragma unroll
+    for (int hg = 0; hg < 4; hg++)
+      pb[hg] = *reinterpret_cast<const f16x8*>(&sh.pt[tile & 1][pw][pt_at(16 * hg + c, 8 * g)]);
+    // transpose source: lane i of a 16-lane group points at key 8g + i/2,
+    // dims 128 pw + 16 t + 8 (i % 2) .. +8; lane j receives keys 8g .. 8g+7
+    // at dim 128 pw + 16 t + j
+    const uint8_t* vrow = cb + pw * kWsSubBytes + 16 * (8 * g + (c >> 1)) + 8 * (c & 1);
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const s32x2 vt = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_s32x2*)(vrow + 512 * t));
+      const f16x4 lo = e4m3x4_to_f16x4((uint32_t)vt[0]);
+      const f16x4 hi = e4m3x4_to_f16x4((uint32_t)vt[1]);
+      const f16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+      for (int hg = 0; hg < 4; hg++) oacc[t][hg] = mfma16x16x32(av, pb[hg], oacc[t][hg]);
+    }
+  };
+  for (int seg_lo = x.k_lo; seg_lo < x.k_hi; seg_lo += kSegKeys) {
+    const int nkeys = min(x.k_hi - seg_lo, kSegKeys);
+    const int ntiles = (nkeys + kPfTileKeys - 1) / kPfTileKeys;
+    ws_resolve(p, x, seg_lo, nkeys, ntiles, sh.rows);
+    ws_dma_nope(kv, sh.rows, sh.ring[0], pw, lane);
+    if (ntiles > 1) ws_dma_nope(kv, sh.rows + kPfTileKeys, sh.ring[1], pw, lane);
+    ws_wait_pv(ntiles > 1);
+    lds_barrier();  // tile 0 landed
+    for (int s = -1; s < ntiles; s++) {
+      const bool dma = s + 3 < ntiles;
+      if (s >= 1) pv(s - 1);
+      if (dma) {
+        // the slot of tile s - 1: this wave's own PV reads of it have returned
+        // (and nothing of the refill is scheduled into the PV above, where
+        // the O accumulators hold the registers)
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        ws_dma_nope(kv, sh.rows + (s + 3) * kPfTileKeys, sh.ring[(s + 3) % kWsRing], pw, lane);
+      }
+      lds_barrier();
+      ws_wait_pv(dma);  // tile s + 2 landed (this wave's part)
+      lds_barrier();
+    }
+    pv(ntiles - 1);
+    lds_barrier();  // the ring and rows are free for the next segment
+  }
+  lds_barrier();  // l of every head in sh.lsum
+  // ---- outputs: o = O / l, or the split's partial ----
+  const f32x4 L = sh.lsum[c];
+#pragma unroll
+  for (int hg = 0; hg < 4; hg++) {
+    const int h = x.hbase + 16 * hg + c;
+    if (h >= p.n_head) continue;
+    const int64_t bh = (int64_t)x.b * p.n_head + h;
+    const float inv = (L[hg] > 0.f) ? 1.f / L[hg] : 0.f;
+    if (p.n_splits == 1) {
+      f16* orow = p.o + bh * kValueDim + 128 * pw;
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        f16x4 v;
+#pragma unroll
+        for (int r = 0; r < 4; r++) v[r] = (f16)(oacc[t][hg][r] * inv);
+        *reinterpret_cast<f16x4*>(orow + 16 * t + 4 * g) = v;
+      }
+    } else {
+      // the partial layout of sparse_mla_prefill_fp8_kernel: per 64-dim chunk j,
+      // lane g's 16 values (dims 64 j + 16 t + 4 g + r, t < 4) at 64 j + 16 g
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        f16x8 o8[2];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            o8[t >> 1][4 * (t & 1) + r] = (f16)(oacc[4 * j + t][hg][r] * inv);
+        u32x4* dst = reinterpret_cast<u32x4*>(p.part_o + (bh * p.n_splits + x.split) * kValueDim +
+                                              64 * (2 * pw + j) + 16 * g);
+        dst[0] = __builtin_bit_cast(u32x4, o8[0]);
+        dst[1] = __builtin_bit_cast(u32x4, o8[1]);
+      }
+    }
+  }
+}
+
+// ---- softmax waves ----
+__device__ __forceinline__ void ws_sm_role(const MlaParams& p, const WsCtx& x, WsSmem& sh) {
+  const int lane = threadIdx.x & 63, sw = (threadIdx.x >> 6) - 8;
+  const int ts = threadIdx.x - 512;
+  const int hh = ts >> 2, kq = ts & 3;  // head, keys 8 kq .. +7
+  const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
+  float m_run = -1e30f, l_run = 0.f;  // identical in the 4 threads of a head
+  // these waves and the PV waves issue ahead of the QK waves (measured: QK
+  // lowest gives 25.0 ms on the 64k prefill against 27-29 ms otherwise)
+  __builtin_amdgcn_s_setprio(2);
+  // softmax of tile `tile` from sh.sp -> sh.pt[tile & 1], alpha.  Its LDS reads
+  // (S partials, row codes, key scales) are all issued before any is used.
+  auto softmax = [&](int tile) {
+    const uint8_t* cb = sh.ring[tile % kWsRing];
+    const int32_t* trows = sh.rows + tile * kPfTileKeys;
+    f32x4 sq[4][2];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+      for (int hf = 0; hf < 2; hf++)
+        sq[q][hf] = *reinterpret_cast<const f32x4*>(&sh.sp[q][sp_at(hh, 8 * kq + 4 * hf)]);
+    const int4 vr0 = *reinterpret_cast<const int4*>(trows + 8 * kq);
+    const int4 vr1 = *reinterpret_cast<const int4*>(trows + 8 * kq + 4);
+    f32x4 ks[8];  // the four tile scales of each key
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      ks[k] = *reinterpret_cast<const f32x4*>(cb + kWsScaleOff + (8 * kq + k) * 16);
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 s4[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+      s4[hf] = sq[0][hf];
+#pragma unroll
+      for (int q = 1; q < 4; q++) s4[hf] += sq[q][hf];
+    }
+    const int vv[8] = {vr0.x, vr0.y, vr0.z, vr0.w, vr1.x, vr1.y, vr1.z, vr1.w};
+    float mt = -1e30f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      s4[k >> 2][k & 3] = vv[k] != -1 ? s4[k >> 2][k & 3] : -INFINITY;  // -2: zero row, a valid key
+      mt = fmaxf(mt, s4[k >> 2][k & 3]);
+    }
+    mt = fmaxf(mt, dppf<0xB1>(mt));  // quad_perm [1,0,3,2]
+    mt = fmaxf(mt, dppf<0x4E>(mt));  // quad_perm [2,3,0,1]
+    float alpha = 1.f;
+    if (mt > m_run + kPfLazyMax) {
+      const float m_new = fmaxf(m_run, mt);
+      alpha = __expf(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+      sh.rescale[tile & 1] = 1;
+    }
+    if (kq == 0) reinterpret_cast<float*>(&sh.alpha[tile & 1][hh & 15])[hh >> 4] = alpha;
+    float pr[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const float sv = s4[k >> 2][k & 3];
+      pr[k] = (sv > -INFINITY) ? __expf(sv - m_run) : 0.f;
+    }
+    // sum in the order of the 8-thread reduction over 4-key groups: each
+    // group sequentially, the two groups of a thread, then across threads
+    float la = 0.f, lb = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) la += pr[k];
+#pragma unroll
+    for (int k = 4; k < 8; k++) lb += pr[k];
+    float ls = la + lb;
+    ls += dppf<0xB1>(ls);
+    ls += dppf<0x4E>(ls);
+    l_run += ls;
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+      f16x8 ph;
+#pragma unroll
+      for (int k = 0; k < 8; k++) ph[k] = (f16)(pr[k] * ks[k][st]);
+      *reinterpret_cast<f16x8*>(&sh.pt[tile & 1][st][pt_at(hh, 8 * kq)]) = ph;
+    }
+  };
+  for (int seg_lo = x.k_lo; seg_lo < x.k_hi; seg_lo += kSegKeys) {
+    const int nkeys = min(x.k_hi - seg_lo, kSegKeys);
+    const int ntiles = (nkeys + kPfTileKeys - 1) / kPfTileKeys;
+    ws_resolve(p, x, seg_lo, nkeys, ntiles, sh.rows);
+    ws_dma_tail(kv, sh.rows, sh.ring[0], sw, lane);
+    if (ntiles > 1) ws_dma_tail(kv, sh.rows + kPfTileKeys, sh.ring[1], sw, lane);
+    ws_wait_sm(ntiles > 1, sw);
+    lds_barrier();  // tile 0 landed
+    for (int s = -1; s < ntiles; s++) {
+      const bool dma = s + 3 < ntiles;
+      // the scales and RoPE of the slot of tile s - 1 were last read by
+      // softmax(s - 1) and QK(s - 1), both before the previous barrier
+      if (dma) ws_dma_tail(kv, sh.rows + (s + 3) * kPfTileKeys, sh.ring[(s + 3) % kWsRing], sw, lane);
+      if (s >= 0) softmax(s);
+      lds_barrier();  // P(s) written; PV(s - 1) done
+      if (ts == 0) sh.rescale[(s + 1) & 1] = 0;  // PV(s - 1) read it; softmax(s + 1) sets it
+      ws_wait_sm(dma, sw);  // tile s + 2 landed (this wave's part)
+      lds_barrier();
+    }
+    lds_barrier();  // PV(ntiles - 1)
+  }
+  // ---- l and lse ----
+  if (kq == 0) {
+    reinterpret_cast<float*>(&sh.lsum[hh & 15])[hh >> 4] = l_run;
+    const int h = x.hbase + hh;
+    if (h < p.n_head) {
+      const int64_t bh = (int64_t)x.b * p.n_head + h;
+      if (p.n_splits == 1) {
+        p.lse[bh] = (l_run > 0.f) ? (m_run + logf(l_run)) : p.empty_lse;
+      } else {
+        const int64_t ps = bh * p.n_splits + x.split;
+        p.part_ml[ps * 2 + 0] = m_run;
+        p.part_ml[ps * 2 + 1] = l_run;
+      }
+    }
+  }
+  lds_barrier();  // l of every head in sh.lsum
+}
+
+__global__ void __launch_bounds__(kWsThreads) sparse_mla_prefill_fp8_ws_kernel(MlaParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  WsSmem& sh = *reinterpret_cast<WsSmem*>(smem_raw);
+  const WsCtx x = ws_ctx(p);
+  const int w = threadIdx.x >> 6;
+  if (w < 4) ws_qk_role(p, x, sh);
+  else if (w < 8) ws_pv_role(p, x, sh);
+  else ws_sm_role(p, x, sh);
+}
+
+// ---------------------------------------------------------------------------
 // fp16-row attention over 64 heads, software-pipelined over 32-key tiles:
 // the fp16 (576-half) latent cache in the prefill configuration, and dense
 // decode (idx == nullptr) split over the context.
@@ -1971,10 +2421,10 @@ static int mla_decode_impl(
   if (plan.kind == kPipelined) {
     const dim3 pgrid(B, (n_head + 63) / 64, S);
     if (kv_fp8) {
-      rc = reserve_lds(reinterpret_cast<const void*>(sparse_mla_prefill_fp8_kernel),
-                       sizeof(P3Smem), "sparse_mla_prefill_fp8");
+      rc = reserve_lds(reinterpret_cast<const void*>(sparse_mla_prefill_fp8_ws_kernel),
+                       sizeof(WsSmem), "sparse_mla_prefill_fp8");
       if (rc) return rc;
-      sparse_mla_prefill_fp8_kernel<<<pgrid, kPfThreads, sizeof(P3Smem), st>>>(prm);
+      sparse_mla_prefill_fp8_ws_kernel<<<pgrid, kWsThreads, sizeof(WsSmem), st>>>(prm);
       rc = check_launch("sparse_mla_decode");
     } else {
       rc = launch_attn_f16(prm, pgrid, st);
