@@ -1336,7 +1336,9 @@ struct WsSmem {
   f32x4 alpha[2][16];            // [tile parity][head % 16][head / 16]
   f32x4 lsum[16];
   int rescale[2];
+  int tmask[kSegKeys / kPfTileKeys];  // tile of the segment holds a masked key (row -1)
 };
+static_assert(sizeof(WsSmem) <= 160 * 1024, "one workgroup per CU");
 
 // The PV wave pw's part of a tile's DMA: NoPE bytes [128 pw, +128) of the 32
 // keys, four instructions; lane l of instruction i fetches chunk 2 i + l / 32
@@ -1614,6 +1616,7 @@ __device__ __forceinline__ void ws_sm_role(const MlaParams& p, const WsCtx& x, W
   const int ts = threadIdx.x - 512;
   const int hh = ts >> 2, kq = ts & 3;  // head, keys 8 kq .. +7
   const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
+  constexpr float kLog2e = 1.4426950408889634f;
   float m_run = -1e30f, l_run = 0.f;  // identical in the 4 threads of a head
   // these waves and the PV waves issue ahead of the QK waves (measured: QK
   // lowest gives 25.0 ms on the 64k prefill against 27-29 ms otherwise)
@@ -1635,6 +1638,7 @@ __device__ __forceinline__ void ws_sm_role(const MlaParams& p, const WsCtx& x, W
 #pragma unroll
     for (int k = 0; k < 8; k++)
       ks[k] = *reinterpret_cast<const f32x4*>(cb + kWsScaleOff + (8 * kq + k) * 16);
+    const int masked = sh.tmask[tile];
     __builtin_amdgcn_sched_barrier(0);
     f32x4 s4[2];
 #pragma unroll
@@ -1643,13 +1647,15 @@ __device__ __forceinline__ void ws_sm_role(const MlaParams& p, const WsCtx& x, W
 #pragma unroll
       for (int q = 1; q < 4; q++) s4[hf] += sq[q][hf];
     }
-    const int vv[8] = {vr0.x, vr0.y, vr0.z, vr0.w, vr1.x, vr1.y, vr1.z, vr1.w};
+    if (masked) {  // wave-uniform: most tiles hold no masked key
+      const int vv[8] = {vr0.x, vr0.y, vr0.z, vr0.w, vr1.x, vr1.y, vr1.z, vr1.w};
+#pragma unroll
+      for (int k = 0; k < 8; k++)  // -2: zero row, a valid key
+        s4[k >> 2][k & 3] = vv[k] != -1 ? s4[k >> 2][k & 3] : -INFINITY;
+    }
     float mt = -1e30f;
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      s4[k >> 2][k & 3] = vv[k] != -1 ? s4[k >> 2][k & 3] : -INFINITY;  // -2: zero row, a valid key
-      mt = fmaxf(mt, s4[k >> 2][k & 3]);
-    }
+    for (int k = 0; k < 8; k++) mt = fmaxf(mt, s4[k >> 2][k & 3]);
     mt = fmaxf(mt, dppf<0xB1>(mt));  // quad_perm [1,0,3,2]
     mt = fmaxf(mt, dppf<0x4E>(mt));  // quad_perm [2,3,0,1]
     float alpha = 1.f;
@@ -1661,12 +1667,13 @@ __device__ __forceinline__ void ws_sm_role(const MlaParams& p, const WsCtx& x, W
       sh.rescale[tile & 1] = 1;
     }
     if (kq == 0) reinterpret_cast<float*>(&sh.alpha[tile & 1][hh & 15])[hh >> 4] = alpha;
+    // p = 2^(s log2 e - m log2 e): m_run is finite (it starts at -1e30), so a
+    // masked key (s = -inf) gives exactly 0
+    const float ml = m_run * kLog2e;
     float pr[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const float sv = s4[k >> 2][k & 3];
-      pr[k] = (sv > -INFINITY) ? __expf(sv - m_run) : 0.f;
-    }
+    for (int k = 0; k < 8; k++)
+      pr[k] = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[k >> 2][k & 3], kLog2e, -ml));
     // sum in the order of the 8-thread reduction over 4-key groups: each
     // group sequentially, the two groups of a thread, then across threads
     float la = 0.f, lb = 0.f;
@@ -1690,6 +1697,19 @@ __device__ __forceinline__ void ws_sm_role(const MlaParams& p, const WsCtx& x, W
     const int nkeys = min(x.k_hi - seg_lo, kSegKeys);
     const int ntiles = (nkeys + kPfTileKeys - 1) / kPfTileKeys;
     ws_resolve(p, x, seg_lo, nkeys, ntiles, sh.rows);
+    {  // which tiles hold a masked key: thread ts checks rows 8 ts .. +7 (tile ts / 4)
+      const bool in = 8 * ts < ntiles * kPfTileKeys;
+      int m = 0;
+      if (in) {
+        const int4 a = *reinterpret_cast<const int4*>(sh.rows + 8 * ts);
+        const int4 b = *reinterpret_cast<const int4*>(sh.rows + 8 * ts + 4);
+        m = (a.x == -1) | (a.y == -1) | (a.z == -1) | (a.w == -1) | (b.x == -1) | (b.y == -1) |
+            (b.z == -1) | (b.w == -1);
+      }
+      const unsigned long long bal = __ballot(m);
+      if (in && (ts & 3) == 0) sh.tmask[ts >> 2] = ((bal >> (lane & ~3)) & 0xfull) != 0;
+    }
+    // (the softmax waves read the flags after the barrier below)
     ws_dma_tail(kv, sh.rows, sh.ring[0], sw, lane);
     if (ntiles > 1) ws_dma_tail(kv, sh.rows + kPfTileKeys, sh.ring[1], sw, lane);
     ws_wait_sm(ntiles > 1, sw);
