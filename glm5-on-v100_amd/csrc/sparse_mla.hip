@@ -907,11 +907,9 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
 }
 
 // ---------------------------------------------------------------------------
-// fp8_ds_mla prefill: shared constants and the LDS-DMA tile gather.
-// 32-key tiles of raw 656-byte rows land in LDS slots by
-// global_load_lds_dwordx4 (piece q of a tile = key q / 41, 16-byte chunk
-// q % 41; padding pieces read a static zero row).  The running softmax max
-// is lazy: O and l are rescaled only when a head's tile max exceeds the
+// 64-head attention kernels (fp8_ds_mla and fp16 latent rows): shared
+// constants.  Keys stream through LDS in 32-key tiles.  The running softmax
+// max is lazy: O and l are rescaled only when a head's tile max exceeds the
 // running max by more than kPfLazyMax, so p = exp(s - m) <= e^8 (well inside
 // fp16) and rescales are rare; o = O / l and lse = m + ln l are unchanged by
 // the choice of m.
@@ -919,58 +917,9 @@ __global__ void __launch_bounds__(kDmaThreads) sparse_mla_decode_dma_kernel(MlaP
 constexpr int kPfWaves = 8;
 constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfTileKeys = 32;
-constexpr int kPfPieces = kPfTileKeys * (kDsmlaRowBytes / 16);          // 1312
-constexpr int kPfRounds = (kPfPieces + kPfThreads - 1) / kPfThreads;    // 3 LDS-DMA ops per thread
-constexpr int kPfSlotBytes = kPfRounds * kPfThreads * 16;
 constexpr float kPfLazyMax = 8.0f;
 
-// LDS-DMA gather of one 32-key tile (rows[0..32), -1 = masked) into a slot.
-__device__ __forceinline__ void pf_dma_tile(const uint8_t* __restrict__ kv, const int32_t* rows,
-                                            uint8_t* slot) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  int row[kPfRounds];
-#pragma unroll
-  for (int u = 0; u < kPfRounds; u++) {
-    const int q = kPfThreads * u + 64 * wave + lane;
-    const int r = q / 41;
-    row[u] = rows[r < kPfTileKeys ? r : 0];
-  }
-#pragma unroll
-  for (int u = 0; u < kPfRounds; u++) {
-    const int q = kPfThreads * u + 64 * wave + lane;
-    const int r = q / 41, ch = q - r * 41;
-    const bool ok = q < kPfPieces && row[u] >= 0;
-    const uint8_t* src = ok ? kv + (int64_t)row[u] * kDsmlaRowBytes + 16 * ch
-                            : kZeroRow + 16 * (q < kPfPieces ? ch : 0);
-    dma16(src, slot + 16 * (kPfThreads * u + 64 * wave));
-  }
-}
-
-// ---------------------------------------------------------------------------
-// fp8_ds_mla prefill, software-pipelined over 32-key tiles.
-//
-// Workgroup = one token x 64 heads, 8 waves; tiles stream through a 3-slot
-// LDS ring by LDS-DMA.  Every e4m3 byte of a tile is converted to fp16 once
-// per workgroup:
-//   * QK: wave w = (key block kb = w & 1, scale tile qd = w >> 1) computes
-//     S^T for keys [16 kb, +16) x all 64 heads over NoPE dims [128 qd, +128)
-//     (one fp8 scale tile) and RoPE dims [512 + 16 qd, +16); each converted
-//     key fragment feeds 4 head-group MFMAs with Q of all 64 heads for those
-//     dims resident in registers.  The four dim partials meet in LDS and are
-//     summed in a fixed order.
-//   * softmax: thread t owns head t / 8 and keys 4 (t % 8) .. +3; online
-//     softmax with a lazy running max (rescale only when a tile max exceeds
-//     it by more than kPfLazyMax); reductions over the 8 threads of a head
-//     are DPP butterflies; P is stored in fp16 already multiplied by each
-//     key's four tile scales.
-//   * PV: wave w owns value dims [64 w, +64) for all 64 heads; each V^T
-//     fragment (8-key transpose read of raw e4m3) is converted once and
-//     feeds 4 head-group MFMAs.
-// Two barrier-separated phases per tile: X = {PV of tile i, QK of tile i+1}
-// (independent MFMA streams that hide each other's LDS latency), then
-// Y = {softmax of tile i+1, LDS-DMA of tile i+3, wait for tile i+2}.
-// ---------------------------------------------------------------------------
-constexpr int kP3Ring = 3;
+constexpr int kP3Ring = 3;  // tile slots of the fp16-row kernel
 // S partials and the P table: one unpadded row of 32 keys per head, the key
 // chunks (4 floats of S, 8 halves of P) permuted by an XOR with bits of the
 // head.  Measured with SQ_LDS_BANK_CONFLICT on gfx950, these orders make the
@@ -986,16 +935,6 @@ __device__ __forceinline__ int pt_at(int head, int key) {  // key % 4 == 0
   return head * kP3PPitch + ((((key >> 3) ^ (2 * ((head >> 3) & 1))) & 3) << 3) + (key & 4);
 }
 
-struct P3Smem {
-  uint8_t ring[kP3Ring][kPfSlotBytes];
-  int32_t rows[kSegKeys];
-  float sp[4][64 * kP3SPitch];  // [dim quarter][head][key]
-  f16 pt[4][64 * kP3PPitch];    // [scale tile][head][key]: fp16(p * scale)
-  f32x4 alpha[16];              // [head % 16][head / 16]: rescale factor for PV
-  f32x4 lsum[16];               // [head % 16][head / 16]: final l
-  int rescale[2];               // tile parity: some head's running max moved
-};
-
 // reductions over aligned groups of 8 lanes (the result is bitwise equal in
 // all 8 lanes: every step combines a value with its partner symmetrically)
 __device__ __forceinline__ float max8(float v) {
@@ -1009,287 +948,12 @@ __device__ __forceinline__ float sum8(float v) {
   return v + dppf<0x141>(v);
 }
 
-__device__ __forceinline__ void p3_wait(int k) {  // at most k tiles still in flight
-  if (k <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kPfRounds) : "memory");
-}
-static_assert(kP3Ring == 3, "p3_wait covers one tile in flight");
-
-__global__ void __launch_bounds__(kPfThreads) sparse_mla_prefill_fp8_kernel(MlaParams p) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  P3Smem& sh = *reinterpret_cast<P3Smem*>(smem_raw);
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int c = lane & 15, g = lane >> 4;
-  const int kb = w & 1, qd = w >> 1;  // QK role
-  // XCD-aware token order: consecutive tokens (overlapping top-k sets) share an XCD
-  int b;
-  {
-    const int nx = gridDim.x, bid = blockIdx.x;
-    const int xcd = bid & 7, j = bid >> 3;
-    const int per = nx >> 3, rem = nx & 7;
-    b = xcd * per + (xcd < rem ? xcd : rem) + j;
-  }
-  const int hbase = blockIdx.y * 64;
-  const int split = blockIdx.z;
-  const uint8_t* kv = reinterpret_cast<const uint8_t*>(p.kv);
-  const int seq_len = p.seq_lens[b];
-  // this workgroup's keys: split `split` of n_splits, whole 32-key tiles
-  const int kps = ((p.topk + p.n_splits - 1) / p.n_splits + kPfTileKeys - 1) / kPfTileKeys *
-                  kPfTileKeys;
-  const int k_lo = min(split * kps, p.topk);
-  const int k_hi = min(k_lo + kps, p.topk);
-
-  // ---- Q of all 64 heads for this wave's QK dims, scaled in fp16 ----
-  // NoPE step s: lane (head c of group hg, g) holds dims 128 qd + 32 g + 8 s .. +8
-  // RoPE: dims 512 + 16 qd + 4 g .. +4
-  f16x8 qn[4][4];
-  f16x4 qr[4];
-  {
-    const f16 sc = (f16)p.scale_h;
-    const f16x8 sc8 = {sc, sc, sc, sc, sc, sc, sc, sc};
-    const f16x4 sc4 = {sc, sc, sc, sc};
-#pragma unroll
-    for (int hg = 0; hg < 4; hg++) {
-      const int h = hbase + 16 * hg + c;
-      const f16* qrow = p.q + ((int64_t)b * p.n_head + (h < p.n_head ? h : 0)) * kLatentDim;
-#pragma unroll
-      for (int s = 0; s < 4; s++)
-        qn[hg][s] = *reinterpret_cast<const f16x8*>(qrow + 128 * qd + 32 * g + 8 * s) * sc8;
-      qr[hg] = *reinterpret_cast<const f16x4*>(qrow + 512 + 16 * qd + 4 * g) * sc4;
-    }
-  }
-
-  // softmax role: head sm_h, keys 4 sm_k .. +3 of a tile
-  const int sm_h = threadIdx.x >> 3, sm_k = threadIdx.x & 7;
-  float m_run = -1e30f, l_run = 0.f;  // identical in the 8 threads of a head
-
-  f32x4 oacc[4][4];  // [dim tile][head group]: O^T of dims 64 w + 16 t + ..
-#pragma unroll
-  for (int t = 0; t < 4; t++)
-#pragma unroll
-    for (int hg = 0; hg < 4; hg++) oacc[t][hg] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  const int st_pv = w >> 1;  // fp8 scale tile of this wave's value dims
-
-  // QK partial of the tile in slot cb -> sh.sp
-  auto qk = [&](const uint8_t* cb) {
-    const uint8_t* krow = cb + (16 * kb + c) * kDsmlaRowBytes;
-    const u32x4 k0 = *reinterpret_cast<const u32x4*>(krow + 128 * qd + 32 * g);
-    const u32x4 k1 = *reinterpret_cast<const u32x4*>(krow + 128 * qd + 32 * g + 16);
-    const f16x4 kr = *reinterpret_cast<const f16x4*>(krow + 528 + 2 * (16 * qd + 4 * g));
-    float ksc[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-      ksc[r] = *reinterpret_cast<const float*>(cb + (16 * kb + 4 * g + r) * kDsmlaRowBytes + 512 +
-                                               4 * qd);
-    f32x4 accn[4], accr[4];
-#pragma unroll
-    for (int hg = 0; hg < 4; hg++) {
-      accn[hg] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      accr[hg] = mfma16x16x16(kr, qr[hg], (f32x4){0.f, 0.f, 0.f, 0.f});
-    }
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-      const uint32_t d0 = s < 2 ? k0[2 * s] : k1[2 * (s - 2)];
-      const uint32_t d1 = s < 2 ? k0[2 * s + 1] : k1[2 * (s - 2) + 1];
-      const f16x4 a0 = e4m3x4_to_f16x4(d0), a1 = e4m3x4_to_f16x4(d1);
-      const f16x8 kf = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-#pragma unroll
-      for (int hg = 0; hg < 4; hg++) accn[hg] = mfma16x16x32(kf, qn[hg][s], accn[hg]);
-    }
-#pragma unroll
-    for (int hg = 0; hg < 4; hg++) {
-      f32x4 v;
-#pragma unroll
-      for (int r = 0; r < 4; r++) v[r] = accr[hg][r] + ksc[r] * accn[hg][r];
-      *reinterpret_cast<f32x4*>(&sh.sp[qd][sp_at(16 * hg + c, 16 * kb + 4 * g)]) = v;
-    }
-  };
-
-  // softmax of the tile in slot cb (rows trows) from sh.sp -> sh.pt, alpha
-  auto softmax = [&](const uint8_t* cb, const int32_t* trows, int* flag) {
-    f32x4 s4 = *reinterpret_cast<const f32x4*>(&sh.sp[0][sp_at(sm_h, 4 * sm_k)]);
-#pragma unroll
-    for (int q = 1; q < 4; q++)
-      s4 += *reinterpret_cast<const f32x4*>(&sh.sp[q][sp_at(sm_h, 4 * sm_k)]);
-    const int4 vr = *reinterpret_cast<const int4*>(trows + 4 * sm_k);
-    f32x4 ks[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-      ks[r] = *reinterpret_cast<const f32x4*>(cb + (4 * sm_k + r) * kDsmlaRowBytes + 512);
-    const int vv[4] = {vr.x, vr.y, vr.z, vr.w};
-    float mt = -1e30f;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      s4[r] = vv[r] != -1 ? s4[r] : -INFINITY;  // -2: zero row, a valid key
-      mt = fmaxf(mt, s4[r]);
-    }
-    mt = max8(mt);
-    float alpha = 1.f;
-    if (mt > m_run + kPfLazyMax) {
-      const float m_new = fmaxf(m_run, mt);
-      alpha = __expf(m_run - m_new);
-      l_run *= alpha;
-      m_run = m_new;
-      *flag = 1;
-    }
-    if (sm_k == 0) reinterpret_cast<float*>(&sh.alpha[sm_h & 15])[sm_h >> 4] = alpha;
-    f32x4 pr;
-    float ls = 0.f;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      pr[r] = (s4[r] > -INFINITY) ? __expf(s4[r] - m_run) : 0.f;
-      ls += pr[r];
-    }
-    l_run += sum8(ls);
-#pragma unroll
-    for (int st = 0; st < 4; st++) {
-      f16x4 ph;
-#pragma unroll
-      for (int r = 0; r < 4; r++) ph[r] = (f16)(pr[r] * ks[r][st]);
-      *reinterpret_cast<f16x4*>(&sh.pt[st][pt_at(sm_h, 4 * sm_k)]) = ph;
-    }
-  };
-
-  // PV of the tile in slot cb with sh.pt (after applying sh.alpha)
-  auto pv = [&](const uint8_t* cb, bool rescale) {
-    if (rescale) {
-      const f32x4 al = sh.alpha[c];
-#pragma unroll
-      for (int t = 0; t < 4; t++)
-#pragma unroll
-        for (int hg = 0; hg < 4; hg++) oacc[t][hg] *= al[hg];
-    }
-    f16x8 pb[4];
-#pragma unroll
-    for (int hg = 0; hg < 4; hg++)
-      pb[hg] = *reinterpret_cast<const f16x8*>(&sh.pt[st_pv][pt_at(16 * hg + c, 8 * g)]);
-    // transpose source: lane i of a 16-lane group points at key 8g + i/2,
-    // bytes 64 w + 16 t + 8 (i % 2); lane j receives keys 8g .. 8g+7 at
-    // dim 64 w + 16 t + j
-    const uint8_t* vsrc = cb + (8 * g + (c >> 1)) * kDsmlaRowBytes + 64 * w + 8 * (c & 1);
-    s32x2 vt[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-      vt[t] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_s32x2*)(vsrc + 16 * t));
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const f16x4 lo = e4m3x4_to_f16x4((uint32_t)vt[t][0]);
-      const f16x4 hi = e4m3x4_to_f16x4((uint32_t)vt[t][1]);
-      const f16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-      for (int hg = 0; hg < 4; hg++) oacc[t][hg] = mfma16x16x32(av, pb[hg], oacc[t][hg]);
-    }
-  };
-
-  for (int seg_lo = k_lo; seg_lo < k_hi; seg_lo += kSegKeys) {
-    const int nkeys = min(k_hi - seg_lo, kSegKeys);
-    const int ntiles = (nkeys + kPfTileKeys - 1) / kPfTileKeys;
-    lds_barrier();  // previous segment done with rows and the ring
-    // ---- resolve idx -> block table -> row for the segment, batched ----
-    for (int base = 0; base < ntiles * kPfTileKeys; base += kPfThreads * kResU) {
-      int pos[kResU], pg[kResU], blk[kResU];
-#pragma unroll
-      for (int u = 0; u < kResU; u++) {
-        const int j = base + u * kPfThreads + (int)threadIdx.x;
-        pos[u] = (j < nkeys) ? p.idx[(int64_t)b * p.topk + seg_lo + j] : -1;
-      }
-      resolve_bt<kPfThreads>(p, b, seq_len, pos, pg, blk);
-#pragma unroll
-      for (int u = 0; u < kResU; u++) {
-        const int j = base + u * kPfThreads + (int)threadIdx.x;
-        if (j < ntiles * kPfTileKeys) {
-          const int64_t row = (int64_t)blk[u] * p.page_size + (pos[u] - pg[u] * p.page_size);
-          const bool in_range = pos[u] >= 0 && pos[u] < seq_len && pg[u] < p.max_blocks;
-          sh.rows[j] = (blk[u] < 0 || row >= p.n_kv_rows)
-                           ? ((in_range && p.zero_unresolved) ? -2 : -1) : (int32_t)row;
-        }
-      }
-    }
-    lds_barrier();
-    // prologue: tiles 0 and 1 in flight, QK + softmax of tile 0
-    pf_dma_tile(kv, sh.rows, sh.ring[0]);
-    if (ntiles > 1) pf_dma_tile(kv, sh.rows + kPfTileKeys, sh.ring[1]);
-    p3_wait(ntiles > 1 ? 1 : 0);
-    if (threadIdx.x == 0) sh.rescale[0] = 0;
-    lds_barrier();  // tile 0 landed
-    qk(sh.ring[0]);
-    lds_barrier();
-    softmax(sh.ring[0], sh.rows, &sh.rescale[0]);
-    if (ntiles > 2) pf_dma_tile(kv, sh.rows + 2 * kPfTileKeys, sh.ring[2]);
-    p3_wait(ntiles > 2 ? 1 : 0);  // tile 1 landed (this wave's part)
-    lds_barrier();
-
-    for (int i = 0; i < ntiles; i++) {
-      // ---- X: PV of tile i, QK of tile i + 1 ----
-      const bool rescale = sh.rescale[i & 1] != 0;
-      if (threadIdx.x == 0) sh.rescale[(i + 1) & 1] = 0;  // read by PV(i - 1), set by softmax(i + 1)
-      pv(sh.ring[i % kP3Ring], rescale);
-      if (i + 1 < ntiles) qk(sh.ring[(i + 1) % kP3Ring]);
-      lds_barrier();  // PV(i) read pt / alpha; sp of tile i+1 is complete
-      if (i + 1 < ntiles) {
-        // ---- Y: softmax of tile i + 1, DMA of tile i + 3 into tile i's slot ----
-        softmax(sh.ring[(i + 1) % kP3Ring], sh.rows + (i + 1) * kPfTileKeys,
-                &sh.rescale[(i + 1) & 1]);
-        if (i + 3 < ntiles) pf_dma_tile(kv, sh.rows + (i + 3) * kPfTileKeys, sh.ring[i % kP3Ring]);
-        p3_wait(i + 3 < ntiles ? 1 : 0);  // tile i + 2 landed (this wave's part)
-        lds_barrier();
-      }
-    }
-  }
-
-  // ---- outputs: o = O / l and lse, or the split's partial ----
-  const bool final_out = (p.n_splits == 1);
-  if (sm_k == 0) {
-    reinterpret_cast<float*>(&sh.lsum[sm_h & 15])[sm_h >> 4] = l_run;
-    const int h = hbase + sm_h;
-    if (h < p.n_head) {
-      const int64_t bh = (int64_t)b * p.n_head + h;
-      if (final_out) {
-        p.lse[bh] = (l_run > 0.f) ? (m_run + logf(l_run)) : p.empty_lse;
-      } else {
-        const int64_t ps = bh * p.n_splits + split;
-        p.part_ml[ps * 2 + 0] = m_run;
-        p.part_ml[ps * 2 + 1] = l_run;
-      }
-    }
-  }
-  lds_barrier();
-  const f32x4 L = sh.lsum[c];
-#pragma unroll
-  for (int hg = 0; hg < 4; hg++) {
-    const int h = hbase + 16 * hg + c;
-    if (h >= p.n_head) continue;
-    const int64_t bh = (int64_t)b * p.n_head + h;
-    const float inv = (L[hg] > 0.f) ? 1.f / L[hg] : 0.f;
-    if (final_out) {
-      f16* orow = p.o + bh * kValueDim + 64 * w;
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-        f16x4 v;
-#pragma unroll
-        for (int r = 0; r < 4; r++) v[r] = (f16)(oacc[t][hg][r] * inv);
-        *reinterpret_cast<f16x4*>(orow + 16 * t + 4 * g) = v;
-      }
-    } else {
-      f16x8 o8[2];
-#pragma unroll
-      for (int t = 0; t < 4; t++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) o8[t >> 1][4 * (t & 1) + r] = (f16)(oacc[t][hg][r] * inv);
-      u32x4* dst = reinterpret_cast<u32x4*>(p.part_o + (bh * p.n_splits + split) * kValueDim +
-                                            64 * w + 16 * g);
-      dst[0] = __builtin_bit_cast(u32x4, o8[0]);
-      dst[1] = __builtin_bit_cast(u32x4, o8[1]);
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
-// fp8_ds_mla 64-head attention with wave roles: the arithmetic of
-// sparse_mla_prefill_fp8_kernel (every S partial, softmax sum, P value and O
-// accumulation in the same order), laid out so that MFMA work and VALU work
-// run in different waves of each SIMD.
+// fp8_ds_mla 64-head attention (the prefill configuration, and decode batches
+// of >= 8 64-head units split over keys), laid out so that MFMA work and VALU
+// work run in different waves of each SIMD.  Every e4m3 byte of a tile is
+// converted to fp16 once per workgroup; products with the fp16 Q and P are
+// exact, and each tile scale multiplies in fp32 (QK) or into P (PV).
 //
 // Workgroup = one token x 64 heads (x one key split), 12 waves, three per
 // SIMD (<= 168 VGPRs each):
@@ -1591,7 +1255,7 @@ __device__ __forceinline__ void ws_pv_role(const MlaParams& p, const WsCtx& x, W
         *reinterpret_cast<f16x4*>(orow + 16 * t + 4 * g) = v;
       }
     } else {
-      // the partial layout of sparse_mla_prefill_fp8_kernel: per 64-dim chunk j,
+      // the split merge's partial layout (merge_dim): per 64-dim chunk j,
       // lane g's 16 values (dims 64 j + 16 t + 4 g + r, t < 4) at 64 j + 16 g
 #pragma unroll
       for (int j = 0; j < 2; j++) {
@@ -1769,12 +1433,13 @@ __global__ void __launch_bounds__(kWsThreads) sparse_mla_prefill_fp8_ws_kernel(M
 //     [32 hh, +32) over dims [288 dh, +288), Q of its 32 heads for those dims
 //     resident in registers.  The two dim halves meet in LDS and are summed
 //     in a fixed order.
-//   * softmax: as the fp8 kernel (thread t owns head t / 8 and keys
-//     4 (t % 8) .. +3, lazy running max, DPP reductions); P in fp16.
+//   * softmax: thread t owns head t / 8 and keys 4 (t % 8) .. +3, lazy
+//     running max, DPP reductions over the 8 threads of a head; P in fp16.
 //   * PV: wave w owns value dims [64 w, +64) for all 64 heads; V^T operands
 //     come from ds_read_b64_tr_b16 transpose reads (4 keys each).
-// Phases per tile as in the fp8 kernel: X = {PV(i), QK(i+1)}, then
-// Y = {softmax(i+1), LDS-DMA of tile i+3, wait for tile i+2}.
+// Two barrier-separated phases per tile: X = {PV(i), QK(i+1)} (independent
+// MFMA streams that hide each other's LDS latency), then Y = {softmax(i+1),
+// LDS-DMA of tile i+3, wait for tile i+2}.
 // Split s of a token covers keys [s kps, (s+1) kps) of its key list (the
 // top-k list, or positions [0, seq_len) in dense mode) and, with more than
 // one split, writes its normalised partial for the merge kernel.
@@ -2318,9 +1983,9 @@ static int launch_mla(const MlaParams& prm, dim3 grid, hipStream_t st) {
 using namespace mi355dsa;
 
 // Which kernel runs a sparse attention call, and over how many key splits:
-//  * kPipelined: the 64-head pipelined kernels (fp8: sparse_mla_prefill_fp8_
-//    kernel, fp16: mla_attn_f16_kernel), workgroup = (token, 64 heads, key
-//    split), tiles streamed through an LDS ring.  Taken from 256 64-head
+//  * kPipelined: the 64-head pipelined kernels (fp8:
+//    sparse_mla_prefill_fp8_ws_kernel, fp16: mla_attn_f16_kernel), workgroup
+//    = (token, 64 heads, key split), tiles streamed through an LDS ring.  Taken from 256 64-head
 //    workgroups up (one split), and for > 32 heads from kPipeMinUnits up
 //    with round(256 / units) splits of at least two 32-key tiles each;
 //  * kSplitDma: fp8 split decode with per-wave LDS-DMA gathers (16 heads per
