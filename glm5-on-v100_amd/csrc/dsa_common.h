@@ -199,6 +199,28 @@ __device__ __forceinline__ float max16(float v) {
 __device__ __forceinline__ float shfl_xor_f(float v, int m) {
   return __shfl_xor(v, m, 64);
 }
+// v + v of lane ^ 16, and v + v of lane ^ 32, as VALU lane swaps (gfx950
+// v_permlane16/32_swap) instead of LDS permutes.  Each swap hands lane l the
+// partner value in one of its two results and keeps its own in the other, so
+// the sum of the two results is the pair sum (bitwise: addition commutes).
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// max(d, 0) of an MFMA result in one instruction: such a value is never a
+// signalling NaN, so the quieting max the compiler puts before fmaxf is not
+// needed (a NaN gives 0, as d > 0 ? d : 0 does).
+__device__ __forceinline__ float relu_mfma(float d) {
+  float r;
+  asm("v_max_f32 %0, 0, %1" : "=v"(r) : "v"(d));
+  return r;
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));

@@ -283,11 +283,11 @@ __device__ __forceinline__ void indexer_logits_body(
       for (int r = 0; r < 4; r++) {
         float d = acc[r];
         if constexpr (KFP8) d *= f.scale;
-        v += (d > 0.f ? d : 0.f) * wv[t][r];
+        v += relu_mfma(d) * wv[t][r];
       }
     }
-    v += shfl_xor_f(v, 16);
-    v += shfl_xor_f(v, 32);
+    v = xor16_sum(v);
+    v = xor32_sum(v);
     return v;
   };
 
