@@ -346,6 +346,11 @@ __device__ __forceinline__ void dma16(const void* gptr, const void* lds) {
   const uint32_t off = (uint32_t)(uintptr_t)lds;
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(off) : "memory");
 }
+// global_load_lds_dword: lane l's 4 bytes at gptr land at lds + 4 l.
+__device__ __forceinline__ void dma4(const void* gptr, const void* lds) {
+  const uint32_t off = (uint32_t)(uintptr_t)lds;
+  asm volatile("global_load_lds_dword %0, off" ::"v"(gptr), "{m0}"(off) : "memory");
+}
 // dma16 of the 16 bytes at gptr + IMM (IMM in the instruction's offset
 // field, so that several loads share one address register).  The offset
 // field applies to the LDS address too, so M0 carries lds - IMM (the caller

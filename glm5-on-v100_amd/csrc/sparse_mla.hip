@@ -966,7 +966,8 @@ __device__ __forceinline__ float sum8(float v) {
 //   * waves 8-11, softmax: thread t owns head t / 4 and keys 8 (t % 4) .. +7
 //     of a tile; these waves also fetch each tile's scales and RoPE dims.
 // A tile slot holds, for its 32 keys: four NoPE blocks (one per dim quarter),
-// the four scales (16 B per key) and the RoPE dims.  The NoPE and RoPE blocks
+// the scales (tile-major: tile t of key r at 128 t + 4 r) and the RoPE dims.
+// The NoPE and RoPE blocks
 // are chunk-major: 16-B chunk j of key r at 512 j + 16 r, so the QK operand
 // reads and the PV transpose reads of 16 keys are contiguous (free of LDS
 // bank conflicts) and every DMA instruction fills 1 KB (two chunks of all 32
@@ -1020,14 +1021,19 @@ __device__ __forceinline__ void ws_dma_nope(const uint8_t* __restrict__ kv, cons
 }
 
 // The softmax wave sw's part: RoPE chunks 2 sw and 2 sw + 1 of the 32 keys
-// (one instruction), and for wave 0 the 16 scale bytes of every key (lanes
-// 0-31).  Per tile wave 0 issues 2 DMA instructions, waves 1-3 issue 1.
+// (one instruction), and for wave 0 the four scales of every key, tile-major
+// (scale of tile t of key r at 128 t + 4 r; two 4-byte instructions, lane l
+// taking tile l / 32 (then + 2) of key l % 32).  Per tile wave 0 issues 3 DMA
+// instructions, waves 1-3 issue 1.
 __device__ __forceinline__ void ws_dma_tail(const uint8_t* __restrict__ kv, const int32_t* trows,
                                             uint8_t* slot, int sw, int lane) {
   const int row = trows[lane & 31];
   const uint8_t* base = row >= 0 ? kv + (int64_t)row * kDsmlaRowBytes : kZeroRow;
   dma16(base + (kDsmlaRowBytes - 128) + 16 * (2 * sw + (lane >> 5)), slot + kWsRopeOff + 1024 * sw);
-  if (sw == 0 && lane < kPfTileKeys) dma16(base + 512, slot + kWsScaleOff);
+  if (sw == 0) {
+    dma4(base + 512 + 4 * (lane >> 5), slot + kWsScaleOff);
+    dma4(base + 520 + 4 * (lane >> 5), slot + kWsScaleOff + 256);
+  }
 }
 
 // vmcnt waits of the DMA waves: at most one tile's DMAs of this wave still in
@@ -1038,7 +1044,7 @@ __device__ __forceinline__ void ws_wait_pv(bool one) {
 }
 __device__ __forceinline__ void ws_wait_sm(bool one, int sw) {
   if (!one) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if (sw == 0) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+  else if (sw == 0) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
   else asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
 }
 
@@ -1119,10 +1125,8 @@ __device__ __forceinline__ void ws_qk_role(const MlaParams& p, const WsCtx& x, W
     const u32x4 k1 = *reinterpret_cast<const u32x4*>(krow + 512 * (2 * g + 1));
     const f16x4 kr = *reinterpret_cast<const f16x4*>(cb + kWsRopeOff + 512 * (2 * qd + (g >> 1)) +
                                                      16 * r + 8 * (g & 1));
-    float ksc[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      ksc[i] = *reinterpret_cast<const float*>(cb + kWsScaleOff + (16 * kb + 4 * g + i) * 16 + 4 * qd);
+    // tile qd's scales of keys 16 kb + 4 g .. +3
+    const f32x4 ksc = *reinterpret_cast<const f32x4*>(cb + kWsScaleOff + 128 * qd + 4 * (16 * kb + 4 * g));
     f32x4 accn[4], accr[4];
 #pragma unroll
     for (int hg = 0; hg < 4; hg++) {
@@ -1298,10 +1302,12 @@ __device__ __forceinline__ void ws_sm_role(const MlaParams& p, const WsCtx& x, W
         sq[q][hf] = *reinterpret_cast<const f32x4*>(&sh.sp[q][sp_at(hh, 8 * kq + 4 * hf)]);
     const int4 vr0 = *reinterpret_cast<const int4*>(trows + 8 * kq);
     const int4 vr1 = *reinterpret_cast<const int4*>(trows + 8 * kq + 4);
-    f32x4 ks[8];  // the four tile scales of each key
+    f32x4 ks[4][2];  // [scale tile][key half]: scales of keys 8 kq + 4 hf .. +3
 #pragma unroll
-    for (int k = 0; k < 8; k++)
-      ks[k] = *reinterpret_cast<const f32x4*>(cb + kWsScaleOff + (8 * kq + k) * 16);
+    for (int st = 0; st < 4; st++)
+#pragma unroll
+      for (int hf = 0; hf < 2; hf++)
+        ks[st][hf] = *reinterpret_cast<const f32x4*>(cb + kWsScaleOff + 128 * st + 4 * (8 * kq + 4 * hf));
     const int masked = sh.tmask[tile];
     __builtin_amdgcn_sched_barrier(0);
     f32x4 s4[2];
@@ -1353,7 +1359,7 @@ __device__ __forceinline__ void ws_sm_role(const MlaParams& p, const WsCtx& x, W
     for (int st = 0; st < 4; st++) {
       f16x8 ph;
 #pragma unroll
-      for (int k = 0; k < 8; k++) ph[k] = (f16)(pr[k] * ks[k][st]);
+      for (int k = 0; k < 8; k++) ph[k] = (f16)(pr[k] * ks[st][k >> 2][k & 3]);
       *reinterpret_cast<f16x8*>(&sh.pt[tile & 1][st][pt_at(hh, 8 * kq)]) = ph;
     }
   };
