@@ -1290,7 +1290,8 @@ __device__ __forceinline__ void ws_sm_role(const MlaParams& p, const WsCtx& x, W
   // lowest gives 25.0 ms on the 64k prefill against 27-29 ms otherwise)
   __builtin_amdgcn_s_setprio(2);
   // softmax of tile `tile` from sh.sp -> sh.pt[tile & 1], alpha.  Its LDS reads
-  // (S partials, row codes, key scales) are all issued before any is used.
+  // (S partials, key scales, the tile's flag) are all issued before any is
+  // used; the row codes are read only for a tile that holds a masked key.
   auto softmax = [&](int tile) {
     const uint8_t* cb = sh.ring[tile % kWsRing];
     const int32_t* trows = sh.rows + tile * kPfTileKeys;
@@ -1300,8 +1301,6 @@ __device__ __forceinline__ void ws_sm_role(const MlaParams& p, const WsCtx& x, W
 #pragma unroll
       for (int hf = 0; hf < 2; hf++)
         sq[q][hf] = *reinterpret_cast<const f32x4*>(&sh.sp[q][sp_at(hh, 8 * kq + 4 * hf)]);
-    const int4 vr0 = *reinterpret_cast<const int4*>(trows + 8 * kq);
-    const int4 vr1 = *reinterpret_cast<const int4*>(trows + 8 * kq + 4);
     f32x4 ks[4][2];  // [scale tile][key half]: scales of keys 8 kq + 4 hf .. +3
 #pragma unroll
     for (int st = 0; st < 4; st++)
@@ -1318,6 +1317,8 @@ __device__ __forceinline__ void ws_sm_role(const MlaParams& p, const WsCtx& x, W
       for (int q = 1; q < 4; q++) s4[hf] += sq[q][hf];
     }
     if (masked) {  // wave-uniform: most tiles hold no masked key
+      const int4 vr0 = *reinterpret_cast<const int4*>(trows + 8 * kq);
+      const int4 vr1 = *reinterpret_cast<const int4*>(trows + 8 * kq + 4);
       const int vv[8] = {vr0.x, vr0.y, vr0.z, vr0.w, vr1.x, vr1.y, vr1.z, vr1.w};
 #pragma unroll
       for (int k = 0; k < 8; k++)  // -2: zero row, a valid key
