@@ -222,6 +222,26 @@ def test_decode_pipelined_key_split(ops, dev, case):
     assert torch.all(o[B // 2] == 0) and torch.all(torch.isinf(lse[B // 2]))
 
 
+PREFILL_SEG = [
+    # seed, B, H, topk, seqs: the prefill configuration (B * ceil(H / 64) >= 256, one
+    # key split) with lists longer than one 2048-key segment, so one workgroup runs
+    # its tile pipeline twice (the second segment 5 and 2 tiles long)
+    (50, 256, 64, 2200, [2600 - 3 * i for i in range(256)]),
+    (51, 260, 32, 2100, [2500 - (i % 7) * 60 for i in range(260)]),  # 32 of 64 heads
+]
+
+
+@pytest.mark.parametrize("case", PREFILL_SEG, ids=[f"B{c[1]}H{c[2]}k{c[3]}" for c in PREFILL_SEG])
+def test_prefill_two_segments(ops, dev, case):
+    """fp8 prefill configuration with more than 2048 keys per token, ragged
+    lists and invalid entries, against the oracle."""
+    seed, B, H, topk, seqs = case
+    q, kv, idx, bt, seq = make(seed, B, H, 60, 64, True, topk, seqs, invalid_frac=0.03)
+    o, lse = run(ops, dev, q, kv, idx, bt, seq)
+    ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
+    check(o, lse, ro, rl)
+
+
 def test_prefill_equals_decode_config(ops, dev):
     """Split-count / configuration invariance: the first rows of a 256-token
     batch (prefill configuration) equal the same rows run alone (decode
