@@ -223,20 +223,26 @@ def test_decode_pipelined_key_split(ops, dev, case):
 
 
 PREFILL_SEG = [
-    # seed, B, H, topk, seqs: the prefill configuration (B * ceil(H / 64) >= 256, one
-    # key split) with lists longer than one 2048-key segment, so one workgroup runs
-    # its tile pipeline twice (the second segment 5 and 2 tiles long)
-    (50, 256, 64, 2200, [2600 - 3 * i for i in range(256)]),
-    (51, 260, 32, 2100, [2500 - (i % 7) * 60 for i in range(260)]),  # 32 of 64 heads
+    # seed, B, H, topk, page, seqs: the fp8 prefill configuration (B * ceil(H / 64) >=
+    # 256, one key split)
+    # lists longer than one 2048-key segment, so one workgroup runs its tile
+    # pipeline twice (the second segment 5 and 2 tiles long)
+    (50, 256, 64, 2200, 64, [2600 - 3 * i for i in range(256)]),
+    (51, 260, 32, 2100, 64, [2500 - (i % 7) * 60 for i in range(260)]),  # 32 of 64 heads
+    # short lists: two tiles, the second ragged; tokens with fewer keys than the list
+    (52, 256, 64, 40, 64, [1 + (i * 7) % 90 for i in range(256)]),
+    # two 64-head groups per token, a page size that is not a power of two
+    (53, 200, 128, 96, 48, [50 + (i * 13) % 700 for i in range(200)]),
 ]
 
 
 @pytest.mark.parametrize("case", PREFILL_SEG, ids=[f"B{c[1]}H{c[2]}k{c[3]}" for c in PREFILL_SEG])
 def test_prefill_two_segments(ops, dev, case):
-    """fp8 prefill configuration with more than 2048 keys per token, ragged
-    lists and invalid entries, against the oracle."""
-    seed, B, H, topk, seqs = case
-    q, kv, idx, bt, seq = make(seed, B, H, 60, 64, True, topk, seqs, invalid_frac=0.03)
+    """fp8 prefill configuration, against the oracle: more than 2048 keys per
+    token, short ragged lists, two head groups, ragged pages, invalid
+    entries."""
+    seed, B, H, topk, page, seqs = case
+    q, kv, idx, bt, seq = make(seed, B, H, 60, page, True, topk, seqs, invalid_frac=0.03)
     o, lse = run(ops, dev, q, kv, idx, bt, seq)
     ro, rl = O.sparse_mla(q, kv, idx, bt, seq, SCALE)
     check(o, lse, ro, rl)
