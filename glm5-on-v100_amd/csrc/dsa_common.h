@@ -362,5 +362,13 @@ __device__ __forceinline__ void dma16_at(const void* gptr, const void* lds) {
   asm volatile("global_load_lds_dwordx4 %0, off offset:%2" ::"v"(gptr), "{m0}"(off), "n"(IMM)
                : "memory");
 }
+// dma4 of the 4 bytes at gptr + IMM, landing at lds + 4 l (M0 = lds - IMM).
+template <int IMM>
+__device__ __forceinline__ void dma4_at(const void* gptr, const void* lds) {
+  static_assert(IMM >= 0 && IMM < 4096, "offset field");
+  const uint32_t off = (uint32_t)(uintptr_t)lds - (uint32_t)IMM;
+  asm volatile("global_load_lds_dword %0, off offset:%2" ::"v"(gptr), "{m0}"(off), "n"(IMM)
+               : "memory");
+}
 
 }  // namespace mi355dsa

@@ -294,6 +294,7 @@ extern "C" int mi355_dsa_decode_layer_indexer(
   d.page_shift = ilog2_pow2(idx_page_size);
   d.max_kv = max_kv;
   d.hist8 = aligned_to(hist, 8) ? 1 : 0;
+  d.span = idx_span_launch(idx_fp8, B, max_kv);
   a.nk.ik = reinterpret_cast<const u32x4*>(idx_k);
   a.nk.slot = idx_slot;
   a.nk.T = T;

@@ -42,9 +42,9 @@ __global__ void __launch_bounds__(kIdxWaves * 64) indexer_logits_kernel(
     const f16* __restrict__ Q, const void* __restrict__ Kv, const f16* __restrict__ W,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens,
     float* __restrict__ score, uint32_t* __restrict__ hist, int64_t n_kv_rows, int max_blocks,
-    int page_shift, int max_kv, int hist8) {
+    int page_shift, int max_kv, int hist8, int span) {
   const IdxDecArgs a{Q, Kv, W, block_table, seq_lens, score, hist, n_kv_rows, max_blocks,
-                     page_shift, max_kv, hist8};
+                     page_shift, max_kv, hist8, span};
   const IdxNewKeys none{};
   indexer_logits_block<KFP8, false>(a, blockIdx.x, blockIdx.y, none);
 }
@@ -567,14 +567,15 @@ extern "C" int mi355_dsa_indexer_logits(
   a.page_shift = shift;
   a.max_kv = max_kv;
   a.hist8 = hist8;
+  a.span = idx_span_launch(k_fp8, B, max_kv);
   if (k_fp8)
     indexer_logits_kernel<true><<<grid, kIdxWaves * 64, 0, st>>>(
         a.Q, a.Kv, a.W, a.block_table, a.seq_lens, a.score, a.hist, a.n_kv_rows, a.max_blocks,
-        a.page_shift, a.max_kv, a.hist8);
+        a.page_shift, a.max_kv, a.hist8, a.span);
   else
     indexer_logits_kernel<false><<<grid, kIdxWaves * 64, 0, st>>>(
         a.Q, a.Kv, a.W, a.block_table, a.seq_lens, a.score, a.hist, a.n_kv_rows, a.max_blocks,
-        a.page_shift, a.max_kv, a.hist8);
+        a.page_shift, a.max_kv, a.hist8, a.span);
   DSA_LAUNCH_CHECK("indexer_logits");
   return MI355_DSA_OK;
 }

@@ -17,17 +17,24 @@ constexpr int kIdxWaves = 4;
 constexpr int kIdxPPB = 1024;             // positions per workgroup
 constexpr int kIdxBlocksPerWave = kIdxPPB / 16 / kIdxWaves;  // 16
 constexpr int kIdxGroup = 2;              // 16-key blocks per pipeline stage
+// LDS slot of one staged fp8 block: 16 rows x 132 bytes, then the padding
+// that the last DMA's lanes 16-63 fill
+constexpr int kIdxSpanSlot = 2048 + 256;
 
 // Key-row fragment of one 16-key block for one lane (key c, group g).
 // fp16 rows: dims 32s + 8g .. +8 for steps s = 0..3, four 16-byte loads of
 // which load s of the four lanes of a key covers 64 contiguous bytes of its
 // row (one half cache line per key and instruction).  fp8 rows: dims
-// [16g, 16g+16) and [64 + 16g, 64 + 16g + 16), two 16-byte loads of which
-// each covers 64 contiguous bytes of the row across the four lanes of a key.
+// [o_g, o_g + 16) and [o_g + 32, o_g + 48) with o_g = idx_fp8_piece(g)
+// (0, 64, 16, 80): lanes g and g ^ 1 read 64 bytes apart, which keeps the
+// LDS reads of the staged 132-byte rows (lanes c, g of a half wave) on
+// distinct banks.
 struct KeyFrag {
   u32x4 v[4];
   float scale;  // fp8: row scale; fp16: 1
 };
+
+__device__ __forceinline__ int idx_fp8_piece(int g) { return 64 * (g & 1) + 16 * (g >> 1); }
 
 template <bool KFP8>
 __device__ __forceinline__ void load_key_frag(KeyFrag& f, const void* kv,
@@ -40,11 +47,11 @@ __device__ __forceinline__ void load_key_frag(KeyFrag& f, const void* kv,
   }
   const int g = (threadIdx.x & 63) >> 4;
   if constexpr (KFP8) {
-    const uint8_t* rp =
-        reinterpret_cast<const uint8_t*>(kv) + row * (int64_t)kIdxkFp8RowBytes;
-    f.v[0] = *reinterpret_cast<const u32x4_a4*>(rp + 16 * g);
-    f.v[1] = *reinterpret_cast<const u32x4_a4*>(rp + 64 + 16 * g);
-    f.scale = *reinterpret_cast<const float*>(rp + 128);
+    const uint8_t* rp = reinterpret_cast<const uint8_t*>(kv) +
+                        row * (int64_t)kIdxkFp8RowBytes + idx_fp8_piece(g);
+    f.v[0] = *reinterpret_cast<const u32x4_a4*>(rp);
+    f.v[1] = *reinterpret_cast<const u32x4_a4*>(rp + 32);
+    f.scale = *reinterpret_cast<const float*>(rp - idx_fp8_piece(g) + 128);
   } else {
     const u32x4* p = reinterpret_cast<const u32x4*>(
         reinterpret_cast<const f16*>(kv) + row * kIdxHeadDim + 8 * g);
@@ -66,8 +73,8 @@ __device__ __forceinline__ void load_key_frag_nb(KeyFrag& f, const void* kv, int
   const int64_t r = row < 0 ? 0 : row;
   if constexpr (KFP8) {
     const uint8_t* rp = reinterpret_cast<const uint8_t*>(kv) + r * (int64_t)kIdxkFp8RowBytes;
-    f.v[0] = *reinterpret_cast<const u32x4_a4*>(rp + 16 * g);
-    f.v[1] = *reinterpret_cast<const u32x4_a4*>(rp + 64 + 16 * g);
+    f.v[0] = *reinterpret_cast<const u32x4_a4*>(rp + idx_fp8_piece(g));
+    f.v[1] = *reinterpret_cast<const u32x4_a4*>(rp + idx_fp8_piece(g) + 32);
     f.scale = *reinterpret_cast<const float*>(rp + 128);
   } else {
     const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const f16*>(kv) +
@@ -79,7 +86,7 @@ __device__ __forceinline__ void load_key_frag_nb(KeyFrag& f, const void* kv, int
 }
 
 // B operand for step s from a key fragment (dims 32s + 8g .. +8 for fp16
-// rows, 64 (s >> 1) + 16g + 8 (s & 1) .. +8 for fp8 rows).
+// rows, idx_fp8_piece(g) + 32 (s >> 1) + 8 (s & 1) .. +8 for fp8 rows).
 template <bool KFP8>
 __device__ __forceinline__ f16x8 key_operand(const KeyFrag& f, int s) {
   if constexpr (KFP8) {
@@ -106,7 +113,17 @@ struct IdxDecArgs {
   int page_shift;
   int max_kv;
   int hist8;  // hist is 8-byte aligned: two bins per 64-bit atomic
+  int span;   // fp8 keys: stage 16-key spans through LDS where the cache allows
 };
+
+// The launch's workgroups per CU above which the fp8 span path pays: with
+// two or more resident per CU the staged spans (fewer, whole-line requests)
+// raise the streaming rate; a launch of one workgroup per CU is bound by each
+// wave's load-to-use latency, which the LDS staging lengthens.
+constexpr int kIdxSpanMinWorkgroups = 512;
+__host__ __device__ inline int idx_span_launch(int k_fp8, int B, int max_kv) {
+  return k_fp8 && (int64_t)B * ((max_kv + kIdxPPB - 1) / kIdxPPB) >= kIdxSpanMinWorkgroups;
+}
 
 // The step's new index keys, for a launch that also writes them to the
 // cache (the fused decode-layer launch): fp16 rows [T, 128] and their slots.
@@ -147,7 +164,7 @@ __device__ __forceinline__ void indexer_logits_body(
     const f16* __restrict__ Q, const void* Kv, const f16* __restrict__ W,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens,
     float* __restrict__ score, uint32_t* __restrict__ hist, int64_t n_kv_rows, int max_blocks,
-    int page_shift, int max_kv, int hist8, int tile, int b, const IdxNewKeys& nk) {
+    int page_shift, int max_kv, int hist8, int span, int tile, int b, const IdxNewKeys& nk) {
   const int p_lo = tile * kIdxPPB;
   const int p_hi = min(p_lo + kIdxPPB, max_kv);
   // The block-table entries of the tile's pages are loaded beside seq_len
@@ -174,7 +191,11 @@ __device__ __forceinline__ void indexer_logits_body(
   }
 
   __shared__ int32_t s_bt[kIdxPPB + 2];
-  __shared__ uint32_t s_hist[kTopkBins];
+  // level-1 counts of this workgroup's keys, two 16-bit bins per word (a
+  // workgroup counts at most 1024 keys)
+  __shared__ uint32_t s_hist[kTopkBins / 2];
+  // fp8 span path: per wave, two stages of kIdxGroup staged blocks
+  __shared__ __align__(16) uint8_t s_span[KFP8 ? kIdxWaves * 2 * kIdxGroup * kIdxSpanSlot : 16];
   __shared__ int32_t s_new[NEWK ? 2 * kIdxMaxNew : 1];  // slots, then "this workgroup reads it"
   const int page = 1 << page_shift;
 #pragma unroll
@@ -183,7 +204,7 @@ __device__ __forceinline__ void indexer_logits_body(
     if (i < npg) s_bt[i] = btv[k];
   }
   if (hist != nullptr)
-    for (int i = threadIdx.x; i < kTopkBins; i += blockDim.x) s_hist[i] = 0u;
+    for (int i = threadIdx.x; i < kTopkBins / 2; i += blockDim.x) s_hist[i] = 0u;
   if constexpr (NEWK) {
     for (int i = threadIdx.x; i < nk.T; i += blockDim.x) {
       s_new[i] = nk.slot[i];
@@ -236,8 +257,8 @@ __device__ __forceinline__ void indexer_logits_body(
 
   // A operands: q rows (heads c and 16 + c), with the keys' k-slot mapping:
   // step s, group g, slot e -> dim 32s + 8g + e (fp16 keys) or
-  // 64 (s >> 1) + 16g + 8 (s & 1) + e (fp8 keys, whose two 16-byte loads per
-  // lane are [16g, +16) and [64 + 16g, +16)).
+  // idx_fp8_piece(g) + 32 (s >> 1) + 8 (s & 1) + e (fp8 keys, whose two
+  // 16-byte pieces per lane start at idx_fp8_piece(g) and 32 bytes later).
   f16x8 qa[2][4];
   const f16* qb = Q + (int64_t)b * kIdxHeads * kIdxHeadDim;
 #pragma unroll
@@ -246,7 +267,7 @@ __device__ __forceinline__ void indexer_logits_body(
     for (int s = 0; s < 4; s++)
       qa[t][s] = *reinterpret_cast<const f16x8*>(
           qb + (16 * t + c) * kIdxHeadDim +
-          (KFP8 ? 64 * (s >> 1) + 16 * g + 8 * (s & 1) : 32 * s + 8 * g));
+          (KFP8 ? idx_fp8_piece(g) + 32 * (s >> 1) + 8 * (s & 1) : 32 * s + 8 * g));
   // head weights of this lane's D rows: heads 4g + r and 16 + 4g + r
   float wv[2][4];
 #pragma unroll
@@ -266,6 +287,7 @@ __device__ __forceinline__ void indexer_logits_body(
 
   KeyFrag cur[kIdxGroup], nxt[kIdxGroup];
   constexpr int n_groups = kIdxBlocksPerWave / kIdxGroup;
+  static_assert(n_groups >= 2, "the span path's vmcnt waits assume two stages or more");
   // wave w owns blocks w, w+4, w+8, ... ; stage i covers its blocks
   // [i*kIdxGroup, (i+1)*kIdxGroup) in that order.
   auto blk_of = [&](int stage, int j) { return (stage * kIdxGroup + j) * kIdxWaves + wave; };
@@ -291,7 +313,84 @@ __device__ __forceinline__ void indexer_logits_body(
     return v;
   };
 
-  if (p_lo + kIdxPPB <= max_kv && n_kv_rows > 0) {
+  // one key into the level-1 count of bin key >> 20
+  auto hist_count = [&](uint32_t key) {
+    atomicAdd(&s_hist[key >> 21], 1u << ((key >> 16) & 16));
+  };
+
+  // fp8 rows, in a launch that asks for it (idx_span_launch), in pages of
+  // >= 16 rows that the cache holds whole (its row count
+  // a multiple of the page), 16-byte aligned: the 16 keys of a block are 16
+  // consecutive rows, one 2112-byte span.
+  const bool span_ok = KFP8 && span && page_shift >= 4 && n_kv_rows > 0 &&
+                       (n_kv_rows & (page - 1)) == 0 &&
+                       ((uintptr_t)Kv & 15) == 0;
+  if (KFP8 && span_ok && p_lo + kIdxPPB <= max_kv) {
+    // Whole workgroup inside the row.  Each block's span goes to LDS by
+    // LDS-DMA in three instructions: bytes [0, 1024) and [1024, 2048), 16
+    // per lane, and [2048, 2112), 4 per lane from lanes 0-15 (lanes 16-63
+    // repeat them into the slot's padding).  A wave then reads its operands
+    // from the staged rows.  Two stages (2 x kIdxGroup slots) per wave: the
+    // next stage's spans are in flight while this one is scored.  A block of
+    // an unmapped page (table entry < 0 or past the cache) fetches rows 0-15
+    // instead and scores its keys as the zero key, 0.
+    uint8_t* ring = s_span + wave * (2 * kIdxGroup * kIdxSpanSlot);
+    const uint8_t* kb = reinterpret_cast<const uint8_t*>(Kv);
+    auto issue = [&](int st, bool (&ok)[kIdxGroup]) {
+#pragma unroll
+      for (int j = 0; j < kIdxGroup; j++) {
+        const int p0 = p_lo + 16 * blk_of(st, j);
+        // one page per block: its table entry is wave-uniform
+        const int32_t pb = __builtin_amdgcn_readfirstlane(s_bt[(p0 >> page_shift) - pg0]);
+        ok[j] = pb >= 0 && ((int64_t)pb << page_shift) < n_kv_rows;
+        const int64_t r0 = ok[j] ? ((int64_t)pb << page_shift) + (p0 & (page - 1)) : 0;
+        const uint8_t* src = kb + r0 * kIdxkFp8RowBytes;
+        uint8_t* slot = ring + ((st & 1) * kIdxGroup + j) * kIdxSpanSlot;
+        dma16_at<0>(src + 16 * lane, slot);
+        dma16_at<1024>(src + 16 * lane, slot + 1024);
+        dma4_at<2048>(src + 4 * (lane & 15), slot + 2048);
+      }
+    };
+    bool okc[kIdxGroup], okn[kIdxGroup];
+    issue(0, okc);
+#pragma unroll
+    for (int st = 0; st < n_groups; st++) {
+      if (st + 1 < n_groups) {
+        // this wave's reads of the slots about to be refilled (stage st - 1)
+        // are complete before their DMAs go out
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(st + 1, okn);
+      }
+      // stage st landed: after its 3 kIdxGroup DMAs come the previous
+      // stage's kIdxGroup score stores and the next stage's DMAs
+      if (st == 0)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * kIdxGroup) : "memory");
+      else if (st + 1 < n_groups)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kIdxGroup) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kIdxGroup) : "memory");
+#pragma unroll
+      for (int j = 0; j < kIdxGroup; j++) {
+        const uint8_t* rw = ring + ((st & 1) * kIdxGroup + j) * kIdxSpanSlot +
+                            kIdxkFp8RowBytes * c;
+        KeyFrag f;
+        f.v[0] = *reinterpret_cast<const u32x4_a4*>(rw + idx_fp8_piece(g));
+        f.v[1] = *reinterpret_cast<const u32x4_a4*>(rw + idx_fp8_piece(g) + 32);
+        f.v[2] = f.v[3] = (u32x4){0u, 0u, 0u, 0u};
+        f.scale = *reinterpret_cast<const float*>(rw + 128);
+        float v = block_score(f);
+        if (!okc[j]) v = 0.f;
+        const int p = p_lo + 16 * blk_of(st, j) + c;
+        const bool live = p < seq_len;
+        srow[p] = live ? v : -INFINITY;
+        if (hist != nullptr && g == 0 && live) hist_count(mono_key(v));
+      }
+      if (st + 1 < n_groups) {
+#pragma unroll
+        for (int j = 0; j < kIdxGroup; j++) okc[j] = okn[j];
+      }
+    }
+  } else if (p_lo + kIdxPPB <= max_kv && n_kv_rows > 0) {
     // Whole workgroup inside the row: no branch around any global load or
     // store.  Every lane stores its key's score (the four lanes of a key
     // write the same bits), so the waits before a stage's MFMAs count
@@ -325,7 +424,7 @@ __device__ __forceinline__ void indexer_logits_body(
         const int p = p_lo + 16 * blk_of(st, j) + c;
         const bool live = p < seq_len;
         srow[p] = live ? v : -INFINITY;
-        if (hist != nullptr && g == 0 && live) atomicAdd(&s_hist[mono_key(v) >> 20], 1u);
+        if (hist != nullptr && g == 0 && live) hist_count(mono_key(v));
       }
       if (st + 1 < n_groups) {
 #pragma unroll
@@ -356,7 +455,7 @@ __device__ __forceinline__ void indexer_logits_body(
           if (g == 0 && p < p_hi) {
             if (p < seq_len) {
               srow[p] = v;
-              if (hist != nullptr) atomicAdd(&s_hist[mono_key(v) >> 20], 1u);
+              if (hist != nullptr) hist_count(mono_key(v));
             } else {
               srow[p] = -INFINITY;
             }
@@ -381,13 +480,14 @@ __device__ __forceinline__ void indexer_logits_body(
       unsigned long long* hrow2 =
           reinterpret_cast<unsigned long long*>(hist + (int64_t)b * kTopkBins);
       for (int i = threadIdx.x; i < kTopkBins / 2; i += blockDim.x) {
-        const unsigned long long lo = s_hist[2 * i], hi = s_hist[2 * i + 1];
-        if (lo | hi) atomicAdd(hrow2 + i, lo | (hi << 32));
+        const uint32_t w2 = s_hist[i];
+        const unsigned long long lo = w2 & 0xffffu, hi = w2 >> 16;
+        if (w2) atomicAdd(hrow2 + i, lo | (hi << 32));
       }
     } else {  // a hist base that is not 8-byte aligned: one bin per atomic
       uint32_t* hrow = hist + (int64_t)b * kTopkBins;
       for (int i = threadIdx.x; i < kTopkBins; i += blockDim.x) {
-        const uint32_t n = s_hist[i];
+        const uint32_t n = (s_hist[i >> 1] >> (16 * (i & 1))) & 0xffffu;
         if (n) atomicAdd(&hrow[i], n);
       }
     }
@@ -399,7 +499,7 @@ __device__ __forceinline__ void indexer_logits_block(const IdxDecArgs& a, int ti
                                                      const IdxNewKeys& nk) {
   indexer_logits_body<KFP8, NEWK>(a.Q, a.Kv, a.W, a.block_table, a.seq_lens, a.score, a.hist,
                                   a.n_kv_rows, a.max_blocks, a.page_shift, a.max_kv, a.hist8,
-                                  tile, b, nk);
+                                  a.span, tile, b, nk);
 }
 
 }  // namespace mi355dsa

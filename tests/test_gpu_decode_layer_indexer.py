@@ -27,6 +27,8 @@ CASES = [
     (4, 2, False, False, [5000, 2600]),           # speculative rows read each other's keys
     (20, 1, True, True, [900 + 301 * r for r in range(20)]),  # short rows: select's early path
     (3, 1, False, True, [2000, 1500, 64]),        # max_kv = top-k: the whole-row kernel path
+    # 20 x 27 = 540 logits workgroups: fp8 index keys staged as 16-row spans
+    (20, 1, False, True, [26000 + 37 * r for r in range(20)]),
 ]
 
 
@@ -39,9 +41,13 @@ def _case(pkg, dev, case, seed):
     H, P = 16, 128
     mb = (max(lens) + PAGE - 1) // PAGE
     nblk = R * mb + 3
-    lat = torch.randn(nblk * PAGE, 576, generator=g) / 24.0
-    lat0 = (O.dsmla_rows(lat).view(nblk, PAGE, 656) if fp8
-            else lat.to(torch.float16).view(nblk, PAGE, 576)).to(dev)
+    if fp8:
+        lat = torch.randn(nblk * PAGE, 576, generator=g) / 24.0
+        lat0 = O.dsmla_rows(lat).view(nblk, PAGE, 656).to(dev)
+    else:  # drawn on the device: the large case's cache has 535k rows
+        gd = torch.Generator(device=dev).manual_seed(seed)
+        lat0 = (torch.randn(nblk * PAGE, 576, generator=gd, device=dev) / 24.0).to(
+            torch.float16).view(nblk, PAGE, 576)
     keys = torch.randn(nblk * PAGE, 128, generator=g).to(torch.float16).to(dev)
     if ik_fp8:  # a quantised cache, written row by row with the store op
         ik0 = torch.zeros(nblk, PAGE, 132, dtype=torch.uint8, device=dev)

@@ -40,6 +40,10 @@ CASES = [
     (3, 2, 40, 64, True, True, 2048, [2000, 2048]),
     (4, 2, 40, 64, True, False, 2560, [2560, 77]),
     (5, 9, 20, 64, False, False, 1280, [1280] * 9),   # B >= 8 (reference WMMA branch)
+    # fp8 rows in 16-row pages (the staged 16-key spans) and in 8-row pages
+    # (per-key loads)
+    (6, 2, 130, 16, True, False, 2048, [2048, 1500]),
+    (7, 2, 300, 8, True, False, 2400, [2400, 1999]),
 ]
 
 
@@ -110,6 +114,41 @@ def test_unmapped_pages_in_full_workgroups(ops, dev, fp8):
     for b in range(3):  # histogram == bincount of the kernel's own scores over p < seq_len
         ref = torch.bincount((O.mono_key(got[b, :int(seq[b])]) >> 20).long(), minlength=4096)
         assert torch.equal(hist[b].cpu().long(), ref)
+
+
+@pytest.mark.parametrize("page", [64, 16])
+def test_fp8_span_and_per_key_loads_agree(ops, dev, page):
+    """fp8 rows in a launch of >= 512 workgroups: workgroups inside the row
+    stage each 16-key block's 16 consecutive rows (2112 bytes) through LDS
+    when the cache is 16-byte aligned; a cache view 4 bytes into its buffer
+    takes the per-key loads (pinned against the oracle by the cases above).
+    Same scores and histogram bit for bit, unmapped pages included."""
+    B, max_kv = 4, 131072  # 4 x 128 workgroups
+    nblk = max_kv // page + 5
+    q, kc, w, bt, _ = make_case(13 + page, B, nblk, page, True, False, max_kv, [max_kv] * B)
+    bt[0, 5] = -1
+    bt[2, 100] = nblk + 7
+    seq = torch.tensor([131072, 131000, 70000, 1000], dtype=torch.int32)
+    buf = torch.zeros(kc.numel() + 16, dtype=torch.uint8, device=dev)
+    outs = []
+    for off in (0, 4):
+        kv = buf[off:off + kc.numel()].view(nblk, page, 132)
+        kv.copy_(kc.to(dev))
+        assert (kv.data_ptr() % 16 == 0) == (off == 0)
+        score = torch.empty(B, max_kv, device=dev)
+        hist = torch.zeros(B, 4096, dtype=torch.int32, device=dev)
+        ops.sm70_indexer_logits(score, q.to(dev), kv, w.to(dev), bt.to(dev), seq.to(dev), hist)
+        outs.append((score.cpu(), hist.cpu()))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+    got = outs[0][0]
+    assert torch.equal(got[0, 5 * page:6 * page], torch.zeros(page))
+    assert torch.equal(got[2, 100 * page:101 * page], torch.zeros(page))
+    for b in range(B):
+        L = int(seq[b])
+        assert torch.isfinite(got[b, :L]).all() and torch.isinf(got[b, L:]).all()
+        ref = torch.bincount((O.mono_key(got[b, :L]) >> 20).long(), minlength=4096)
+        assert torch.equal(outs[0][1][b].long(), ref)
 
 
 def test_duplicate_keys_score_identically(ops, dev):
