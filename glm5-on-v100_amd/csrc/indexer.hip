@@ -128,26 +128,35 @@ struct PkArgs {
 };
 
 // One workgroup tile of NW waves: queries [q_base, q_base + QT) x keys
-// [p_base, +256), QT = 16 QB NW / 4 (wave w: keys 64 (w & 3), query blocks
-// QB (w >> 2) .. +QB).
-template <bool KFP8, int QB, int NW, typename SM>
+// [p_base, +256).  HS = 1: QT = 16 QB NW / 4 (wave w: keys 64 (w & 3), query
+// blocks QB (w >> 2) .. +QB, all 32 heads).  HS = 2 (NW = 8, small launches):
+// QT = 16 QB, and wave w takes keys 64 (w & 3) of every query for heads
+// [16 (w >> 2), +16), so that each wave's head loop is half as long; ring
+// slot h then holds heads h and h + 16, and the two halves' relu * w sums
+// are added through LDS at the end (head sum = heads 0-15, then + heads
+// 16-31).
+template <bool KFP8, int QB, int NW, int HS, typename SM>
 __device__ __forceinline__ void pk_tile(const PkArgs& a, SM& sh, int q_base, int p_base) {
+  static_assert(HS == 1 || (HS == 2 && NW == 8), "head split: 8 waves");
   constexpr int NT = 64 * NW;
-  constexpr int QT = 16 * QB * (NW / 4);          // queries of the tile
-  constexpr int QROUNDS = QT * 256 / 16 / NT;     // LDS-DMA ops per thread per head
+  constexpr int QT = 16 * QB * (NW / 4 / HS);     // queries of the tile
+  constexpr int NHP = kIdxHeads / 2 / HS;         // head pairs per wave
+  constexpr int QROUNDS = HS * QT * 256 / 16 / NT;  // LDS-DMA ops per thread per ring slot
   constexpr int SLOT = sizeof(sh.q[0]) / sizeof(f16);
   // fp16 key rows (64 KB) are staged in ring slots KSLOT0 .. : slots 2..5 of
   // 16 KB slots (slots 0, 1 stay free for the first head pair), or the whole
   // ring of 8 KB slots
   constexpr int KSLOT0 = SLOT * 2 >= 16384 ? 2 : 0;
-  static_assert(QT * kIdxHeadDim <= SLOT, "ring slot too small for the tile");
+  static_assert(HS * QT * kIdxHeadDim <= SLOT, "ring slot too small for the tile");
   static_assert((kPkRing - KSLOT0) * SLOT * 2 >= kPkKT * kIdxHeadDim * 2, "keys do not fit the ring");
   const f16* __restrict__ Qp = a.Qp;
   const int B = a.B, max_kv = a.max_kv, page_shift = a.page_shift, max_blocks = a.max_blocks;
   const int n_qt = (B + 15) >> 4;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int half = wave >> 2;           // query-block group
+  const int half = HS == 1 ? wave >> 2 : 0;  // query-block group
+  const int hh = HS == 1 ? 0 : wave >> 2;    // head half (HS = 2)
+  const int hoff = (kIdxHeads / HS) * hh;    // its first head
   const int c = lane & 15, g = lane >> 4;
 
   // Q ring: head h of the tile's 2 QB query tiles [qt0, qt0 + 2 QB) is
@@ -163,10 +172,14 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, SM& sh, int q_base, int
   const bool qfull = qt0 + QT / 16 <= n_qt;
   auto issue_q_round = [&](int h, int u) {
     const int i = threadIdx.x + u * NT;  // LDS 16-byte unit
-    const int qt = qt0 + (i >> 8);               // 256 units per tile
-    const int st = (i >> 6) & 3, gg = (i >> 4) & 3, cc = i & 15;
+    // HS = 2: units [0, 16 QT) hold head h, [16 QT, 32 QT) head h + 16
+    const int hsel = HS == 1 ? 0 : i / (16 * QT);
+    const int ii = i - 16 * QT * hsel;
+    const int qt = qt0 + (ii >> 8);              // 256 units per tile
+    const int st = (ii >> 6) & 3, gg = (ii >> 4) & 3, cc = ii & 15;
     const int piece = (2 * st + (gg >> 1)) * 32 + cc * 2 + (gg & 1);
-    const int64_t src = ((int64_t)h * n_qt + ((qfull || qt < n_qt) ? qt : 0)) * 2048 + piece * 8;
+    const int hq = h + (kIdxHeads / HS) * hsel;
+    const int64_t src = ((int64_t)hq * n_qt + ((qfull || qt < n_qt) ? qt : 0)) * 2048 + piece * 8;
     dma16(Qp + src, &sh.q[h % kPkRing][(u * NT + 64 * wave) * 8]);
   };
   auto issue_q = [&](int h) {
@@ -322,7 +335,7 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, SM& sh, int q_base, int
     }
   // B operand: query column c of tile qb0 + qb, dims 32st + 8g .. +8, at LDS
   // unit (tile, st, lane)
-  const int boff = qb0 * 2048 + lane * 8;
+  const int boff = hh * (QT * kIdxHeadDim) + qb0 * 2048 + lane * 8;
   auto load_b = [&](const f16* qs, int st, f16x8 (&b)[QB]) {
 #pragma unroll
     for (int qb = 0; qb < QB; qb++)
@@ -331,7 +344,7 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, SM& sh, int q_base, int
   // load_w: the weights of head h for this lane's query columns
   auto load_w = [&](int h, float (&w2)[QB]) {
 #pragma unroll
-    for (int qb = 0; qb < QB; qb++) w2[qb] = sh.w[h][16 * (qb0 + qb) + c];
+    for (int qb = 0; qb < QB; qb++) w2[qb] = sh.w[hoff + h][16 * (qb0 + qb) + c];
   };
   // head h: MFMAs into acc, epilogue of head h - 1 (prev, weights wn); with
   // next_in_pair, its last step also reads head h + 1's first B operands and
@@ -382,7 +395,7 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, SM& sh, int q_base, int
   // that neither has a branch inside its MFMA sequence.
   auto pair = [&](int j, bool refill) {
     const int h0 = 2 * j;
-    pk_wait<QROUNDS>(min(kIdxHeads / 2 - 1 - j, kAhead - 1));
+    pk_wait<QROUNDS>(min(NHP - 1 - j, kAhead - 1));
     lds_barrier();  // pair j landed; every wave is done with pair j - 1
     f16x8 bn[QB];
     float wn[QB];
@@ -394,16 +407,40 @@ __device__ __forceinline__ void pk_tile(const PkArgs& a, SM& sh, int q_base, int
     head(h0 + 1, accB, accA, bn, wn, false, refill);
   };
 #pragma nounroll
-  for (int j = 0; j < kIdxHeads / 2 - kAhead; j++) pair(j, true);
+  for (int j = 0; j < NHP - kAhead; j++) pair(j, true);
 #pragma nounroll
-  for (int j = kIdxHeads / 2 - kAhead; j < kIdxHeads / 2; j++) pair(j, false);
+  for (int j = NHP - kAhead; j < NHP; j++) pair(j, false);
 #pragma unroll
   for (int qb = 0; qb < QB; qb++) {
-    const float wl = sh.w[kIdxHeads - 1][16 * (qb0 + qb) + c];
+    const float wl = sh.w[hoff + 2 * NHP - 1][16 * (qb0 + qb) + c];
 #pragma unroll
     for (int kb = 0; kb < 4; kb++)
 #pragma unroll
       for (int r = 0; r < 4; r++) sacc[kb][qb][r] += relu1(accB[kb][qb][r]) * wl;
+  }
+  if constexpr (HS == 2) {
+    // heads 16-31 of each key group meet heads 0-15 in LDS (the ring is free:
+    // the last pair waited for every DMA, and the barrier for every read)
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(&sh.q[0][0]);
+    const int kg = wave & 3;
+    static_assert(4 * 4 * QB * 256 * 4 <= sizeof(sh.q), "reduction buffer");
+    if (hh == 1) {
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+        for (int qb = 0; qb < QB; qb++)
+          *reinterpret_cast<f32x4*>(&red[((kg * 4 + kb) * QB + qb) * 256 + lane * 4]) =
+              sacc[kb][qb];
+    }
+    __syncthreads();
+    if (hh == 1) return;
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+      for (int qb = 0; qb < QB; qb++)
+        sacc[kb][qb] += *reinterpret_cast<const f32x4*>(
+            &red[((kg * 4 + kb) * QB + qb) * 256 + lane * 4]);
   }
 
   // D layout: lane (query col c, key rows 4g+r) -> 4 consecutive keys.
@@ -439,13 +476,13 @@ __global__ void __launch_bounds__(kPkThreads) indexer_logits_packed_kernel(PkArg
   __shared__ PkSmem sh;
   const int id = blockIdx.x;
   if (id < a.n_full) {
-    pk_tile<KFP8, 2, kPkWaves>(a, sh, (id / a.n_kt) * kPkMaxQT, (id % a.n_kt) * kPkKT);
+    pk_tile<KFP8, 2, kPkWaves, 1>(a, sh, (id / a.n_kt) * kPkMaxQT, (id % a.n_kt) * kPkKT);
   } else {
     const int j = id - a.n_full;
     const int t = a.n_full + (j >> 1);
     const int q_base = (t / a.n_kt) * kPkMaxQT + 32 * (j & 1);
     if (q_base >= a.B) return;  // a half tile past the last query (no DMA issued yet)
-    pk_tile<KFP8, 1, kPkWaves>(a, sh, q_base, (t % a.n_kt) * kPkKT);
+    pk_tile<KFP8, 1, kPkWaves, 1>(a, sh, q_base, (t % a.n_kt) * kPkKT);
   }
 }
 
@@ -467,7 +504,7 @@ __global__ void __launch_bounds__(kPkhWaves * 64, 2) indexer_logits_packed_h_ker
   const int id = blockIdx.x;
   const int q_base = (id / a.n_kt) * kPkhQT;
   if (q_base >= a.B) return;
-  pk_tile<KFP8, 2, kPkhWaves>(a, sh, q_base, (id % a.n_kt) * kPkKT);
+  pk_tile<KFP8, 2, kPkhWaves, 1>(a, sh, q_base, (id % a.n_kt) * kPkKT);
 }
 
 // Launches of more than one round of four-wave workgroups whose last round
@@ -483,32 +520,36 @@ __global__ void __launch_bounds__(kPkhWaves * 64, 2) indexer_logits_packed_hq_ke
   if (id < a.n_full) {
     const int q_base = (id / a.n_kt) * kPkhQT;
     if (q_base >= a.B) return;
-    pk_tile<KFP8, 2, kPkhWaves>(a, sh, q_base, (id % a.n_kt) * kPkKT);
+    pk_tile<KFP8, 2, kPkhWaves, 1>(a, sh, q_base, (id % a.n_kt) * kPkKT);
   } else {
     const int j = id - a.n_full;
     const int hq = a.n_full + (j >> 1);  // the 32-query workgroup this quarter is half of
     const int q_base = (hq / a.n_kt) * kPkhQT + 16 * (j & 1);
     if (q_base >= a.B) return;
-    pk_tile<KFP8, 1, kPkhWaves>(a, sh, q_base, (hq % a.n_kt) * kPkKT);
+    pk_tile<KFP8, 1, kPkhWaves, 1>(a, sh, q_base, (hq % a.n_kt) * kPkKT);
   }
 }
 
-// Quarter tiles: four-wave workgroups over 16 queries x 256 keys (each
-// wave: 64 keys x one 16-query block), with the four-wave kernel's LDS.  A
-// launch of at most kPkqMaxTiles full tiles runs as quarters, one per CU:
-// 11.7-12.8 us per launch against 15.6-16.4 for halves (128-row sub-chunks
-// of a causal prefill).  Larger launches gain nothing from them: two
-// quarters sharing a CU take as long as one half tile alone.
+// Quarter tiles for launches of at most kPkqMaxTiles full tiles (one piece
+// per CU): 8 waves over 16 queries x 256 keys, the 32 heads split over two
+// wave groups (each wave: 64 keys x the 16 queries x 16 heads), so that two
+// waves per SIMD share the piece's MFMAs and hide each other's epilogue and
+// barrier waits.  Per launch (128-row sub-chunks of a causal prefill):
+// 10.4-11.8 us, against 11.7-12.8 us for four-wave quarters with all 32
+// heads per wave and 15.6-16.4 us for half tiles.  Larger launches gain
+// nothing from quarters: two sharing a CU take as long as one half tile
+// alone; and the head split over 32-query pieces (65-128 tiles) measured
+// level with the 8-wave half tiles, which already run two waves per SIMD.
 constexpr int kPkqQT = 16;
 constexpr int64_t kPkqMaxTiles = kPkCUs / 4;
 
 template <bool KFP8>
-__global__ void __launch_bounds__(kPkhWaves * 64, 2) indexer_logits_packed_q_kernel(PkArgs a) {
-  __shared__ PkSmemH sh;
+__global__ void __launch_bounds__(kPkThreads) indexer_logits_packed_qs_kernel(PkArgs a) {
+  __shared__ PkSmemT<2 * kPkqQT> sh;  // ring slots of two heads
   const int id = blockIdx.x;
   const int q_base = (id / a.n_kt) * kPkqQT;
   if (q_base >= a.B) return;
-  pk_tile<KFP8, 1, kPkhWaves>(a, sh, q_base, (id % a.n_kt) * kPkKT);
+  pk_tile<KFP8, 1, kPkWaves, 2>(a, sh, q_base, (id % a.n_kt) * kPkKT);
 }
 
 // Tiles of a launch with W full tiles that run as two half tiles: all of
@@ -616,12 +657,12 @@ extern "C" int mi355_dsa_indexer_logits_packed(
   a.n_full = (int)(W - split);
   hipStream_t st = as_stream(stream);
   if (W <= kPkqMaxTiles) {
-    // small launches: quarter tiles, up to one per CU
+    // small launches: 16-query head-split pieces, up to one per CU
     const int64_t gq = n_kt * ((B + kPkqQT - 1) / kPkqQT);
     if (k_fp8)
-      indexer_logits_packed_q_kernel<true><<<dim3((unsigned)gq), kPkhWaves * 64, 0, st>>>(a);
+      indexer_logits_packed_qs_kernel<true><<<dim3((unsigned)gq), kPkThreads, 0, st>>>(a);
     else
-      indexer_logits_packed_q_kernel<false><<<dim3((unsigned)gq), kPkhWaves * 64, 0, st>>>(a);
+      indexer_logits_packed_qs_kernel<false><<<dim3((unsigned)gq), kPkThreads, 0, st>>>(a);
   } else if (W >= kPkhMinTiles) {
     // large launches: four-wave 32-query workgroups, two per CU; a last
     // round of at most half a round runs as quarter tiles

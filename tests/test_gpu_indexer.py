@@ -231,8 +231,9 @@ def test_packed_matches_decode_kernel_on_dyadic(ops, dev):
 # (W = 260, 280 with a partial last query tile, and fp8 keys), which takes
 # the four-wave 32-query kernel, its last round as 16-query quarter tiles when
 # that round holds at most 256 of its workgroups (W = 260, 280, 384; W = 400
-# keeps a full last round); launches of at most 64 tiles as quarter tiles,
-# and of 65-128 tiles as half tiles.
+# keeps a full last round); launches of at most 64 tiles as 16-query pieces
+# with the 32 heads split over two wave groups, and of 65-128 tiles as half
+# tiles.
 SPLIT = [
     # seed, B, max_kv, fp8
     (31, 128, 256 * 100, False),
@@ -243,12 +244,14 @@ SPLIT = [
     (35, 128, 256 * 200, False),
     (36, 100, 256 * 200, True),      # a partial 32-query tile
     (37, 1000, 256 * 24, False),
-    # <= 64 full tiles: quarter tiles (16 queries), one per CU
+    # <= 64 full tiles: head-split 16-query pieces, one per CU
     (38, 128, 256 * 30, False),
     (39, 37, 256 * 20, False),       # a partial 16-query tile
     (40, 64, 256 * 50, True),
+    (43, 20, 256 * 3, False),        # two pieces per key tile, the second partial
     # 65-128 full tiles: every tile as two halves
     (41, 128, 256 * 50, False),
+    (42, 96, 256 * 40, True),        # fp8 keys, a partial query tile
 ]
 
 
