@@ -233,6 +233,10 @@ PREFILL_SEG = [
     (52, 256, 64, 40, 64, [1 + (i * 7) % 90 for i in range(256)]),
     # two 64-head groups per token, a page size that is not a power of two
     (53, 200, 128, 96, 48, [50 + (i * 13) % 700 for i in range(200)]),
+    # workgroups of 4-5 consecutive tokens (one tile stream across them)
+    (54, 1100, 64, 96, 64, [30 + (i * 37) % 900 for i in range(1100)]),
+    # one tile per token: every tile starts and ends a token
+    (55, 700, 64, 20, 16, [1 + (i * 11) % 300 for i in range(700)]),
 ]
 
 
